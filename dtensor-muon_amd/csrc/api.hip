@@ -1,0 +1,369 @@
+// C ABI entry points (include/muon_amd.h): argument checks, workspace layout and the
+// launch sequence of one Muon step. Kernels live in gemm.hip, elementwise.hip, lp.hip.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+
+#include "common.h"
+
+// ---- launchers defined in the kernel files ------------------------------------------
+int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M, int64_t N,
+                     int64_t K, const void* a, int64_t lda, int64_t sa, const void* b,
+                     int64_t ldb, int64_t sb, const void* cin, int64_t ldc, int64_t sc,
+                     void* out, int64_t ldo, int64_t so, void* out_t, int64_t ldt, int64_t st,
+                     int64_t Mv, int64_t Nv, float alpha, float beta, const float* scale,
+                     int scale_mode, hipStream_t stream);
+int muon_launch_prepass(int ntensors, void* const* grads, void* const* bufs, int gdt, int bdt,
+                        int64_t nb, int64_t rows, int64_t cols, int64_t s_pitch,
+                        int64_t s_mstride, float momentum, int nesterov, int maximize,
+                        int write_grad, int write_direct, const OrthLayout& L, void* ws,
+                        int wdt, int64_t mat0, hipStream_t s);
+int muon_launch_finalize(const OrthLayout& L, void* ws, int64_t batch, float prescale,
+                         float eps, hipStream_t s);
+int muon_launch_momentum(int ntensors, void* const* grads, void* const* bufs, int gdt, int bdt,
+                         int64_t numel, float momentum, int nesterov, int maximize,
+                         int write_grad, hipStream_t s);
+int muon_launch_scale(const OrthLayout& L, void* x, int wdt, int64_t batch, const float* scale,
+                      hipStream_t s);
+int muon_launch_postpass(int ntensors, void* const* params, const float* adj, int pdt,
+                         const void* u, int udt, int64_t u_pitch, int64_t u_mstride, int64_t nb,
+                         int64_t rows, int64_t cols, float wd, int cautious, hipStream_t s);
+int muon_launch_extract(const void* src, int wdt, int64_t pitch, int64_t mstride, void* dst,
+                        int odt, int64_t rows, int64_t cols, int64_t batch, hipStream_t s);
+int muon_check_lp_format(int qformat, int64_t numel, int64_t block);
+int muon_launch_lp_prepass(int ntensors, void* const* grads, int gdt, void* const* codes,
+                           void* const* scales, const float* qmap, int qf, int64_t block,
+                           int64_t nb, int64_t rows, int64_t cols, float momentum,
+                           int nesterov, int maximize, void* direct, int64_t d_pitch,
+                           int64_t d_mstride, hipStream_t s);
+
+enum { MODE_GEMM = 0, MODE_SYRK = 1 };
+
+static thread_local char g_err[512];
+
+void muon_set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+// Padding granule of the workspace extents: the bf16 tile (256); fp32 tiles (128)
+// divide it.
+static const int64_t PAD = 256;
+
+OrthLayout muon_orth_layout(int dtype, int64_t batch, int64_t rows, int64_t cols) {
+  OrthLayout L;
+  memset(&L, 0, sizeof(L));
+  L.rows = rows;
+  L.cols = cols;
+  L.tall = rows > cols;
+  L.m = std::min(rows, cols);
+  L.n = std::max(rows, cols);
+  L.m_pad = round_up(std::max<int64_t>(L.m, 1), PAD);
+  L.n_pad = round_up(std::max<int64_t>(L.n, 1), PAD);
+  L.es = dtype == MUON_DT_F32 ? 4 : 2;
+  L.batch = batch;
+  L.parts = (L.m_pad / 64) * (L.n_pad / 64);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t o = off;
+    off = (size_t)round_up((int64_t)(off + bytes), 256);
+    return o;
+  };
+  const size_t xs = (size_t)(batch * L.m_pad * L.n_pad * L.es);
+  const size_t as = (size_t)(batch * L.m_pad * L.m_pad * L.es);
+  L.off_x = take(xs);
+  L.off_xt0 = take(xs);
+  L.off_xt1 = take(xs);
+  L.off_a = take(as);
+  L.off_b = take(as);
+  L.off_part = take((size_t)(batch * L.parts * 4));
+  L.off_scale = take((size_t)(batch * 4));
+  L.total = off;
+  return L;
+}
+
+static bool iter_dtype_ok(int dt) { return dt == MUON_DT_BF16 || dt == MUON_DT_F32; }
+static bool io_dtype_ok(int dt) {
+  return dt == MUON_DT_BF16 || dt == MUON_DT_F32 || dt == MUON_DT_F16;
+}
+
+extern "C" {
+
+int muon_amd_abi_version(void) { return 1; }
+
+const char* muon_amd_last_error(void) { return g_err; }
+
+int muon_amd_init(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    muon_set_error("init: no HIP device");
+    return MUON_ERR_DEVICE;
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+    muon_set_error("init: hipGetDeviceProperties failed");
+    return MUON_ERR_DEVICE;
+  }
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    muon_set_error("init: device %d is %s; this library is built for gfx950 only", dev,
+                   prop.gcnArchName);
+    return MUON_ERR_DEVICE;
+  }
+  return MUON_OK;
+}
+
+int muon_gram(const void* x, void* y, int dtype, int64_t batch, int64_t M, int64_t K,
+              void* stream) {
+  if (!iter_dtype_ok(dtype)) {
+    muon_set_error("gram: dtype %d not supported (bf16 or fp32)", dtype);
+    return MUON_ERR_DTYPE;
+  }
+  if (batch < 0 || M < 0 || K < 0) {
+    muon_set_error("gram: negative extent");
+    return MUON_ERR_SHAPE;
+  }
+  if (batch == 0 || M == 0) return MUON_OK;
+  return muon_launch_gemm(dtype, MODE_SYRK, true, batch, M, M, std::max<int64_t>(K, 1), x, K,
+                          M * K, x, K, M * K, nullptr, 0, 0, y, M, M * M, nullptr, 0, 0, M, M,
+                          1.0f, 0.0f, nullptr, 0, (hipStream_t)stream);
+}
+
+int64_t muon_orth_workspace_bytes(int dtype, int64_t batch, int64_t rows, int64_t cols) {
+  if (!iter_dtype_ok(dtype) || batch < 0 || rows <= 0 || cols <= 0) return -1;
+  return (int64_t)muon_orth_layout(dtype, batch, rows, cols).total;
+}
+
+int muon_orth_result(int dtype, int64_t batch, int64_t rows, int64_t cols, int steps,
+                     int64_t* offset_bytes, int64_t* row_pitch, int64_t* matrix_stride) {
+  if (!iter_dtype_ok(dtype) || rows <= 0 || cols <= 0 || steps < 0) {
+    muon_set_error("orth_result: bad arguments");
+    return MUON_ERR_ARG;
+  }
+  OrthLayout L = muon_orth_layout(dtype, batch, rows, cols);
+  if (L.tall) {
+    *offset_bytes = (int64_t)((steps % 2) ? L.off_xt1 : L.off_xt0);
+    *row_pitch = L.m_pad;
+  } else {
+    *offset_bytes = (int64_t)L.off_x;
+    *row_pitch = L.n_pad;
+  }
+  *matrix_stride = L.m_pad * L.n_pad;
+  return MUON_OK;
+}
+
+int muon_prepass(int ntensors, void* const* grads, void* const* bufs, int g_dtype,
+                 int buf_dtype, int64_t nb, int64_t rows, int64_t cols, float momentum,
+                 int nesterov, int maximize, int write_back_grad, void* ws, int ws_dtype,
+                 int64_t ws_batch, void* stream) {
+  if (!iter_dtype_ok(ws_dtype) || !io_dtype_ok(g_dtype) || (bufs && !io_dtype_ok(buf_dtype))) {
+    muon_set_error("prepass: unsupported dtype (grad %d, buf %d, ws %d)", g_dtype, buf_dtype,
+                   ws_dtype);
+    return MUON_ERR_DTYPE;
+  }
+  if (ntensors < 0 || nb <= 0 || rows <= 0 || cols <= 0) {
+    muon_set_error("prepass: bad extents (ntensors %d, nb %lld)", ntensors, (long long)nb);
+    return MUON_ERR_SHAPE;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  if (!ws) {
+    // momentum only: g' goes back into the grad tensors (write_back_grad) or stays
+    // in the buffers (no Nesterov)
+    if (!bufs) {
+      muon_set_error("prepass: nothing to do without buffers or a workspace");
+      return MUON_ERR_ARG;
+    }
+    for (int t0 = 0; t0 < ntensors; t0 += MUON_MAX_TENSORS) {
+      const int cnt = std::min(MUON_MAX_TENSORS, ntensors - t0);
+      int rc = muon_launch_momentum(cnt, grads + t0, bufs + t0, g_dtype, buf_dtype,
+                                    nb * rows * cols, momentum, nesterov, maximize,
+                                    write_back_grad, s);
+      if (rc != MUON_OK) return rc;
+    }
+    return MUON_OK;
+  }
+  if ((int64_t)ntensors * nb > ws_batch) {
+    muon_set_error("prepass: %lld matrices exceed the workspace capacity %lld",
+                   (long long)ntensors * nb, (long long)ws_batch);
+    return MUON_ERR_SHAPE;
+  }
+  OrthLayout L = muon_orth_layout(ws_dtype, ws_batch, rows, cols);
+  for (int t0 = 0; t0 < ntensors; t0 += MUON_MAX_TENSORS) {
+    const int cnt = std::min(MUON_MAX_TENSORS, ntensors - t0);
+    int rc = muon_launch_prepass(cnt, grads + t0, bufs ? bufs + t0 : nullptr, g_dtype,
+                                 buf_dtype, nb, rows, cols, cols, rows * cols, momentum,
+                                 nesterov, maximize, write_back_grad, 1, L, ws, ws_dtype,
+                                 (int64_t)t0 * nb, s);
+    if (rc != MUON_OK) return rc;
+  }
+  return MUON_OK;
+}
+
+int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64_t rows,
+                  int64_t cols, const double* coeffs, int steps, float prescale, float eps,
+                  void* stream) {
+  if (!iter_dtype_ok(ws_dtype)) {
+    muon_set_error("orth_run: unsupported dtype %d", ws_dtype);
+    return MUON_ERR_DTYPE;
+  }
+  if (batch < 0 || batch > ws_batch || rows <= 0 || cols <= 0 || steps < 0 ||
+      (steps > 0 && !coeffs)) {
+    muon_set_error("orth_run: bad arguments (batch %lld of %lld, steps %d)", (long long)batch,
+                   (long long)ws_batch, steps);
+    return MUON_ERR_ARG;
+  }
+  if (batch == 0) return MUON_OK;
+  OrthLayout L = muon_orth_layout(ws_dtype, ws_batch, rows, cols);
+  hipStream_t s = (hipStream_t)stream;
+  char* w = (char*)ws;
+  int rc = muon_launch_finalize(L, ws, batch, prescale, eps, s);
+  if (rc != MUON_OK) return rc;
+  const float* scale = (const float*)(w + L.off_scale);
+  char* X = w + L.off_x;
+  char* XT[2] = {w + L.off_xt0, w + L.off_xt1};
+  char* A = w + L.off_a;
+  char* B = w + L.off_b;
+  const int64_t mp = L.m_pad, np = L.n_pad;
+  if (steps == 0) return muon_launch_scale(L, L.tall ? XT[0] : X, ws_dtype, batch, scale, s);
+  for (int it = 0; it < steps; ++it) {
+    const float a = (float)coeffs[3 * it], b = (float)coeffs[3 * it + 1],
+                c = (float)coeffs[3 * it + 2];
+    const bool first = it == 0, last = it == steps - 1;
+    // A = X X^T (the first iteration folds the Frobenius prescale s in as s^2)
+    rc = muon_launch_gemm(ws_dtype, MODE_SYRK, false, batch, mp, mp, np, X, np, mp * np, X, np,
+                          mp * np, nullptr, 0, 0, A, mp, mp * mp, nullptr, 0, 0, L.m, L.m, 1.0f,
+                          0.0f, scale, first ? 2 : 0, s);
+    if (rc != MUON_OK) return rc;
+    // B = b*A + c*(A A)
+    rc = muon_launch_gemm(ws_dtype, MODE_SYRK, false, batch, mp, mp, mp, A, mp, mp * mp, A, mp,
+                          mp * mp, A, mp, mp * mp, B, mp, mp * mp, nullptr, 0, 0, L.m, L.m, c, b,
+                          nullptr, 0, s);
+    if (rc != MUON_OK) return rc;
+    // X' = a*X + B X, as B(i, k) . X^T(j, k); X is updated in place (its elements are
+    // only touched by the epilogue of their own tile), X^T ping-pongs.
+    void* out = (last && L.tall) ? nullptr : (void*)X;
+    void* out_t = (last && !L.tall) ? nullptr : (void*)XT[(it + 1) & 1];
+    rc = muon_launch_gemm(ws_dtype, MODE_GEMM, false, batch, mp, np, mp, B, mp, mp * mp,
+                          XT[it & 1], mp, np * mp, X, np, mp * np, out, np, mp * np, out_t, mp,
+                          np * mp, L.m, L.n, 1.0f, a, scale, first ? 1 : 0, s);
+    if (rc != MUON_OK) return rc;
+  }
+  return MUON_OK;
+}
+
+int muon_orth_extract(const void* ws, int ws_dtype, int64_t ws_batch, int64_t batch,
+                      int64_t rows, int64_t cols, int steps, void* out, int out_dtype,
+                      void* stream) {
+  if (!iter_dtype_ok(ws_dtype) || !io_dtype_ok(out_dtype)) {
+    muon_set_error("orth_extract: unsupported dtype");
+    return MUON_ERR_DTYPE;
+  }
+  if (batch < 0 || batch > ws_batch) {
+    muon_set_error("orth_extract: bad batch");
+    return MUON_ERR_ARG;
+  }
+  if (batch == 0) return MUON_OK;
+  int64_t off, pitch, mst;
+  int rc = muon_orth_result(ws_dtype, ws_batch, rows, cols, steps, &off, &pitch, &mst);
+  if (rc != MUON_OK) return rc;
+  return muon_launch_extract((const char*)ws + off, ws_dtype, pitch, mst, out, out_dtype, rows,
+                             cols, batch, (hipStream_t)stream);
+}
+
+int muon_postpass(int ntensors, void* const* params, int p_dtype, const void* u, int u_dtype,
+                  const void* ws, int ws_dtype, int64_t ws_batch, int steps, int64_t nb,
+                  int64_t rows, int64_t cols, const float* adjusted_lrs, float wd,
+                  int cautious, void* stream) {
+  if (!io_dtype_ok(p_dtype)) {
+    muon_set_error("postpass: unsupported param dtype %d", p_dtype);
+    return MUON_ERR_DTYPE;
+  }
+  if (ntensors < 0 || nb <= 0 || rows <= 0 || cols <= 0) {
+    muon_set_error("postpass: bad extents");
+    return MUON_ERR_SHAPE;
+  }
+  const char* ubase;
+  int udt;
+  int64_t pitch, mst;
+  if (u) {
+    if (!io_dtype_ok(u_dtype)) {
+      muon_set_error("postpass: unsupported update dtype %d", u_dtype);
+      return MUON_ERR_DTYPE;
+    }
+    ubase = (const char*)u;
+    udt = u_dtype;
+    pitch = cols;
+    mst = rows * cols;
+  } else {
+    if (!iter_dtype_ok(ws_dtype) || (int64_t)ntensors * nb > ws_batch) {
+      muon_set_error("postpass: bad workspace arguments");
+      return MUON_ERR_ARG;
+    }
+    int64_t off;
+    int rc = muon_orth_result(ws_dtype, ws_batch, rows, cols, steps, &off, &pitch, &mst);
+    if (rc != MUON_OK) return rc;
+    ubase = (const char*)ws + off;
+    udt = ws_dtype;
+  }
+  const int es = udt == MUON_DT_F32 ? 4 : 2;
+  hipStream_t s = (hipStream_t)stream;
+  for (int t0 = 0; t0 < ntensors; t0 += MUON_MAX_TENSORS) {
+    const int cnt = std::min(MUON_MAX_TENSORS, ntensors - t0);
+    int rc = muon_launch_postpass(cnt, params + t0, adjusted_lrs + t0, p_dtype,
+                                  ubase + (int64_t)t0 * nb * mst * es, udt, pitch, mst, nb, rows,
+                                  cols, wd, cautious, s);
+    if (rc != MUON_OK) return rc;
+  }
+  return MUON_OK;
+}
+
+int muon_lp_prepass(int ntensors, void* const* grads, int g_dtype, void* const* codes,
+                    void* const* scales, const float* qmap, int qformat, int64_t block,
+                    int64_t nb, int64_t rows, int64_t cols, float momentum, int nesterov,
+                    int maximize, void* ws, int ws_dtype, int64_t ws_batch, void* stream) {
+  if (ws_dtype != MUON_DT_BF16 || !io_dtype_ok(g_dtype)) {
+    muon_set_error("lp_prepass: workspace must be bf16 and grads bf16/fp16/fp32");
+    return MUON_ERR_DTYPE;
+  }
+  if (ntensors < 0 || nb <= 0 || rows <= 0 || cols <= 0 || (int64_t)ntensors * nb > ws_batch) {
+    muon_set_error("lp_prepass: bad extents");
+    return MUON_ERR_SHAPE;
+  }
+  int rc = muon_check_lp_format(qformat, nb * rows * cols, block);
+  if (rc != MUON_OK) return rc;
+  if (qformat != MUON_Q_FP8 && !qmap) {
+    muon_set_error("lp_prepass: missing qmap");
+    return MUON_ERR_ARG;
+  }
+  OrthLayout L = muon_orth_layout(ws_dtype, ws_batch, rows, cols);
+  hipStream_t s = (hipStream_t)stream;
+  char* w = (char*)ws;
+  char* direct = w + (L.tall ? L.off_xt0 : L.off_x);
+  const int64_t d_pitch = L.tall ? L.m_pad : L.n_pad;
+  const int64_t mst = L.m_pad * L.n_pad;
+  for (int t0 = 0; t0 < ntensors; t0 += MUON_MAX_TENSORS) {
+    const int cnt = std::min(MUON_MAX_TENSORS, ntensors - t0);
+    rc = muon_launch_lp_prepass(cnt, grads + t0, g_dtype, codes + t0, scales + t0, qmap,
+                                qformat, block, nb, rows, cols, momentum, nesterov, maximize,
+                                direct + (int64_t)t0 * nb * mst * L.es, d_pitch, mst, s);
+    if (rc != MUON_OK) return rc;
+  }
+  // Second layout and norm partials from the stored-layout X just written: a plain
+  // (no momentum) prepass that reads the valid region of the workspace itself and
+  // rewrites only its padding.
+  const int64_t nmat = (int64_t)ntensors * nb;
+  for (int64_t m0 = 0; m0 < nmat; m0 += MUON_MAX_TENSORS) {
+    const int cnt = (int)std::min<int64_t>(MUON_MAX_TENSORS, nmat - m0);
+    void* srcs[MUON_MAX_TENSORS];
+    for (int i = 0; i < cnt; ++i) srcs[i] = direct + (m0 + i) * mst * L.es;
+    rc = muon_launch_prepass(cnt, srcs, nullptr, MUON_DT_BF16, MUON_DT_BF16, 1, rows, cols,
+                             d_pitch, mst, 0.0f, 0, 0, 0, 2, L, ws, ws_dtype, m0, s);
+    if (rc != MUON_OK) return rc;
+  }
+  return MUON_OK;
+}
+
+}  // extern "C"

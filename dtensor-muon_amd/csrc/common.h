@@ -1,0 +1,148 @@
+// Shared device helpers for the MI355X (gfx950) Muon kernels.
+//
+// Numeric conventions follow PyTorch's CPU/GPU semantics so the kernels can be
+// compared bit-for-bit with the CPU oracle where the reference is elementwise:
+//  * fp32 -> bf16 is round-to-nearest-even, NaN -> 0x7FC0 (torch's BFloat16 cast).
+//  * fp32 -> fp8 e4m3fn is round-to-nearest-even with magnitudes that round past
+//    448 mapped to NaN (torch's Float8_e4m3fn cast).
+//  * No FMA contraction in elementwise math (see the pragmas in each kernel).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/muon_amd.h"
+
+#define MUON_DEVICE __device__ __forceinline__
+
+typedef uint16_t bf16_t;  // raw bfloat16 bits
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_mfma;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+MUON_DEVICE float bf16_to_f32(bf16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
+
+MUON_DEVICE bf16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)0x7fc0;  // NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+// fp16 (IEEE binary16) <-> fp32 via the hardware conversion (exact / RNE).
+MUON_DEVICE float f16_to_f32(uint16_t v) {
+  _Float16 h;
+  __builtin_memcpy(&h, &v, 2);
+  return (float)h;
+}
+MUON_DEVICE uint16_t f32_to_f16(float f) {
+  _Float16 h = (_Float16)f;
+  uint16_t v;
+  __builtin_memcpy(&v, &h, 2);
+  return v;
+}
+
+// Element load/store by dtype code (MUON_DT_*).
+template <int DT>
+struct Elem;
+template <>
+struct Elem<MUON_DT_F32> {
+  typedef float T;
+  static MUON_DEVICE float load(const void* p, int64_t i) { return ((const float*)p)[i]; }
+  static MUON_DEVICE void store(void* p, int64_t i, float v) { ((float*)p)[i] = v; }
+  static MUON_DEVICE float round(float v) { return v; }
+};
+template <>
+struct Elem<MUON_DT_BF16> {
+  typedef bf16_t T;
+  static MUON_DEVICE float load(const void* p, int64_t i) { return bf16_to_f32(((const bf16_t*)p)[i]); }
+  static MUON_DEVICE void store(void* p, int64_t i, float v) { ((bf16_t*)p)[i] = f32_to_bf16(v); }
+  static MUON_DEVICE float round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+};
+template <>
+struct Elem<MUON_DT_F16> {
+  typedef uint16_t T;
+  static MUON_DEVICE float load(const void* p, int64_t i) { return f16_to_f32(((const uint16_t*)p)[i]); }
+  static MUON_DEVICE void store(void* p, int64_t i, float v) { ((uint16_t*)p)[i] = f32_to_f16(v); }
+  static MUON_DEVICE float round(float v) { return f16_to_f32(f32_to_f16(v)); }
+};
+
+// fp32 -> float8_e4m3fn (bias 7, no infinities, 0x7f/0xff are NaN, max 448).
+// Written from the format definition: exact round-to-nearest-even onto the e4m3fn
+// grid; a magnitude that rounds above 448 becomes NaN (matching torch's cast).
+MUON_DEVICE uint8_t f32_to_e4m3fn(float f) {
+  uint32_t u = __float_as_uint(f);
+  uint8_t sign = (uint8_t)((u >> 24) & 0x80u);
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint8_t)(sign | 0x7f);  // NaN
+  // Values >= 464 (the midpoint between 448 and the next, unrepresentable, grid
+  // point 480) round above the largest finite value. 464 itself ties to even (448).
+  if (a > 0x43e80000u) return (uint8_t)(sign | 0x7f);  // > 464 -> NaN (inf too)
+  if (a < 0x3c800000u) {
+    // |f| < 2^-6: subnormal range of e4m3 (step 2^-9). Round |f| * 2^9 to an integer
+    // with ties-to-even; exact in fp32 because the scaling is a power of two.
+    float s = __uint_as_float(a) * 512.0f;
+    float r = __builtin_rintf(s);  // current rounding mode = nearest-even
+    return (uint8_t)(sign | (uint8_t)r);  // r in [0, 8]; 8 == smallest normal 0x08
+  }
+  // Normal range: keep 3 mantissa bits, round to nearest even on the dropped 20 bits.
+  uint32_t exp = (a >> 23) - 127 + 7;  // e4m3 biased exponent, >= 1 here
+  uint32_t mant = a & 0x7fffffu;
+  uint32_t q = (exp << 3) | (mant >> 20);
+  uint32_t rem = mant & 0xfffffu;
+  if (rem > 0x80000u || (rem == 0x80000u && (q & 1u))) q += 1;
+  return (uint8_t)(sign | (uint8_t)q);  // q <= 0x7e guaranteed by the 464 bound
+}
+
+MUON_DEVICE float e4m3fn_to_f32(uint8_t v) {
+  uint32_t sign = ((uint32_t)v & 0x80u) << 24;
+  uint32_t e = (v >> 3) & 0xfu;
+  uint32_t m = v & 0x7u;
+  if (e == 0xf && m == 0x7) return __uint_as_float(sign | 0x7fc00000u);
+  if (e == 0) {
+    float r = (float)m * 0.001953125f;  // m * 2^-9
+    return sign ? -r : r;
+  }
+  return __uint_as_float(sign | ((e - 7 + 127) << 23) | (m << 20));
+}
+
+MUON_DEVICE float warp_sum(float v) {
+  // Fixed butterfly order over the 64-lane wavefront: deterministic.
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+MUON_DEVICE float warp_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+static inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+// Thread-local last-error text for muon_amd_last_error().
+void muon_set_error(const char* fmt, ...);
+
+#define MUON_CHECK_LAUNCH(what)                                          \
+  do {                                                                   \
+    hipError_t _e = hipGetLastError();                                   \
+    if (_e != hipSuccess) {                                              \
+      muon_set_error("%s: launch failed: %s", what, hipGetErrorString(_e)); \
+      return MUON_ERR_LAUNCH;                                            \
+    }                                                                    \
+  } while (0)
+
+// Workspace layout shared by the prepass, iteration and postpass entry points.
+struct OrthLayout {
+  int64_t rows, cols;  // stored (param) matrix shape
+  int64_t m, n;        // m = min, n = max: the iteration runs on the wide m x n matrix
+  int64_t m_pad, n_pad;
+  int tall;            // rows > cols: stored layout is the transpose of X
+  int es;              // element size of the iteration dtype
+  int64_t batch;       // capacity in matrices
+  int64_t parts;       // norm partials per matrix
+  size_t off_x, off_xt0, off_xt1, off_a, off_b, off_part, off_scale, total;
+};
+
+OrthLayout muon_orth_layout(int dtype, int64_t batch, int64_t rows, int64_t cols);

@@ -1,0 +1,489 @@
+// HBM-bound elementwise passes around the orthogonalization.
+//
+// All passes walk the stored (param-layout) matrices in 64 x 64 tiles so the
+// pre-pass can emit both the stored layout and its transpose (through LDS) in one
+// read of the gradient and momentum, and reduce the Frobenius-norm partials of each
+// tile in a fixed order (deterministic, no atomics).
+#include "common.h"
+
+namespace {
+
+constexpr int TILE = 64;
+
+struct PrepassArgs {
+  void* grads[MUON_MAX_TENSORS];
+  void* bufs[MUON_MAX_TENSORS];
+  int64_t nb, rows, cols;
+  int64_t s_pitch, s_mstride;  // source (grad) row pitch and matrix stride, elements
+  void* direct;        // stored-layout output (workspace), matrix 0 of this launch
+  int64_t d_pitch, d_mstride;
+  void* trans;         // transposed output (workspace)
+  int64_t t_pitch, t_mstride;
+  float* partials;     // [matrix][tile]
+  int64_t parts;       // partials per matrix
+  int tiles_c;         // tiles along cols of the padded stored layout
+  float momentum;
+  int nesterov, maximize, has_buf, write_grad;
+  int write_direct;    // 0: no, 1: every element, 2: padding only (source is the direct buffer)
+};
+
+// g -> (momentum) -> x for one element; mirrors muon.py:39-56 op for op:
+// buf' = buf * mu + g ; g' = g + buf' * mu (Nesterov) or buf'.
+template <int GDT, int BDT>
+MUON_DEVICE float momentum_elem(const PrepassArgs& a, void* gp, void* bp, int64_t idx) {
+#pragma clang fp contract(off)
+  float g = Elem<GDT>::load(gp, idx);
+  if (a.maximize) g = -g;
+  if (!a.has_buf) return g;
+  float buf = Elem<BDT>::load(bp, idx);
+  float nb = buf * a.momentum;
+  nb = nb + g;
+  Elem<BDT>::store(bp, idx, nb);
+  // The per-tensor reference keeps using the fp32 value it just stored (rounded
+  // into a low-precision buffer only by the copy), muon.py:49-56.
+  if (!a.nesterov) return nb;
+  float t = nb * a.momentum;
+  return g + t;
+}
+
+// grid: x = tile index within the padded stored matrix, y = matrix of this launch.
+template <int GDT, int BDT, int WDT, int VEC>
+__global__ __launch_bounds__(256) void prepass_kernel(PrepassArgs a) {
+#pragma clang fp contract(off)
+  __shared__ float tile[TILE][TILE + 1];
+  __shared__ float wsum[4];
+  const int mat = blockIdx.y;
+  const int tr = blockIdx.x / a.tiles_c, tc = blockIdx.x % a.tiles_c;
+  const int t = (int)(mat / a.nb);
+  const int64_t mb = mat % a.nb;
+  void* gp = a.grads[t];
+  void* bp = a.bufs[t];
+  const int64_t base = mb * a.s_mstride;
+  const int tid = threadIdx.x;
+  const int64_t r0 = (int64_t)tr * TILE, c0 = (int64_t)tc * TILE;
+
+  float ss = 0.0f;
+  // Stored layout: 64 rows x 64 cols; each thread VEC consecutive columns.
+  constexpr int TPR = TILE / VEC;          // threads per row
+  constexpr int RPP = 256 / TPR;           // rows per pass
+  const int cl = (tid % TPR) * VEC;
+#pragma unroll
+  for (int rp = 0; rp < TILE / RPP; ++rp) {
+    const int rl = rp * RPP + tid / TPR;
+    const int64_t r = r0 + rl;
+    float xv[VEC];
+    bool valid[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const int64_t c = c0 + cl + e;
+      float x = 0.0f;
+      valid[e] = r < a.rows && c < a.cols;
+      if (valid[e]) {
+        const int64_t idx = base + r * a.s_pitch + c;
+        float gq = momentum_elem<GDT, BDT>(a, gp, bp, idx);
+        if (a.write_grad) Elem<GDT>::store(gp, idx, gq);
+        x = Elem<WDT>::round(gq);
+        ss += x * x;
+      }
+      xv[e] = x;
+      tile[rl][cl + e] = x;
+    }
+    if (a.write_direct) {
+      const int64_t o = (int64_t)mat * a.d_mstride + r * a.d_pitch + c0 + cl;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        if (a.write_direct == 1 || !valid[e]) Elem<WDT>::store(a.direct, o + e, xv[e]);
+    }
+  }
+  __syncthreads();
+  // Transposed layout: row (c0 + cc) of the transpose holds column cc of the tile.
+#pragma unroll
+  for (int rp = 0; rp < TILE / RPP; ++rp) {
+    const int cc = rp * RPP + tid / TPR;
+    const int64_t o = (int64_t)mat * a.t_mstride + (c0 + cc) * a.t_pitch + r0 + cl;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) Elem<WDT>::store(a.trans, o + e, tile[cl + e][cc]);
+  }
+  ss = warp_sum(ss);
+  if ((tid & 63) == 0) wsum[tid >> 6] = ss;
+  __syncthreads();
+  if (tid == 0) {
+    float s = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+    a.partials[(int64_t)mat * a.parts + blockIdx.x] = s;
+  }
+}
+
+// Momentum only (no workspace): buf' and g' as in momentum_elem, g' stored into the
+// grad tensor when write_grad. Used when the orthogonalization is supplied by the
+// caller (the module-level zeropower seam) and needs g' as a tensor.
+template <int GDT, int BDT>
+__global__ __launch_bounds__(256) void momentum_kernel(PrepassArgs a, int64_t numel) {
+#pragma clang fp contract(off)
+  const int t = blockIdx.y;
+  void* gp = a.grads[t];
+  void* bp = a.bufs[t];
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < numel;
+       i += (int64_t)gridDim.x * 256) {
+    float gq = momentum_elem<GDT, BDT>(a, gp, bp, i);
+    if (a.write_grad) Elem<GDT>::store(gp, i, gq);
+  }
+}
+
+// scale[b] = 1 / (sqrt(sum of partials) * prescale + eps); one workgroup per matrix,
+// fixed-order reduction in double.
+__global__ __launch_bounds__(256) void finalize_scale_kernel(const float* partials,
+                                                             int64_t parts, float* scale,
+                                                             float prescale, float eps) {
+#pragma clang fp contract(off)
+  __shared__ double red[256];
+  const int64_t b = blockIdx.x;
+  const float* p = partials + b * parts;
+  double s = 0.0;
+  for (int64_t i = threadIdx.x; i < parts; i += 256) s += (double)p[i];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    float norm = (float)sqrt(red[0]);
+    float denom = norm * prescale;
+    denom = denom + eps;
+    scale[b] = 1.0f / denom;
+  }
+}
+
+// x *= scale[b] over the padded stored-layout matrices (steps == 0 path).
+template <int WDT>
+__global__ __launch_bounds__(256) void scale_kernel(void* x, int64_t mstride,
+                                                    const float* scale) {
+  const int64_t b = blockIdx.y;
+  const float s = scale[b];
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < mstride;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t idx = b * mstride + i;
+    Elem<WDT>::store(x, idx, Elem<WDT>::load(x, idx) * s);
+  }
+}
+
+struct PostArgs {
+  void* params[MUON_MAX_TENSORS];
+  float adj[MUON_MAX_TENSORS];
+  const void* u;        // matrix 0 of this launch
+  int64_t u_pitch, u_mstride;
+  int64_t nb, rows, cols;
+  int tiles_c;
+  float wd;
+  int cautious;
+};
+
+// muon.py:62-77 for one element, eager op order, no contraction.
+template <int PDT, int UDT>
+MUON_DEVICE float apply_elem(float p, float u, float wd, int cautious, float adj) {
+#pragma clang fp contract(off)
+  if (wd != 0.0f) {
+    float t = wd * p;
+    if (cautious) {
+      float prod = u * p;
+      float mask = prod > 0.0f ? 1.0f : 0.0f;
+      t = t * mask;
+    }
+    float v = u + t;
+    float step = adj * v;
+    return p - step;
+  }
+  float step = Elem<UDT>::round(adj * u);  // 0-dim fp32 * u keeps u's dtype
+  return p - step;
+}
+
+template <int PDT, int UDT, int VEC>
+__global__ __launch_bounds__(256) void postpass_kernel(PostArgs a) {
+#pragma clang fp contract(off)
+  const int mat = blockIdx.y;
+  const int tr = blockIdx.x / a.tiles_c, tc = blockIdx.x % a.tiles_c;
+  const int t = (int)(mat / a.nb);
+  const int64_t mb = mat % a.nb;
+  void* pp = a.params[t];
+  const float adj = a.adj[t];
+  const int tid = threadIdx.x;
+  const int64_t r0 = (int64_t)tr * TILE, c0 = (int64_t)tc * TILE;
+  constexpr int TPR = TILE / VEC;
+  constexpr int RPP = 256 / TPR;
+  const int cl = (tid % TPR) * VEC;
+#pragma unroll
+  for (int rp = 0; rp < TILE / RPP; ++rp) {
+    const int64_t r = r0 + rp * RPP + tid / TPR;
+    if (r >= a.rows) continue;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const int64_t c = c0 + cl + e;
+      if (c >= a.cols) continue;
+      const int64_t pi = mb * a.rows * a.cols + r * a.cols + c;
+      const int64_t ui = (int64_t)mat * a.u_mstride + r * a.u_pitch + c;
+      const float p = Elem<PDT>::load(pp, pi);
+      const float u = Elem<UDT>::load(a.u, ui);
+      Elem<PDT>::store(pp, pi, apply_elem<PDT, UDT>(p, u, a.wd, a.cautious, adj));
+    }
+  }
+}
+
+// Copy the stored-layout result out of the workspace (with dtype conversion).
+template <int WDT, int ODT>
+__global__ __launch_bounds__(256) void extract_kernel(const void* src, int64_t pitch,
+                                                      int64_t mstride, void* dst, int64_t rows,
+                                                      int64_t cols) {
+  const int64_t b = blockIdx.y;
+  const int64_t n = rows * cols;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / cols, c = i % cols;
+    Elem<ODT>::store(dst, b * n + i, Elem<WDT>::load(src, b * mstride + r * pitch + c));
+  }
+}
+
+template <int GDT, int BDT, int WDT>
+void launch_prepass_t(const PrepassArgs& a, dim3 grid, bool vec4, hipStream_t s) {
+  if (vec4)
+    hipLaunchKernelGGL((prepass_kernel<GDT, BDT, WDT, 4>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((prepass_kernel<GDT, BDT, WDT, 1>), grid, dim3(256), 0, s, a);
+}
+
+template <int GDT, int BDT>
+int launch_prepass_w(int wdt, const PrepassArgs& a, dim3 grid, bool vec4, hipStream_t s) {
+  if (wdt == MUON_DT_BF16)
+    launch_prepass_t<GDT, BDT, MUON_DT_BF16>(a, grid, vec4, s);
+  else if (wdt == MUON_DT_F32)
+    launch_prepass_t<GDT, BDT, MUON_DT_F32>(a, grid, vec4, s);
+  else
+    return MUON_ERR_DTYPE;
+  return MUON_OK;
+}
+
+template <int GDT>
+int launch_prepass_b(int bdt, int wdt, const PrepassArgs& a, dim3 grid, bool vec4,
+                     hipStream_t s) {
+  switch (bdt) {
+    case MUON_DT_F32: return launch_prepass_w<GDT, MUON_DT_F32>(wdt, a, grid, vec4, s);
+    case MUON_DT_BF16: return launch_prepass_w<GDT, MUON_DT_BF16>(wdt, a, grid, vec4, s);
+    case MUON_DT_F16: return launch_prepass_w<GDT, MUON_DT_F16>(wdt, a, grid, vec4, s);
+  }
+  return MUON_ERR_DTYPE;
+}
+
+template <int PDT, int UDT>
+void launch_post_t(const PostArgs& a, dim3 grid, bool vec4, hipStream_t s) {
+  if (vec4)
+    hipLaunchKernelGGL((postpass_kernel<PDT, UDT, 4>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((postpass_kernel<PDT, UDT, 1>), grid, dim3(256), 0, s, a);
+}
+
+template <int PDT>
+int launch_post_u(int udt, const PostArgs& a, dim3 grid, bool vec4, hipStream_t s) {
+  switch (udt) {
+    case MUON_DT_F32: launch_post_t<PDT, MUON_DT_F32>(a, grid, vec4, s); return MUON_OK;
+    case MUON_DT_BF16: launch_post_t<PDT, MUON_DT_BF16>(a, grid, vec4, s); return MUON_OK;
+    case MUON_DT_F16: launch_post_t<PDT, MUON_DT_F16>(a, grid, vec4, s); return MUON_OK;
+  }
+  return MUON_ERR_DTYPE;
+}
+
+template <int WDT>
+int launch_extract_o(int odt, const void* src, int64_t pitch, int64_t mstride, void* dst,
+                     int64_t rows, int64_t cols, int64_t batch, hipStream_t s) {
+  const int64_t n = rows * cols;
+  dim3 grid((unsigned)std::min<int64_t>((n + 255) / 256, 4096), (unsigned)batch);
+  switch (odt) {
+    case MUON_DT_F32:
+      hipLaunchKernelGGL((extract_kernel<WDT, MUON_DT_F32>), grid, dim3(256), 0, s, src, pitch,
+                         mstride, dst, rows, cols);
+      return MUON_OK;
+    case MUON_DT_BF16:
+      hipLaunchKernelGGL((extract_kernel<WDT, MUON_DT_BF16>), grid, dim3(256), 0, s, src, pitch,
+                         mstride, dst, rows, cols);
+      return MUON_OK;
+    case MUON_DT_F16:
+      hipLaunchKernelGGL((extract_kernel<WDT, MUON_DT_F16>), grid, dim3(256), 0, s, src, pitch,
+                         mstride, dst, rows, cols);
+      return MUON_OK;
+  }
+  return MUON_ERR_DTYPE;
+}
+
+}  // namespace
+
+// ---- launchers used by api.hip ------------------------------------------------------
+
+// One prepass launch over ntensors (<= MUON_MAX_TENSORS) tensors whose matrices
+// start at workspace matrix `mat0`.
+int muon_launch_prepass(int ntensors, void* const* grads, void* const* bufs, int gdt, int bdt,
+                        int64_t nb, int64_t rows, int64_t cols, int64_t s_pitch,
+                        int64_t s_mstride, float momentum, int nesterov, int maximize,
+                        int write_grad, int write_direct, const OrthLayout& L, void* ws,
+                        int wdt, int64_t mat0, hipStream_t s) {
+  PrepassArgs a;
+  for (int i = 0; i < ntensors; ++i) {
+    a.grads[i] = grads[i];
+    a.bufs[i] = bufs ? bufs[i] : nullptr;
+  }
+  a.nb = nb;
+  a.rows = rows;
+  a.cols = cols;
+  a.s_pitch = s_pitch;
+  a.s_mstride = s_mstride;
+  char* w = (char*)ws;
+  const int64_t rows_pad = L.tall ? L.n_pad : L.m_pad;
+  const int64_t cols_pad = L.tall ? L.m_pad : L.n_pad;
+  const int64_t mst = L.m_pad * L.n_pad;
+  char* direct = w + (L.tall ? L.off_xt0 : L.off_x);
+  char* trans = w + (L.tall ? L.off_x : L.off_xt0);
+  a.direct = direct + mat0 * mst * L.es;
+  a.trans = trans + mat0 * mst * L.es;
+  a.d_pitch = cols_pad;
+  a.t_pitch = rows_pad;
+  a.d_mstride = mst;
+  a.t_mstride = mst;
+  a.partials = (float*)(w + L.off_part) + mat0 * L.parts;
+  a.parts = L.parts;
+  a.tiles_c = (int)(cols_pad / TILE);
+  a.momentum = momentum;
+  a.nesterov = nesterov;
+  a.maximize = maximize;
+  a.has_buf = bufs != nullptr;
+  a.write_grad = write_grad;
+  a.write_direct = write_direct;
+  const bool vec4 = (cols % 4) == 0 && (s_pitch % 4) == 0;
+  dim3 grid((unsigned)((rows_pad / TILE) * (cols_pad / TILE)), (unsigned)(ntensors * nb));
+  int rc;
+  switch (gdt) {
+    case MUON_DT_F32: rc = launch_prepass_b<MUON_DT_F32>(bdt, wdt, a, grid, vec4, s); break;
+    case MUON_DT_BF16: rc = launch_prepass_b<MUON_DT_BF16>(bdt, wdt, a, grid, vec4, s); break;
+    case MUON_DT_F16: rc = launch_prepass_b<MUON_DT_F16>(bdt, wdt, a, grid, vec4, s); break;
+    default: rc = MUON_ERR_DTYPE;
+  }
+  if (rc != MUON_OK) {
+    muon_set_error("prepass: unsupported dtypes (grad %d, buf %d, ws %d)", gdt, bdt, wdt);
+    return rc;
+  }
+  MUON_CHECK_LAUNCH("prepass");
+  return MUON_OK;
+}
+
+template <int GDT>
+int launch_momentum_b(int bdt, const PrepassArgs& a, int64_t numel, dim3 grid, hipStream_t s) {
+  switch (bdt) {
+    case MUON_DT_F32:
+      hipLaunchKernelGGL((momentum_kernel<GDT, MUON_DT_F32>), grid, dim3(256), 0, s, a, numel);
+      return MUON_OK;
+    case MUON_DT_BF16:
+      hipLaunchKernelGGL((momentum_kernel<GDT, MUON_DT_BF16>), grid, dim3(256), 0, s, a, numel);
+      return MUON_OK;
+    case MUON_DT_F16:
+      hipLaunchKernelGGL((momentum_kernel<GDT, MUON_DT_F16>), grid, dim3(256), 0, s, a, numel);
+      return MUON_OK;
+  }
+  return MUON_ERR_DTYPE;
+}
+
+int muon_launch_momentum(int ntensors, void* const* grads, void* const* bufs, int gdt, int bdt,
+                         int64_t numel, float momentum, int nesterov, int maximize,
+                         int write_grad, hipStream_t s) {
+  PrepassArgs a;
+  for (int i = 0; i < ntensors; ++i) {
+    a.grads[i] = grads[i];
+    a.bufs[i] = bufs[i];
+  }
+  a.momentum = momentum;
+  a.nesterov = nesterov;
+  a.maximize = maximize;
+  a.has_buf = 1;
+  a.write_grad = write_grad;
+  dim3 grid((unsigned)std::min<int64_t>((numel + 255) / 256, 8192), (unsigned)ntensors);
+  int rc;
+  switch (gdt) {
+    case MUON_DT_F32: rc = launch_momentum_b<MUON_DT_F32>(bdt, a, numel, grid, s); break;
+    case MUON_DT_BF16: rc = launch_momentum_b<MUON_DT_BF16>(bdt, a, numel, grid, s); break;
+    case MUON_DT_F16: rc = launch_momentum_b<MUON_DT_F16>(bdt, a, numel, grid, s); break;
+    default: rc = MUON_ERR_DTYPE;
+  }
+  if (rc != MUON_OK) {
+    muon_set_error("momentum: unsupported dtypes (grad %d, buf %d)", gdt, bdt);
+    return rc;
+  }
+  MUON_CHECK_LAUNCH("momentum");
+  return MUON_OK;
+}
+
+int muon_launch_finalize(const OrthLayout& L, void* ws, int64_t batch, float prescale,
+                         float eps, hipStream_t s) {
+  char* w = (char*)ws;
+  hipLaunchKernelGGL(finalize_scale_kernel, dim3((unsigned)batch), dim3(256), 0, s,
+                     (const float*)(w + L.off_part), L.parts, (float*)(w + L.off_scale),
+                     prescale, eps);
+  MUON_CHECK_LAUNCH("finalize_scale");
+  return MUON_OK;
+}
+
+int muon_launch_scale(const OrthLayout& L, void* x, int wdt, int64_t batch, const float* scale,
+                      hipStream_t s) {
+  const int64_t mst = L.m_pad * L.n_pad;
+  dim3 grid((unsigned)std::min<int64_t>((mst + 255) / 256, 4096), (unsigned)batch);
+  if (wdt == MUON_DT_BF16)
+    hipLaunchKernelGGL((scale_kernel<MUON_DT_BF16>), grid, dim3(256), 0, s, x, mst, scale);
+  else
+    hipLaunchKernelGGL((scale_kernel<MUON_DT_F32>), grid, dim3(256), 0, s, x, mst, scale);
+  MUON_CHECK_LAUNCH("scale");
+  return MUON_OK;
+}
+
+int muon_launch_postpass(int ntensors, void* const* params, const float* adj, int pdt,
+                         const void* u, int udt, int64_t u_pitch, int64_t u_mstride, int64_t nb,
+                         int64_t rows, int64_t cols, float wd, int cautious, hipStream_t s) {
+  PostArgs a;
+  for (int i = 0; i < ntensors; ++i) {
+    a.params[i] = params[i];
+    a.adj[i] = adj[i];
+  }
+  a.u = u;
+  a.u_pitch = u_pitch;
+  a.u_mstride = u_mstride;
+  a.nb = nb;
+  a.rows = rows;
+  a.cols = cols;
+  a.wd = wd;
+  a.cautious = cautious;
+  const int64_t tiles_r = (rows + TILE - 1) / TILE, tiles_c = (cols + TILE - 1) / TILE;
+  a.tiles_c = (int)tiles_c;
+  const bool vec4 = (cols % 4) == 0 && (u_pitch % 4) == 0;
+  dim3 grid((unsigned)(tiles_r * tiles_c), (unsigned)(ntensors * nb));
+  int rc;
+  switch (pdt) {
+    case MUON_DT_F32: rc = launch_post_u<MUON_DT_F32>(udt, a, grid, vec4, s); break;
+    case MUON_DT_BF16: rc = launch_post_u<MUON_DT_BF16>(udt, a, grid, vec4, s); break;
+    case MUON_DT_F16: rc = launch_post_u<MUON_DT_F16>(udt, a, grid, vec4, s); break;
+    default: rc = MUON_ERR_DTYPE;
+  }
+  if (rc != MUON_OK) {
+    muon_set_error("postpass: unsupported dtypes (param %d, u %d)", pdt, udt);
+    return rc;
+  }
+  MUON_CHECK_LAUNCH("postpass");
+  return MUON_OK;
+}
+
+int muon_launch_extract(const void* src, int wdt, int64_t pitch, int64_t mstride, void* dst,
+                        int odt, int64_t rows, int64_t cols, int64_t batch, hipStream_t s) {
+  int rc;
+  if (wdt == MUON_DT_BF16)
+    rc = launch_extract_o<MUON_DT_BF16>(odt, src, pitch, mstride, dst, rows, cols, batch, s);
+  else
+    rc = launch_extract_o<MUON_DT_F32>(odt, src, pitch, mstride, dst, rows, cols, batch, s);
+  if (rc != MUON_OK) {
+    muon_set_error("extract: unsupported dtype %d", odt);
+    return rc;
+  }
+  MUON_CHECK_LAUNCH("extract");
+  return MUON_OK;
+}

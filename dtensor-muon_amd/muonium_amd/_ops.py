@@ -1,0 +1,346 @@
+"""Device operations of the Muon step, each a short launch sequence on libmuon_amd.
+
+Shapes: a Muon tensor is handed over as ``nb`` stored matrices of ``rows x cols``
+(its transformed-gradient shape, optim.py:395-401), contiguous. Same-shape tensors
+of a foreach bucket share one batched workspace, so one launch sequence covers the
+whole bucket.
+"""
+
+from __future__ import annotations
+
+import threading
+
+import numpy as np
+from typing import Sequence
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+# ---------------------------------------------------------------------------------
+# workspace cache: one growable buffer per (device, iteration dtype, padded m, n)
+
+_PAD = 256
+_ws_lock = threading.Lock()
+_ws_cache: dict[tuple, tuple[int, Tensor]] = {}
+
+
+def _pad(x: int) -> int:
+    return (max(x, 1) + _PAD - 1) // _PAD * _PAD
+
+
+def workspace(device: torch.device, dtype: torch.dtype, batch: int, rows: int, cols: int):
+    """(buffer, capacity) with room for ``batch`` matrices of rows x cols.
+
+    The layout only depends on the padded (min, max) extents and the capacity, so
+    tall and wide matrices of the same extents share a buffer. Contents need no
+    initialization (every launch rewrites what it reads later)."""
+    m, n = _pad(min(rows, cols)), _pad(max(rows, cols))
+    key = (device, dtype, m, n)
+    with _ws_lock:
+        hit = _ws_cache.get(key)
+        if hit is not None and hit[0] >= batch:
+            return hit[1], hit[0]
+        nbytes = _lib.load().muon_orth_workspace_bytes(_lib.dtype_code(dtype), batch, rows, cols)
+        if nbytes < 0:
+            raise RuntimeError(f"muonium_amd: bad workspace request {batch}x{rows}x{cols}")
+        if hit is not None:
+            del _ws_cache[key]
+            del hit
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        _ws_cache[key] = (batch, buf)
+        return buf, batch
+
+
+def release_workspaces() -> None:
+    """Drop every cached workspace (they are re-created on demand)."""
+    with _ws_lock:
+        _ws_cache.clear()
+
+
+# ---------------------------------------------------------------------------------
+# shape helpers
+
+
+def matrix_view(t) -> tuple[int, int, int]:
+    """(nb, rows, cols) of a 2D+ tensor (or shape) viewed as a batch of its last two
+    dims."""
+    shape = tuple(t.shape) if isinstance(t, Tensor) else tuple(t)
+    rows, cols = shape[-2], shape[-1]
+    nb = 1
+    for d in shape[:-2]:
+        nb *= d
+    return nb, rows, cols
+
+
+def _check_cuda_contig(ts: Sequence[Tensor], what: str) -> None:
+    for t in ts:
+        if not t.is_cuda:
+            raise RuntimeError(f"muonium_amd: {what} must live on a HIP device (got {t.device})")
+        if not t.is_contiguous():
+            raise RuntimeError(f"muonium_amd: {what} must be contiguous")
+
+
+def coeffs_for(strategy: str, steps: int) -> tuple[list[tuple[float, float, float]], float]:
+    from .orthogonalize.newton_schulz import NS_COEFFS
+    from .orthogonalize.polar_express import POLAR_EXPRESS_COEFFS
+
+    if strategy == "polar_express":
+        return list(POLAR_EXPRESS_COEFFS[:steps]), 1.02
+    if strategy == "newton_schulz":
+        return [NS_COEFFS] * steps, 1.0
+    raise ValueError(f"Unknown orthogonalization strategy: {strategy}")
+
+
+def _flat_coeffs(coeffs: Sequence[tuple[float, float, float]]):
+    return _lib.f64_array([c for abc in coeffs for c in abc])
+
+
+# ---------------------------------------------------------------------------------
+# gram
+
+
+def gram_(x: Tensor, y: Tensor) -> None:
+    """y = x x^T over the last two dims; x (B, M, K) and y (B, M, M) contiguous."""
+    lib = _lib.load()
+    _lib.ensure_device(x.device)
+    B, M, K = matrix_view(x)
+    _lib.check(
+        lib.muon_gram(x.data_ptr(), y.data_ptr(), _lib.dtype_code(x.dtype), B, M, K,
+                      _lib.stream(x.device)),
+        "muon_gram",
+    )
+
+
+# ---------------------------------------------------------------------------------
+# orthogonalization of a list of same-shape tensors (zeropower / loop functions)
+
+
+def orthogonalize(
+    tensors: Sequence[Tensor],
+    coeffs: Sequence[tuple[float, float, float]],
+    *,
+    prescale: float,
+    eps: float,
+    iter_dtype: torch.dtype,
+    out_dtype: torch.dtype,
+) -> Tensor:
+    """Run the polynomial iteration on every matrix of ``tensors`` (same shape, any
+    float dtype, cast to ``iter_dtype`` on the fly) and return the stacked result
+    of shape (len(tensors), *shape) in ``out_dtype``."""
+    lib = _lib.load()
+    t0 = tensors[0]
+    device = t0.device
+    _lib.ensure_device(device)
+    _check_cuda_contig(tensors, "orthogonalization inputs")
+    nb, rows, cols = matrix_view(t0)
+    count = len(tensors)
+    out = torch.empty((count, *t0.shape), dtype=out_dtype, device=device)
+    if out.numel() == 0:
+        return out
+    ws, cap = workspace(device, iter_dtype, count * nb, rows, cols)
+    wdt = _lib.dtype_code(iter_dtype)
+    s = _lib.stream(device)
+    steps = len(coeffs)
+    grads = _lib.ptr_array(tensors)
+    _lib.check(
+        lib.muon_prepass(count, grads, None, _lib.dtype_code(t0.dtype), 0, nb, rows, cols, 0.0,
+                         0, 0, 0, ws.data_ptr(), wdt, cap, s),
+        "muon_prepass",
+    )
+    _lib.check(
+        lib.muon_orth_run(ws.data_ptr(), wdt, cap, count * nb, rows, cols, _flat_coeffs(coeffs),
+                          steps, prescale, eps, s),
+        "muon_orth_run",
+    )
+    _lib.check(
+        lib.muon_orth_extract(ws.data_ptr(), wdt, cap, count * nb, rows, cols, steps,
+                              out.data_ptr(), _lib.dtype_code(out_dtype), s),
+        "muon_orth_extract",
+    )
+    return out
+
+
+# ---------------------------------------------------------------------------------
+# the Muon step pieces
+
+
+def adjusted_lrs(lr_ratios: Sequence[Tensor], lr: Tensor | float) -> list[float]:
+    """lr_ratio * lr as the fp32 product of two 0-dim fp32 tensors (muon.py:71,115)."""
+    lr32 = np.float32(float(lr))
+    return [float(np.float32(float(r)) * lr32) for r in lr_ratios]
+
+
+def momentum_only(
+    grads: Sequence[Tensor], bufs: Sequence[Tensor], *, momentum: float, nesterov: bool,
+    maximize: bool, write_back_grad: bool,
+) -> None:
+    """buf' = buf*mu + g (and, with write_back_grad, grad <- g + mu*buf') in place."""
+    lib = _lib.load()
+    g0 = grads[0]
+    _lib.ensure_device(g0.device)
+    _check_cuda_contig(list(grads) + list(bufs), "momentum inputs")
+    nb, rows, cols = matrix_view(g0)
+    _lib.check(
+        lib.muon_prepass(len(grads), _lib.ptr_array(grads), _lib.ptr_array(bufs),
+                         _lib.dtype_code(g0.dtype), _lib.dtype_code(bufs[0].dtype), nb, rows, cols,
+                         momentum, int(nesterov), int(maximize), int(write_back_grad), None, 1,
+                         0, _lib.stream(g0.device)),
+        "muon_prepass(momentum)",
+    )
+
+
+def postpass(
+    params: Sequence[Tensor], us: Sequence[Tensor] | Tensor, lrs: Sequence[float], *,
+    weight_decay: float, cautious_wd: bool, shape=None,
+) -> None:
+    """p <- p - lr_t * (u + wd * p * [u*p > 0]) elementwise.
+
+    ``us`` is either one contiguous stacked tensor or a list of tensors with the
+    elements of each param in the same order; ``shape`` (default: the params') gives
+    the (…, rows, cols) matrix view."""
+    lib = _lib.load()
+    p0 = params[0]
+    _lib.ensure_device(p0.device)
+    _check_cuda_contig(params, "params")
+    nb, rows, cols = matrix_view(p0 if shape is None else shape)
+    s = _lib.stream(p0.device)
+    if isinstance(us, Tensor):
+        chunks = [(list(range(len(params))), us)]
+    else:
+        chunks = [([i], u) for i, u in enumerate(us)]
+    for idx, u in chunks:
+        u = u.contiguous()
+        ps = [params[i] for i in idx]
+        _lib.check(
+            lib.muon_postpass(len(ps), _lib.ptr_array(ps), _lib.dtype_code(p0.dtype),
+                              u.data_ptr(), _lib.dtype_code(u.dtype), None, 1, 0, 0, nb, rows,
+                              cols, _lib.f32_array([lrs[i] for i in idx]),
+                              float(weight_decay), int(cautious_wd), s),
+            "muon_postpass",
+        )
+
+
+def fused_step(
+    params: Sequence[Tensor],
+    grads: Sequence[Tensor],
+    bufs: Sequence[Tensor],
+    lrs: Sequence[float],
+    *,
+    momentum: float,
+    nesterov: bool,
+    maximize: bool,
+    write_back_grad: bool,
+    weight_decay: float,
+    cautious_wd: bool,
+    coeffs: Sequence[tuple[float, float, float]],
+    prescale: float,
+    eps: float = 1e-7,
+) -> None:
+    """One Muon step over a same-shape bucket: momentum pre-pass into the batched bf16
+    workspace, the iteration, and the weight-decay/apply post-pass reading the
+    result straight from the workspace."""
+    lib = _lib.load()
+    g0 = grads[0]
+    device = g0.device
+    _lib.ensure_device(device)
+    _check_cuda_contig(list(params) + list(grads) + list(bufs), "Muon step tensors")
+    nb, rows, cols = matrix_view(g0)
+    count = len(grads)
+    ws, cap = workspace(device, torch.bfloat16, count * nb, rows, cols)
+    s = _lib.stream(device)
+    steps = len(coeffs)
+    _lib.check(
+        lib.muon_prepass(count, _lib.ptr_array(grads), _lib.ptr_array(bufs),
+                         _lib.dtype_code(g0.dtype), _lib.dtype_code(bufs[0].dtype), nb, rows, cols,
+                         momentum, int(nesterov), int(maximize), int(write_back_grad),
+                         ws.data_ptr(), _lib.DT_BF16, cap, s),
+        "muon_prepass",
+    )
+    _lib.check(
+        lib.muon_orth_run(ws.data_ptr(), _lib.DT_BF16, cap, count * nb, rows, cols,
+                          _flat_coeffs(coeffs), steps, prescale, eps, s),
+        "muon_orth_run",
+    )
+    _lib.check(
+        lib.muon_postpass(count, _lib.ptr_array(params), _lib.dtype_code(params[0].dtype), None,
+                          0, ws.data_ptr(), _lib.DT_BF16, cap, steps, nb, rows, cols,
+                          _lib.f32_array(lrs), float(weight_decay), int(cautious_wd), s),
+        "muon_postpass",
+    )
+
+
+def fused_lp_step(
+    params: Sequence[Tensor],
+    grads: Sequence[Tensor],
+    states: Sequence,  # QuantizedState objects
+    lrs: Sequence[float],
+    *,
+    momentum: float,
+    nesterov: bool,
+    maximize: bool,
+    weight_decay: float,
+    cautious_wd: bool,
+    coeffs: Sequence[tuple[float, float, float]],
+    prescale: float,
+    eps: float = 1e-7,
+) -> None:
+    """fused_step with quantized momentum: dequant -> momentum -> requant pre-pass."""
+    lib = _lib.load()
+    g0 = grads[0]
+    device = g0.device
+    _lib.ensure_device(device)
+    _check_cuda_contig(list(params) + list(grads), "MuonLP step tensors")
+    st0 = states[0]
+    nb, rows, cols = matrix_view(g0)
+    count = len(grads)
+    ws, cap = workspace(device, torch.bfloat16, count * nb, rows, cols)
+    s = _lib.stream(device)
+    steps = len(coeffs)
+    _lib.check(
+        lib.muon_lp_prepass(
+            count, _lib.ptr_array(grads), _lib.dtype_code(g0.dtype),
+            _lib.ptr_array([st.codes for st in states]), _lib.ptr_array([st.scale for st in states]),
+            st0.qmap.data_ptr() if st0.qmap is not None else None, st0.qformat, st0.block_size,
+            nb, rows, cols, momentum, int(nesterov), int(maximize), ws.data_ptr(), _lib.DT_BF16,
+            cap, s,
+        ),
+        "muon_lp_prepass",
+    )
+    _lib.check(
+        lib.muon_orth_run(ws.data_ptr(), _lib.DT_BF16, cap, count * nb, rows, cols,
+                          _flat_coeffs(coeffs), steps, prescale, eps, s),
+        "muon_orth_run",
+    )
+    _lib.check(
+        lib.muon_postpass(count, _lib.ptr_array(params), _lib.dtype_code(params[0].dtype), None,
+                          0, ws.data_ptr(), _lib.DT_BF16, cap, steps, nb, rows, cols,
+                          _lib.f32_array(lrs), float(weight_decay), int(cautious_wd), s),
+        "muon_postpass",
+    )
+
+
+def lp_quantize(src: Tensor, codes: Tensor, scale: Tensor, qmap: Tensor | None, qformat: int,
+                block: int) -> None:
+    lib = _lib.load()
+    _lib.ensure_device(src.device)
+    src = src.contiguous().float()
+    _lib.check(
+        lib.muon_lp_quantize(src.data_ptr(), codes.data_ptr(), scale.data_ptr(),
+                             qmap.data_ptr() if qmap is not None else None, qformat, src.numel(),
+                             block, _lib.stream(src.device)),
+        "muon_lp_quantize",
+    )
+
+
+def lp_dequantize(codes: Tensor, scale: Tensor, qmap: Tensor | None, qformat: int, block: int,
+                  numel: int, out: Tensor) -> None:
+    lib = _lib.load()
+    _lib.ensure_device(codes.device)
+    _lib.check(
+        lib.muon_lp_dequantize(codes.data_ptr(), scale.data_ptr(),
+                               qmap.data_ptr() if qmap is not None else None, qformat, numel,
+                               block, out.data_ptr(), _lib.stream(codes.device)),
+        "muon_lp_dequantize",
+    )

@@ -1,0 +1,140 @@
+"""NorMuon: Muon with neuron-wise update normalization (arXiv:2510.05491).
+
+Mirrors muonium/optim/algorithms/normuon.py:16-203. Momentum, orthogonalization and
+the weight-decay/apply pass run on the MI355X kernels; the per-row normalization of
+the orthogonalized update (a handful of row/matrix reductions) is expressed with torch
+device ops for now.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from muonium_amd import _ops
+from muonium_amd.orthogonalize import OrthogonalizationStrategy
+
+from .base import (
+    BufferSpec,
+    MuonAlgorithm,
+    orthogonalize_batch,
+    orthogonalize_single,
+    register_muon_algorithm,
+)
+from .muon import _Contig, momentum_seam, schedule
+
+
+def _normuon_normalize(
+    u: Tensor, v: Tensor, muon_beta2: float, split_sizes: tuple[int, ...] | None = None
+) -> tuple[Tensor, Tensor]:
+    """Per-row second-moment EMA v' = lerp(v, mean_row(u^2), 1 - beta2), u / (sqrt(v')
+    + 1e-8), rescaled to u's Frobenius norm; per row block with split_sizes
+    (normuon.py:16-55)."""
+    if split_sizes is not None:
+        parts = [
+            _normuon_normalize(ub, vb, muon_beta2)
+            for ub, vb in zip(
+                u.split(list(split_sizes), dim=-2), v.split(list(split_sizes), dim=-2), strict=True
+            )
+        ]
+        return torch.cat([p[0] for p in parts], dim=-2), torch.cat([p[1] for p in parts], dim=-2)
+    u = u.to(v.dtype)
+    norm_u = u.norm(p=2, dim=(-2, -1), keepdim=True)
+    v_new = torch.lerp(v, (u * u).mean(dim=-1, keepdim=True), 1 - muon_beta2)
+    u = u / (v_new.sqrt() + 1e-8)
+    norm_u_new = u.norm(p=2, dim=(-2, -1), keepdim=True).clamp(min=1e-8)
+    return u * (norm_u / norm_u_new), v_new
+
+
+def _normuon_step(params, grads, bufs, variances, lr_ratios, *, lr, weight_decay, cautious_wd,
+                  momentum, nesterov, maximize, ns_steps, orthogonalization_strategy,
+                  split_sizes, muon_beta2, batched):
+    lrs = _ops.adjusted_lrs(lr_ratios, lr)
+    schedule(orthogonalization_strategy, ns_steps)
+    P, G, B = _Contig(params), _Contig(grads), _Contig(bufs)
+    gq = momentum_seam(G.work, B.work, momentum=momentum, nesterov=nesterov,
+                       maximize=maximize, batched=batched)
+    if batched:
+        us = orthogonalize_batch(gq, ns_steps=ns_steps, strategy=orthogonalization_strategy,
+                                 split_sizes=split_sizes)
+    else:
+        us = [orthogonalize_single(gq[0], ns_steps=ns_steps, strategy=orthogonalization_strategy,
+                                   split_sizes=split_sizes)]
+    normalized = []
+    for u, v in zip(us, variances, strict=True):
+        un, v_new = _normuon_normalize(u, v.to(torch.float32), muon_beta2, split_sizes)
+        v.copy_(v_new)
+        normalized.append(un.contiguous())
+    pview = [p.view(g.shape) for p, g in zip(P.work, G.work)]
+    _ops.postpass(pview, normalized, lrs, weight_decay=weight_decay, cautious_wd=cautious_wd,
+                  shape=G.work[0].shape)
+    P.writeback()
+    if batched and nesterov and not maximize:
+        G.writeback()
+    B.writeback()
+
+
+@register_muon_algorithm
+class NorMuon(MuonAlgorithm):
+    """Muon plus a neuron-wise second-moment normalization of the update."""
+
+    name = "normuon"
+    options = {"muon_beta2": 0.95}
+    state_spec = {
+        "momentum_buffer": BufferSpec(like="grad", signed=True),
+        "variance_neuron": BufferSpec(like="grad_rows", signed=False),
+    }
+
+    def update(
+        self,
+        param: Tensor,
+        grad: Tensor,
+        state: dict[str, Tensor],
+        lr_ratio: Tensor,
+        *,
+        lr: Tensor,
+        weight_decay: float,
+        cautious_wd: bool,
+        momentum: float,
+        nesterov: bool,
+        maximize: bool,
+        ns_steps: int,
+        orthogonalization_strategy: OrthogonalizationStrategy,
+        split_sizes: tuple[int, ...] | None,
+        muon_beta2: float = 0.95,
+        **opts,
+    ) -> None:
+        _normuon_step(
+            [param], [grad], [state["momentum_buffer"]], [state["variance_neuron"]], [lr_ratio],
+            lr=lr, weight_decay=weight_decay, cautious_wd=cautious_wd, momentum=momentum,
+            nesterov=nesterov, maximize=maximize, ns_steps=ns_steps,
+            orthogonalization_strategy=orthogonalization_strategy, split_sizes=split_sizes,
+            muon_beta2=muon_beta2, batched=False,
+        )
+
+    def foreach_update(
+        self,
+        params: list[Tensor],
+        grads: list[Tensor],
+        state: dict[str, list[Tensor]],
+        lr_ratios: list[Tensor],
+        *,
+        lr: Tensor,
+        weight_decay: float,
+        cautious_wd: bool,
+        momentum: float,
+        nesterov: bool,
+        maximize: bool,
+        ns_steps: int,
+        orthogonalization_strategy: OrthogonalizationStrategy,
+        split_sizes: tuple[int, ...] | None,
+        muon_beta2: float = 0.95,
+        **opts,
+    ) -> None:
+        _normuon_step(
+            params, grads, state["momentum_buffer"], state["variance_neuron"], lr_ratios,
+            lr=lr, weight_decay=weight_decay, cautious_wd=cautious_wd, momentum=momentum,
+            nesterov=nesterov, maximize=maximize, ns_steps=ns_steps,
+            orthogonalization_strategy=orthogonalization_strategy, split_sizes=split_sizes,
+            muon_beta2=muon_beta2, batched=True,
+        )

@@ -1,0 +1,160 @@
+/*
+ * muon_amd.h — C ABI of the MI355X-native Muon optimizer step (libmuon_amd.so).
+ *
+ * The library replaces the device-side work of muonium's `Muon.step()` hot path
+ * (tonyf/dtensor-muon, package `muonium`). Every entry point takes plain device
+ * pointers, sizes and a hipStream_t passed as `void*`; nothing allocates, frees or
+ * synchronizes: the caller (the Python host package, or any FFI user) owns every
+ * buffer. All launches are asynchronous on the given stream.
+ *
+ * Return value: MUON_OK (0) or one of the MUON_ERR_* codes; the text of the last
+ * error on the calling thread is available from muon_amd_last_error().
+ *
+ * Shapes. A "tensor" handed to the step entry points is `nb` stored matrices of
+ * `rows x cols`, contiguous (row-major, matrix after matrix): the transformed
+ * gradient shape of muonium's `_init_muon_group` (optim.py:395-401). The
+ * orthogonalization runs on the wide orientation X (m x n, m = min(rows, cols)),
+ * transposing tall matrices as pe_loop/ns_loop do (polar_express.py:52-54,
+ * newton_schulz.py:41-43).
+ *
+ * Workspace. The iteration works in a caller-allocated workspace whose size comes
+ * from muon_orth_workspace_bytes(); the same (dtype, batch, rows, cols) quadruple
+ * must be passed to every call that touches it. Its contents need no
+ * initialization: every call rewrites what it reads later.
+ */
+#ifndef MUON_AMD_H
+#define MUON_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes */
+#define MUON_DT_F32 0
+#define MUON_DT_BF16 1
+#define MUON_DT_F16 2
+
+/* status codes */
+#define MUON_OK 0
+#define MUON_ERR_SHAPE 1
+#define MUON_ERR_DTYPE 2
+#define MUON_ERR_ALIGN 3
+#define MUON_ERR_LAUNCH 4
+#define MUON_ERR_ARG 5
+#define MUON_ERR_DEVICE 6
+
+/* quantized-state formats (muon_lp_*) */
+#define MUON_Q_8BIT 8
+#define MUON_Q_4BIT 4
+#define MUON_Q_FP8 0
+
+/* Maximum tensors per multi-tensor launch; larger lists are chunked internally. */
+#define MUON_MAX_TENSORS 32
+
+/* ABI version of this header (bumped on any signature change). */
+int muon_amd_abi_version(void);
+
+/* Text of the last error reported on the calling thread ("" if none). */
+const char* muon_amd_last_error(void);
+
+/* Checks that the current HIP device is a gfx950 (MI355X) and that the code
+ * objects load. No counterpart in the reference (Triton JIT-compiles on first use). */
+int muon_amd_init(void);
+
+/* ---- Gram kernel -------------------------------------------------------------
+ * y[b] = x[b] @ x[b]^T for b < batch; x is (batch, M, K) contiguous, y is
+ * (batch, M, M) contiguous, both `dtype` (bf16 or fp32), fp32 accumulation, output
+ * exactly symmetric (upper-triangle tiles computed, lower mirrored).
+ * Replaces: muonium/kernels/gram.py:109-152 `gram_(d_in, d_out)` (the Triton
+ * `gram_nd`, gram.py:21-106). The contract checks of gram.py:114-130 live in the
+ * Python wrapper, which raises the reference's AssertionError. */
+int muon_gram(const void* x, void* y, int dtype, int64_t batch, int64_t M, int64_t K,
+              void* stream);
+
+/* ---- Orthogonalization workspace ---------------------------------------------- */
+int64_t muon_orth_workspace_bytes(int dtype, int64_t batch, int64_t rows, int64_t cols);
+
+/* Location of the orthogonalized result U (stored layout rows x cols) inside the
+ * workspace after muon_orth_run(..., steps, ...): byte offset of matrix 0, row
+ * pitch and matrix stride in elements. */
+int muon_orth_result(int dtype, int64_t batch, int64_t rows, int64_t cols, int steps,
+                     int64_t* offset_bytes, int64_t* row_pitch, int64_t* matrix_stride);
+
+/* ---- Pre-pass: momentum / Nesterov -> bf16 X (both layouts) + norm partials ------
+ * For tensor t < ntensors (each nb matrices of rows x cols, elementwise):
+ *   g  = maximize ? -grad : grad                                  (muon.py:41-42)
+ *   buf' = buf * momentum + g        (fp32 math, stored in buf's dtype) (muon.py:49-50)
+ *   g' = nesterov ? g + buf' * momentum : buf'                     (muon.py:53-56)
+ *   X[t*nb + i] = cast(g', iteration dtype)                        (orthogonalize.py:101-102)
+ * With bufs == NULL the momentum step is skipped (g' = g): the zeropower cast path.
+ * write_back_grad stores g' into grad (the foreach driver's in-place Nesterov
+ * update of the gradient list, muon.py:117-118). The sum of squares of the cast
+ * values is accumulated per matrix for the Frobenius prescale (polar_express.py:89).
+ * Replaces: muonium/optim/algorithms/muon.py:39-56 and :108-119, plus the
+ * `torch.stack(...).bfloat16()` of orthogonalize.py:159-161. */
+int muon_prepass(int ntensors, void* const* grads, void* const* bufs, int g_dtype,
+                 int buf_dtype, int64_t nb, int64_t rows, int64_t cols, float momentum,
+                 int nesterov, int maximize, int write_back_grad, void* ws, int ws_dtype,
+                 int64_t ws_batch, void* stream);
+
+/* ---- Iteration: Newton-Schulz / Polar Express on the workspace -----------------
+ * For the first `batch` matrices of the workspace: X /= (||X||_F * prescale + eps),
+ * then for each of `steps` coefficient triples (a, b, c) (coeffs is steps*3 doubles):
+ *   A = X X^T;  B = b*A + c*A A;  X = a*X + B X
+ * in bf16 (fp32 accumulation) or fp32 according to ws_dtype.
+ * Replaces: muonium/orthogonalize/polar_express.py:71-115 `pe_loop_triton`
+ * (prescale 1.02) and newton_schulz.py:60-107 `ns_loop_triton` (prescale 1.0). */
+int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64_t rows,
+                  int64_t cols, const double* coeffs, int steps, float prescale, float eps,
+                  void* stream);
+
+/* Copy U (first `batch` matrices, stored layout) out of the workspace into a
+ * contiguous (batch, rows, cols) tensor of out_dtype. Replaces the return/unbind of
+ * orthogonalize.py:101-102, :159-162. */
+int muon_orth_extract(const void* ws, int ws_dtype, int64_t ws_batch, int64_t batch,
+                      int64_t rows, int64_t cols, int steps, void* out, int out_dtype,
+                      void* stream);
+
+/* ---- Post-pass: cautious weight decay + shape-scaled apply ----------------------
+ * For tensor t, element e (u from the workspace when u == NULL, else from the
+ * contiguous tensor u of u_dtype holding ntensors*nb*rows*cols elements):
+ *   v = wd != 0 ? (cautious ? u + (wd*p)*(u*p > 0) : u + wd*p) : u    (muon.py:62-69)
+ *   p = round(p - adjusted_lrs[t] * v)                                 (muon.py:71-77)
+ * in fp32 with no contraction; when wd == 0 the product adjusted_lr*u is rounded to
+ * u's dtype first (eager type promotion of a 0-dim fp32 tensor times a bf16 tensor).
+ * Replaces: muonium/optim/algorithms/muon.py:59-77 and :121-140. */
+int muon_postpass(int ntensors, void* const* params, int p_dtype, const void* u, int u_dtype,
+                  const void* ws, int ws_dtype, int64_t ws_batch, int steps, int64_t nb,
+                  int64_t rows, int64_t cols, const float* adjusted_lrs, float wd,
+                  int cautious, void* stream);
+
+/* ---- Quantized momentum (MuonLP) -------------------------------------------------
+ * State of one tensor of `numel` values: codes (uint8; numel bytes for 8-bit and
+ * fp8, numel/2 for 4-bit with element 2i in the high nibble) and one fp32 scale per
+ * block of `block` consecutive values. 8/4-bit codes index the 256/16-entry fp32
+ * `qmap`; value = qmap[code] * scale. fp8 codes are float8_e4m3fn; value =
+ * float(code) * scale. Quantizing a block: absmax = max(|x|) clipped at 1e-12;
+ * scale = absmax (fp8: absmax / 448); y = x / scale (IEEE division); 8/4-bit code =
+ * largest i with qmap[i] <= y, then i+1 if y - qmap[i] >= (qmap[i+1]-qmap[i])*0.5.
+ * Replaces the torchao 0.17.0 OptimState8bit / OptimState4bit / OptimStateFp8
+ * arithmetic reached from muonium/optim/optim_lp.py:118-133 via muon.py:45,50. */
+int muon_lp_quantize(const float* src, void* codes, float* scales, const float* qmap,
+                     int qformat, int64_t numel, int64_t block, void* stream);
+int muon_lp_dequantize(const void* codes, const float* scales, const float* qmap,
+                       int qformat, int64_t numel, int64_t block, float* dst, void* stream);
+
+/* Fused dequant -> momentum -> requant pre-pass for quantized momentum buffers:
+ * as muon_prepass, with buf = dequant(codes, scales) and buf' requantized in
+ * place; Nesterov uses the unquantized buf' (muon.py:49-56). */
+int muon_lp_prepass(int ntensors, void* const* grads, int g_dtype, void* const* codes,
+                    void* const* scales, const float* qmap, int qformat, int64_t block,
+                    int64_t nb, int64_t rows, int64_t cols, float momentum, int nesterov,
+                    int maximize, void* ws, int ws_dtype, int64_t ws_batch, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MUON_AMD_H */

@@ -1,0 +1,28 @@
+"""CPU oracle for the MI355X Muon step — TEST INFRASTRUCTURE ONLY.
+
+This package restates, on the CPU, the arithmetic of the reference's hot path
+(tonyf/dtensor-muon, package ``muonium`` 0.2.0): the Newton-Schulz / Polar Express
+iteration, the Muon / NorMuon update rules, the per-parameter and foreach drivers, and
+the blockwise quantizers of the low-precision momentum state. Every function cites the
+reference file:line it follows.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
+may import it, and only as the checker (or as the CPU baseline that is timed). The
+product package (``dtensor-muon_amd/muonium_amd``) never imports, calls or links
+anything here.
+
+Pinning status (what fixes each function independently of its own formula):
+
+* ``muon_ref.polar_iteration`` / ``pe_loop`` / ``ns_loop``: the reference's own
+  property tests (orthogonality, SVD closeness, steps=0 prescale, manual one-step
+  expansion with overridden coefficients, transpose symmetry, zero/rank-1 inputs,
+  orthogonal fixed point, scale invariance, batched == unbatched) and the fp64 run of
+  the same iteration.
+* ``muon_ref.muon_update`` / ``muon_foreach_update`` / ``normuon_*`` /
+  ``split_*``: the closed-form known answers of the reference tests
+  (test_optim.py:392-584, test_algorithms.py:174-393).
+* ``quant_ref``: the quantized-state arithmetic lives in torchao 0.17.0, which is not
+  present here; the restatement follows torchao's published algorithm and is pinned
+  by brute-force nearest-code search, map structure, round-trip error bounds and
+  torch's own float8_e4m3fn cast. Bit parity with torchao itself is UNPINNED.
+"""

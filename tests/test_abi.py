@@ -1,0 +1,80 @@
+"""The C ABI library on the CPU: it loads, exports every entry point include/muon_amd.h
+declares, and validates arguments (returning an error, never touching the device)
+before any launch."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from muonium_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "muon_amd.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(muon_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared()
+    assert len(declared) >= 12
+    missing = [s for s in declared if not hasattr(lib, s)]
+    assert not missing, missing
+    assert sorted(_lib.EXPORTED_SYMBOLS) == declared
+
+
+def test_abi_version_and_error_text():
+    lib = _lib.load()
+    assert lib.muon_amd_abi_version() == 1
+    assert isinstance(_lib.last_error(), str)
+
+
+def test_workspace_size_formula():
+    lib = _lib.load()
+    # bf16, 2 matrices of 300 x 130 -> m_pad 256, n_pad 512
+    nbytes = lib.muon_orth_workspace_bytes(_lib.DT_BF16, 2, 300, 130)
+    x = 2 * 256 * 512 * 2
+    a = 2 * 256 * 256 * 2
+    parts = 2 * (256 // 64) * (512 // 64) * 4
+    assert nbytes == 3 * x + 2 * a + parts + 256
+    assert lib.muon_orth_workspace_bytes(_lib.DT_BF16, 1, 300, 130) < nbytes
+    assert lib.muon_orth_workspace_bytes(7, 1, 4, 4) == -1
+    assert lib.muon_orth_workspace_bytes(_lib.DT_F32, 1, 0, 4) == -1
+
+
+def test_result_location_follows_orientation():
+    lib = _lib.load()
+    off, pitch, mst = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    assert lib.muon_orth_result(_lib.DT_BF16, 4, 100, 300, 5, off, pitch, mst) == 0
+    assert off.value == 0 and pitch.value == 512 and mst.value == 256 * 512
+    assert lib.muon_orth_result(_lib.DT_BF16, 4, 300, 100, 5, off, pitch, mst) == 0
+    tall_odd = off.value
+    assert lib.muon_orth_result(_lib.DT_BF16, 4, 300, 100, 4, off, pitch, mst) == 0
+    assert pitch.value == 256 and off.value != tall_odd
+
+
+@pytest.mark.parametrize(
+    "call,code",
+    [
+        (lambda L: L.muon_gram(None, None, 9, 1, 4, 4, None), 2),
+        (lambda L: L.muon_gram(None, None, 1, -1, 4, 4, None), 1),
+        (lambda L: L.muon_prepass(1, None, None, 1, 0, 0, 4, 4, 0.9, 1, 0, 0, None, 1, 1, None), 1),
+        (lambda L: L.muon_prepass(1, None, None, 1, 0, 1, 4, 4, 0.9, 1, 0, 0, None, 1, 1, None), 5),
+        (lambda L: L.muon_orth_run(None, 1, 1, 2, 4, 4, None, 1, 1.0, 1e-7, None), 5),
+        (lambda L: L.muon_orth_run(None, 5, 1, 1, 4, 4, None, 1, 1.0, 1e-7, None), 2),
+        (lambda L: L.muon_postpass(1, None, 9, None, 1, None, 1, 1, 1, 1, 4, 4, None, 0.0, 0, None), 2),
+        (lambda L: L.muon_lp_quantize(None, None, None, None, 3, 256, 256, None), 5),
+        (lambda L: L.muon_lp_quantize(None, None, None, None, 8, 300, 256, None), 1),
+        (lambda L: L.muon_lp_dequantize(None, None, None, 4, 254, 127, None, None), 1),
+    ],
+)
+def test_argument_errors_return_codes_without_launching(call, code):
+    lib = _lib.load()
+    assert call(lib) == code
+    assert _lib.last_error() != ""

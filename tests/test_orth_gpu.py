@@ -1,0 +1,147 @@
+"""Newton-Schulz / Polar Express iteration on the HIP path vs the CPU oracle.
+
+bf16 iteration: compared with the oracle restated at the HIP path's bf16 storage
+points (tolerance 1e-2 rel-Frobenius, the bar stated for bf16 iteration), and bounded
+against the fp64 iteration and against the reference's compiled-Triton rounding
+points. fp32 iteration: compared with the oracle's fp32 iteration at 1e-5
+rel-Frobenius. Mirrors tests/orthogonalize/test_{newton_schulz,polar_express,
+orthogonalize}.py of the reference.
+"""
+
+import pytest
+import torch
+
+from helpers import rel_fro
+from muonium_amd.orthogonalize import foreach_zeropower, zeropower
+from muonium_amd.orthogonalize.newton_schulz import ns_loop, ns_loop_triton
+from muonium_amd.orthogonalize.orthogonalize import _get_orthogonalization_fn
+from muonium_amd.orthogonalize.polar_express import POLAR_EXPRESS_COEFFS, pe_loop
+from oracle import muon_ref
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-2   # HIP bf16 vs the oracle at the same storage points
+FP64_TOL = 2e-2   # HIP bf16 vs the exact (fp64) iteration
+TRITON_TOL = 4e-2  # HIP bf16 vs the reference's pe_loop_triton rounding points
+FP32_TOL = 1e-5   # HIP fp32 iteration vs the fp64 iteration (non-square inputs)
+FP32_TOL_SQUARE = 3e-5  # square Gaussian inputs: the fp32 iteration itself is ~1.3e-5 off
+
+SHAPES = [(8, 256, 128), (8, 128, 256), (4, 512, 512), (256, 128), (128, 256), (3, 130, 70),
+          (2, 70, 300), (1, 768, 2304)]
+STRATS = ["polar_express", "newton_schulz"]
+
+
+def _inputs(shape, seed=0):
+    return torch.randn(*shape, generator=torch.Generator().manual_seed(seed))
+
+
+@pytest.mark.parametrize("strategy", STRATS)
+@pytest.mark.parametrize("steps", [1, 3, 5])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_bf16_iteration_matches_oracle(shape, steps, strategy):
+    X = _inputs(shape)
+    coeffs, prescale = muon_ref.strategy_coeffs(strategy, steps)
+    fn = pe_loop if strategy == "polar_express" else ns_loop
+    got = fn(X.bfloat16().cuda(), steps, eps=1e-7).cpu()
+    assert got.dtype == torch.bfloat16 and got.shape == X.shape
+    ref = muon_ref.polar_iteration_bf16(X, coeffs, prescale=prescale, eps=1e-7)
+    assert rel_fro(got, ref) <= BF16_TOL, f"vs fused-bf16 oracle {rel_fro(got, ref):.3e}"
+    exact = muon_ref.polar_iteration(X.bfloat16().double(), coeffs, prescale=prescale, eps=1e-7)
+    assert rel_fro(got, exact) <= FP64_TOL, f"vs fp64 {rel_fro(got, exact):.3e}"
+    tri = muon_ref.polar_iteration_bf16(X, coeffs, prescale=prescale, eps=1e-7, rounding="triton")
+    assert rel_fro(got, tri) <= TRITON_TOL, f"vs triton rounding {rel_fro(got, tri):.3e}"
+
+
+@pytest.mark.parametrize("strategy", STRATS)
+@pytest.mark.parametrize("shape", [(4, 256, 128), (128, 256), (3, 130, 70), (2, 512, 512)])
+def test_fp32_iteration_matches_oracle(shape, strategy):
+    X = _inputs(shape, seed=1)
+    coeffs, prescale = muon_ref.strategy_coeffs(strategy, 5)
+    fn = pe_loop if strategy == "polar_express" else ns_loop
+    got = fn(X.cuda(), 5, eps=1e-7).cpu()
+    assert got.dtype == torch.float32
+    ref = muon_ref.polar_iteration(X.double(), coeffs, prescale=prescale, eps=1e-7)
+    tol = FP32_TOL_SQUARE if shape[-1] == shape[-2] else FP32_TOL
+    assert rel_fro(got, ref) <= tol, f"{rel_fro(got, ref):.3e}"
+
+
+@pytest.mark.parametrize("strategy", STRATS)
+def test_steps_zero_returns_prescaled_input(strategy):
+    X = _inputs((3, 130, 70), seed=2)
+    prescale = 1.02 if strategy == "polar_express" else 1.0
+    got = zeropower(X.cuda(), steps=0, strategy=strategy).cpu()
+    ref = muon_ref.prescale_fp32(X, prescale=prescale, eps=1e-7)
+    torch.testing.assert_close(got.float(), ref.float(), rtol=8e-3, atol=0)
+
+
+@pytest.mark.parametrize("strategy", STRATS)
+def test_transposed_input_gives_transposed_output_exactly(strategy):
+    X = _inputs((96, 40), seed=3).bfloat16().cuda()
+    a = zeropower(X, strategy=strategy)
+    b = zeropower(X.T.contiguous(), strategy=strategy).T
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("strategy", STRATS)
+def test_batched_equals_unbatched_exactly(strategy):
+    Xs = [_inputs((64, 32), seed=10 + i).cuda() for i in range(3)]
+    batched = foreach_zeropower(Xs, strategy=strategy)
+    for x, u in zip(Xs, batched):
+        assert torch.equal(u, zeropower(x, strategy=strategy))
+
+
+def test_iteration_is_deterministic():
+    X = _inputs((4, 300, 200), seed=4).cuda()
+    assert torch.equal(zeropower(X, strategy="polar_express"),
+                       zeropower(X, strategy="polar_express"))
+
+
+@pytest.mark.parametrize("strategy", STRATS)
+def test_zero_and_rank_one_inputs(strategy):
+    zeros = torch.zeros(32, 16, device="cuda")
+    out = zeropower(zeros, strategy=strategy)
+    assert torch.count_nonzero(out) == 0
+    gen = torch.Generator().manual_seed(4)
+    r1 = torch.outer(torch.randn(32, generator=gen), torch.randn(16, generator=gen)).cuda()
+    assert torch.isfinite(zeropower(r1, strategy=strategy).float()).all()
+
+
+@pytest.mark.parametrize("strategy", STRATS)
+def test_output_is_near_orthogonal(strategy):
+    X = _inputs((256, 128), seed=5).cuda()
+    U = zeropower(X, strategy=strategy).float()
+    sv = torch.linalg.svdvals(U.cpu())
+    lo, hi = (0.6, 1.3) if strategy == "newton_schulz" else (0.8, 1.2)
+    assert sv.min() > lo and sv.max() < hi, (sv.min(), sv.max())
+
+
+def test_zeropower_returns_bf16_and_foreach_keeps_order():
+    Gs = [_inputs((32, 16), seed=20 + i).cuda() + i for i in range(3)]
+    outs = foreach_zeropower(Gs, strategy="polar_express")
+    assert len(outs) == 3
+    for g, u in zip(Gs, outs):
+        assert u.dtype is torch.bfloat16
+        assert torch.equal(u, zeropower(g, strategy="polar_express"))
+
+
+def test_foreach_zeropower_contract_errors():
+    with pytest.raises(RuntimeError, match="stack"):
+        foreach_zeropower([torch.randn(32, 16, device="cuda"), torch.randn(16, 32, device="cuda")])
+    with pytest.raises(IndexError):
+        foreach_zeropower([])
+
+
+def test_strategy_validation_and_dispatch_table():
+    G = torch.randn(16, 8, device="cuda")
+    with pytest.raises(ValueError, match="Unknown orthogonalization strategy"):
+        zeropower(G, strategy="bogus")
+    with pytest.raises(AssertionError, match="only supports up to 5 optimization steps"):
+        zeropower(G, steps=6, strategy="polar_express")
+    assert _get_orthogonalization_fn("newton_schulz", True) is ns_loop_triton
+    assert _get_orthogonalization_fn("newton_schulz", False) is ns_loop
+    assert len(POLAR_EXPRESS_COEFFS) == 5
+
+
+def test_empty_batch_is_passthrough():
+    X = torch.randn(0, 256, 128, device="cuda", dtype=torch.bfloat16)
+    assert pe_loop(X, 5).shape == X.shape

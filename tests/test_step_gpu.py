@@ -1,0 +1,385 @@
+"""The Muon step on the HIP path vs the oracle (muonium's Muon/MuonBaseline semantics).
+
+* Known answers of the reference tests (test_optim.py:392-584) with the orthogonalizer
+  replaced by identity, run on the device (momentum, Nesterov, cautious / plain wd,
+  maximize, flatten, lr_ratio).
+* Bit-exactness of the fused pre/post passes: given the same U, the fused step equals
+  the oracle's fp32 update arithmetic exactly, and its momentum buffer is exact.
+* foreach == per-parameter, grad mutation semantics, multi-step trajectories,
+  checkpoint continuity, host-offloaded parameters, NorMuon and split_sizes.
+"""
+
+import math
+
+import pytest
+import torch
+import torch.nn as nn
+
+import muonium_amd.optim.algorithms.base as algo_base
+from helpers import rel_fro
+from muonium_amd import Muon
+from muonium_amd.orthogonalize import zeropower
+from oracle import muon_ref
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _identity(monkeypatch):
+    monkeypatch.setattr(algo_base, "zeropower", lambda g, **_: g)
+    monkeypatch.setattr(algo_base, "foreach_zeropower", lambda gs, **_: [g for g in gs])
+
+
+# ---- known answers (identity orthogonalizer) ------------------------------------------
+
+
+@pytest.mark.parametrize("foreach", [False, True])
+def test_direct_update_initializes_state_and_uses_lr_ratio(monkeypatch, foreach):
+    _identity(monkeypatch)
+    p = nn.Parameter(torch.ones(4, 2, device=DEV))
+    p.grad = torch.full_like(p, 0.5)
+    opt = Muon([p], lr=0.1, wd=0.0, momentum=0.0, nesterov=False, foreach=foreach)
+    opt.step()
+    st = opt.state[p]
+    assert torch.equal(st["step"], torch.tensor(1.0))
+    assert torch.equal(st["lr_ratio"], torch.tensor(math.sqrt(2.0)))
+    torch.testing.assert_close(st["momentum_buffer"], torch.full_like(p, 0.5))
+    torch.testing.assert_close(p, torch.ones_like(p) - math.sqrt(2.0) * 0.1 * 0.5)
+
+
+@pytest.mark.parametrize("foreach", [False, True])
+def test_nesterov_uses_updated_buffer(monkeypatch, foreach):
+    _identity(monkeypatch)
+    p = nn.Parameter(torch.ones(2, 2, device=DEV))
+    p.grad = torch.full_like(p, 0.5)
+    opt = Muon([p], lr=0.1, wd=0.0, momentum=0.5, nesterov=True, foreach=foreach)
+    opt.step()
+    torch.testing.assert_close(opt.state[p]["momentum_buffer"], torch.full_like(p, 0.5))
+    torch.testing.assert_close(p, torch.ones_like(p) - 0.1 * 0.75)
+
+
+@pytest.mark.parametrize("foreach", [False, True])
+@pytest.mark.parametrize("cautious,expected", [(True, [[-1.0, -2.0], [2.0, 1.0]]),
+                                                (False, [[-1.0, -1.0], [1.0, 1.0]])])
+def test_weight_decay_known_answers(monkeypatch, foreach, cautious, expected):
+    _identity(monkeypatch)
+    p = nn.Parameter(torch.tensor([[1.0, -1.0], [1.0, -1.0]], device=DEV))
+    p.grad = torch.tensor([[1.0, 1.0], [-1.0, -1.0]], device=DEV)
+    opt = Muon([p], lr=1.0, wd=1.0, momentum=0.0, nesterov=False, use_cautious_wd=cautious,
+               foreach=foreach)
+    opt.step()
+    torch.testing.assert_close(p, torch.tensor(expected, device=DEV))
+
+
+@pytest.mark.parametrize("foreach", [False, True])
+def test_maximize_keeps_grad_and_direction(monkeypatch, foreach):
+    _identity(monkeypatch)
+    p = nn.Parameter(torch.ones(2, 2, device=DEV))
+    grad = torch.full_like(p, 0.5)
+    p.grad = grad
+    opt = Muon([p], lr=0.1, wd=0.0, momentum=0.0, nesterov=False, maximize=True,
+               foreach=foreach)
+    opt.step()
+    first = p.detach().clone()
+    opt.step()
+    torch.testing.assert_close(grad, torch.full_like(grad, 0.5))
+    torch.testing.assert_close(first, torch.full_like(first, 1.05))
+    torch.testing.assert_close(p, torch.full_like(p, 1.10))
+
+
+def test_bf16_params_keep_fp32_momentum(monkeypatch):
+    _identity(monkeypatch)
+    p = nn.Parameter(torch.ones(2, 2, dtype=torch.bfloat16, device=DEV))
+    p.grad = torch.full_like(p, 0.5)
+    opt = Muon([p], lr=0.1, wd=0.0, momentum=0.9, nesterov=False)
+    opt.step()
+    assert opt.state[p]["momentum_buffer"].dtype is torch.float32
+
+
+def test_skips_params_without_grad(monkeypatch):
+    _identity(monkeypatch)
+    a = nn.Parameter(torch.ones(2, 2, device=DEV))
+    b = nn.Parameter(torch.ones(2, 2, device=DEV))
+    a.grad = torch.full_like(a, 0.5)
+    opt = Muon([a, b], lr=0.1, wd=0.0, momentum=0.0)
+    opt.step()
+    assert a in opt.state and b not in opt.state
+    torch.testing.assert_close(b, torch.ones_like(b))
+
+
+@pytest.mark.parametrize(
+    "shape,flatten,seen,ratio",
+    [((2, 2, 2, 2), True, (2, 8), 1.0), ((2, 2, 2, 2), False, (4, 2, 2), 1.0),
+     ((2, 4, 2), False, (2, 4, 2), math.sqrt(2.0)), ((2, 2, 2), False, (2, 2, 2), 1.0)],
+)
+def test_flatten_shapes(monkeypatch, shape, flatten, seen, ratio):
+    seen_shapes = []
+
+    def fake(g, **_):
+        seen_shapes.append(tuple(g.shape))
+        return g
+
+    monkeypatch.setattr(algo_base, "zeropower", fake)
+    p = nn.Parameter(torch.ones(*shape, device=DEV))
+    p.grad = torch.full_like(p, 0.5)
+    opt = Muon([{"params": [p], "flatten": flatten}], lr=0.1, wd=0.0, momentum=0.0,
+               foreach=False)
+    opt.step()
+    assert seen_shapes == [seen]
+    assert torch.equal(opt.state[p]["lr_ratio"], torch.tensor(ratio))
+    torch.testing.assert_close(p, torch.ones_like(p) - ratio * 0.1 * 0.5)
+
+
+# ---- the fused step vs the oracle --------------------------------------------------------
+
+CASES = [
+    # shape, param dtype, grad dtype
+    ((64, 48), torch.float32, torch.float32),
+    ((48, 64), torch.float32, torch.float32),
+    ((256, 512), torch.float32, torch.float32),
+    ((300, 130), torch.bfloat16, torch.bfloat16),
+    ((3, 40, 72), torch.bfloat16, torch.bfloat16),
+    ((130, 70), torch.float16, torch.float16),
+]
+HP = [
+    dict(wd=0.1, use_cautious_wd=True, momentum=0.95, nesterov=True, maximize=False,
+         orthogonalization_strategy="polar_express"),
+    dict(wd=0.3, use_cautious_wd=False, momentum=0.9, nesterov=False, maximize=False,
+         orthogonalization_strategy="newton_schulz"),
+    dict(wd=0.0, use_cautious_wd=True, momentum=0.95, nesterov=True, maximize=True,
+         orthogonalization_strategy="polar_express"),
+]
+
+
+def _make(shape, pdt, gdt, seed):
+    gen = torch.Generator().manual_seed(seed)
+    p0 = torch.randn(shape, generator=gen).to(pdt)
+    g0 = torch.randn(shape, generator=gen).to(gdt)
+    buf0 = torch.randn(shape, generator=gen) * 0.1
+    return p0, g0, buf0
+
+
+def _oracle_step(p0, g0, buf0, hp, orth, lr=0.02):
+    strategy = hp["orthogonalization_strategy"]
+    return muon_ref.muon_update(
+        p0, g0, buf0, muon_ref.lr_ratio(g0.shape), lr=lr, weight_decay=hp["wd"],
+        cautious_wd=hp["use_cautious_wd"], momentum=hp["momentum"], nesterov=hp["nesterov"],
+        maximize=hp["maximize"], ns_steps=5, strategy=strategy, orth_single=orth,
+    )
+
+
+def _run_step(p0, g0, buf0, hp, foreach, lr=0.02):
+    p = nn.Parameter(p0.clone().to(DEV))
+    p.grad = g0.clone().to(DEV)
+    opt = Muon([p], lr=lr, foreach=foreach, **hp)
+    opt._init_muon_group  # noqa: B018
+    # seed the momentum buffer with buf0 through a first state init
+    st = opt.state[p]
+    st["step"] = torch.tensor(0.0)
+    st["momentum_buffer"] = buf0.clone().to(DEV)
+    st["lr_ratio"] = torch.tensor(math.sqrt(max(1.0, g0.shape[-2] / g0.shape[-1])))
+    opt.step()
+    torch.cuda.synchronize()
+    return p, opt
+
+
+@pytest.mark.parametrize("hp", HP, ids=["pe-cautious-nesterov", "ns-plain-wd", "pe-maximize-nowd"])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"{c[0]}-{str(c[1])[6:]}")
+@pytest.mark.parametrize("foreach", [False, True])
+def test_fused_step_bit_exact_given_u(case, hp, foreach):
+    shape, pdt, gdt = case
+    p0, g0, buf0 = _make(shape, pdt, gdt, seed=7)
+    p, opt = _run_step(p0, g0, buf0, hp, foreach)
+    # g' exactly as the kernel computes it, then U from the HIP orthogonalizer
+    gt = muon_ref.transform_grad(g0, False)
+    _, ref_buf, gq, _ = _oracle_step(p0, g0, buf0, hp, orth=lambda g: g)
+    strategy = hp["orthogonalization_strategy"]
+    U = zeropower(gq.to(DEV), steps=5, strategy=strategy).cpu()
+    ref_p, _, _, _ = _oracle_step(p0, g0, buf0, hp, orth=lambda g: U)
+    assert torch.equal(opt.state[p]["momentum_buffer"].cpu(), ref_buf), "momentum buffer"
+    got = p.detach().cpu()
+    assert torch.equal(got, ref_p), (
+        f"param mismatch: {(got.float() - ref_p.float()).abs().max().item():.3e}"
+    )
+    assert gt.shape == g0.shape
+
+
+@pytest.mark.parametrize("hp", HP[:2], ids=["pe", "ns"])
+@pytest.mark.parametrize("case", CASES[:4], ids=lambda c: f"{c[0]}")
+def test_fused_step_matches_oracle_update(case, hp):
+    shape, pdt, gdt = case
+    p0, g0, buf0 = _make(shape, pdt, gdt, seed=11)
+    p, _ = _run_step(p0, g0, buf0, hp, foreach=True)
+    coeffs, prescale = muon_ref.strategy_coeffs(hp["orthogonalization_strategy"], 5)
+    orth = lambda g: muon_ref.polar_iteration_bf16(g, coeffs, prescale=prescale, eps=1e-7)
+    ref_p, _, _, _ = _oracle_step(p0, g0, buf0, hp, orth=orth)
+    d_got = p.detach().cpu().double() - p0.double()
+    d_ref = ref_p.double() - p0.double()
+    assert rel_fro(d_got, d_ref) <= 2e-2
+
+
+def test_foreach_equals_per_param_and_mutates_grads_under_nesterov():
+    shapes = [(32, 16), (32, 16), (16, 32), (24, 24), (3, 8, 12)]
+    gen = torch.Generator().manual_seed(0)
+    init = [torch.randn(s, generator=gen) for s in shapes]
+    kwargs = dict(lr=0.2, wd=0.3, nesterov=True, use_cautious_wd=True,
+                  orthogonalization_strategy="polar_express")
+    ref_p = [nn.Parameter(t.clone().to(DEV)) for t in init]
+    fe_p = [nn.Parameter(t.clone().to(DEV)) for t in init]
+    ref = Muon(ref_p, foreach=False, **kwargs)
+    fe = Muon(fe_p, foreach=True, **kwargs)
+    for step in range(3):
+        grads = [torch.randn(s, generator=gen).to(DEV) for s in shapes]
+        for p, g in zip(ref_p, grads):
+            p.grad = g.clone()
+        for p, g in zip(fe_p, grads):
+            p.grad = g.clone()
+        ref.step()
+        fe.step()
+        for p, g in zip(ref_p, grads):
+            assert torch.equal(p.grad, g), "per-param driver must not touch the grad"
+        for p, g in zip(fe_p, grads):
+            buf = fe.state[p]["momentum_buffer"]
+            assert torch.equal(p.grad, g + buf * 0.95) or rel_fro(p.grad, g + 0.95 * buf) < 1e-6
+    for r, f in zip(ref_p, fe_p):
+        assert torch.equal(r, f)
+
+
+def test_multi_step_trajectory_matches_oracle():
+    shapes = [(64, 32), (32, 96), (2, 48, 40)]
+    gen = torch.Generator().manual_seed(3)
+    init = [torch.randn(s, generator=gen) for s in shapes]
+    params = [nn.Parameter(t.clone().to(DEV)) for t in init]
+    opt = Muon(params, lr=0.05, wd=0.1, foreach=True)
+    ref = muon_ref.MuonRef([t.clone() for t in init], lr=0.05, wd=0.1)
+    coeffs, prescale = muon_ref.strategy_coeffs("polar_express", 5)
+
+    for _ in range(3):
+        grads = [torch.randn(s, generator=gen) for s in shapes]
+        for p, g in zip(params, grads):
+            p.grad = g.to(DEV)
+        opt.step()
+        # oracle: same arithmetic, orthogonalization at the HIP storage points
+        for i, (rp, g) in enumerate(zip(ref.params, grads)):
+            st = ref.state.setdefault(i, {
+                "step": torch.tensor(0.0), "momentum_buffer": torch.zeros_like(g),
+                "lr_ratio": torch.tensor(math.sqrt(max(1.0, g.shape[-2] / g.shape[-1])))})
+            st["step"] += 1
+            new_p, new_buf, _, _ = muon_ref.muon_update(
+                rp, g, st["momentum_buffer"], float(st["lr_ratio"]), lr=0.05, weight_decay=0.1,
+                cautious_wd=True, momentum=0.95, nesterov=True, maximize=False,
+                orth_single=lambda x: muon_ref.polar_iteration_bf16(x, coeffs, prescale=prescale,
+                                                                    eps=1e-7),
+            )
+            rp.copy_(new_p)
+            st["momentum_buffer"] = new_buf
+    for i, (p, rp, p0) in enumerate(zip(params, ref.params, init)):
+        assert rel_fro(p.detach().cpu() - p0, rp - p0) < 2e-2
+        assert torch.equal(opt.state[p]["momentum_buffer"].cpu(), ref.state[i]["momentum_buffer"])
+
+
+def test_state_dict_round_trip_continuity():
+    gen = torch.Generator().manual_seed(5)
+    init = torch.randn(48, 32, generator=gen)
+    a = nn.Parameter(init.clone().to(DEV))
+    b = nn.Parameter(init.clone().to(DEV))
+    c = nn.Parameter(init.clone().to(DEV))
+    kw = dict(lr=0.1, wd=0.1, momentum=0.5, nesterov=False)
+    oa, ob, oc = Muon([a], **kw), Muon([b], **kw), Muon([c], **kw)
+    g1 = torch.randn(48, 32, generator=gen).to(DEV)
+    a.grad, b.grad = g1.clone(), g1.clone()
+    oa.step()
+    ob.step()
+    c.data.copy_(b.data)
+    oc.load_state_dict(ob.state_dict())
+    g2 = torch.randn(48, 32, generator=gen).to(DEV)
+    a.grad, c.grad = g2.clone(), g2.clone()
+    oa.step()
+    oc.step()
+    assert torch.equal(a, c)
+    for key in ["step", "momentum_buffer", "lr_ratio"]:
+        assert torch.equal(oa.state[a][key], oc.state[c][key])
+
+
+@pytest.mark.parametrize("foreach", [True, False])
+def test_host_resident_params_round_trip_through_device(foreach):
+    gen = torch.Generator().manual_seed(6)
+    init = torch.randn(32, 16, generator=gen)
+    g = torch.randn(32, 16, generator=gen)
+    cpu_p = nn.Parameter(init.clone())
+    dev_p = nn.Parameter(init.clone().to(DEV))
+    cpu_p.grad = g.clone()
+    dev_p.grad = g.clone().to(DEV)
+    kw = dict(lr=0.1, wd=0.0, orthogonalization_strategy="newton_schulz")
+    Muon([cpu_p], foreach=foreach, **kw).step()
+    Muon([dev_p], foreach=foreach, **kw).step()
+    assert cpu_p.device.type == "cpu" and cpu_p.grad.device.type == "cpu"
+    assert torch.equal(cpu_p.detach(), dev_p.detach().cpu())
+
+
+def test_mixed_muon_and_adam_groups(monkeypatch):
+    _identity(monkeypatch)
+    mp = nn.Parameter(torch.ones(2, 2, device=DEV))
+    ap = nn.Parameter(torch.randn(3, device=DEV))
+    aref = nn.Parameter(ap.detach().clone())
+    opt = Muon([{"params": [mp], "lr": 0.1, "wd": 0.0, "momentum": 0.0},
+                {"params": [ap], "algorithm": "adamw", "lr": 0.01, "wd": 0.1, "fused": False}])
+    ref = torch.optim.AdamW([aref], lr=0.01, weight_decay=0.1)
+    mp.grad = torch.full_like(mp, 0.5)
+    ag = torch.randn_like(ap)
+    ap.grad, aref.grad = ag.clone(), ag.clone()
+    opt.step()
+    ref.step()
+    torch.testing.assert_close(mp, torch.full_like(mp, 0.95))
+    torch.testing.assert_close(ap, aref)
+
+
+# ---- NorMuon and split_sizes --------------------------------------------------------------
+
+
+@pytest.mark.parametrize("shape", [(40, 24), (24, 40), (2, 24, 40)])
+def test_normuon_matches_oracle(shape):
+    gen = torch.Generator().manual_seed(8)
+    p0 = torch.randn(shape, generator=gen)
+    p = nn.Parameter(p0.clone().to(DEV))
+    opt = Muon([{"params": [p], "algorithm": "normuon", "muon_beta2": 0.9}], lr=0.1, wd=0.1,
+               momentum=0.5, nesterov=True)
+    ref_p, ref_buf = p0.clone(), torch.zeros(shape)
+    ref_v = torch.zeros(*shape[:-1], 1)
+    for step in range(2):
+        g = torch.randn(shape, generator=gen)
+        p.grad = g.clone().to(DEV)
+        opt.step()
+        gq_buf = ref_buf * 0.5 + g
+        gq = g + gq_buf * 0.5
+        U = zeropower(gq.to(DEV), strategy="polar_express").cpu()
+        ref_p, ref_buf, ref_v, _ = muon_ref.normuon_update(
+            ref_p, g, ref_buf, ref_v, muon_ref.lr_ratio(shape), lr=0.1, weight_decay=0.1,
+            cautious_wd=True, momentum=0.5, nesterov=True, maximize=False, beta2=0.9,
+            orth_single=lambda x: U,
+        )
+    assert rel_fro(p.detach().cpu() - p0, ref_p - p0) < 1e-4
+    torch.testing.assert_close(opt.state[p]["variance_neuron"].cpu(), ref_v, rtol=1e-4, atol=1e-7)
+
+
+def test_split_sizes_match_oracle():
+    from muonium_amd.orthogonalize import foreach_zeropower
+
+    gen = torch.Generator().manual_seed(9)
+    p0 = torch.randn(96, 32, generator=gen)
+    g = torch.randn(96, 32, generator=gen)
+    p = nn.Parameter(p0.clone().to(DEV))
+    p.grad = g.clone().to(DEV)
+    opt = Muon([{"params": [p], "split_sizes": (64, 16, 16)}], lr=0.1, wd=0.0, momentum=0.0,
+               nesterov=False)
+    opt.step()
+    # oracle: base.py:73-99 block split/scale/cat with the HIP orthogonalizer per height
+    hip_batch = lambda blocks: [u.cpu() for u in foreach_zeropower([b.to(DEV) for b in blocks],
+                                                                  strategy="polar_express")]
+    ref_p, _, _, _ = muon_ref.muon_update(
+        p0, g, torch.zeros(96, 32), muon_ref.lr_ratio((96, 32)), lr=0.1, weight_decay=0.0,
+        cautious_wd=True, momentum=0.0, nesterov=False, maximize=False,
+        split_sizes=(64, 16, 16), orth_batch=hip_batch,
+    )
+    assert torch.equal(p.detach().cpu(), ref_p)
