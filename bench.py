@@ -1,0 +1,259 @@
+"""Benchmark: one full Muon optimizer.step() on the Llama-3-8B-shaped parameter set.
+
+Workload: 32 layers x {q, o 4096x4096; k, v 1024x4096;
+gate, up 14336x4096; down 4096x14336} bf16 parameters (6.98e9 values) with fp32
+momentum, synthetic gradients g = diag(exp(z)) Z (z ~ N(0,1) per row, Z ~ N(0,1)),
+Polar Express 5 steps, cautious weight decay 0.1, Nesterov 0.95, foreach batching by
+shape. A step is one optimizer.step() over the whole set; inputs are resident in HBM.
+
+Prints one JSON line: value = orthogonalization TFLOP/s of the whole step
+(symmetric-minimal FLOPs 3 m^2 n + m^3 per matrix per iteration / step time),
+ms_per_step = Muon step time, plus the roofline of the dominant kernel (the B X GEMM)
+from hipEvent timing of every launch, per-kernel breakdowns, and the CPU baseline
+(the oracle's per-parameter loop on a bounded sample, on this host's cores).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config llama|gpt2|moe]
+       [--lp 8bit|4bit|fp8] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "dtensor-muon_amd"))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+CONFIGS = {
+    # name: (layers, [(rows, cols, per-layer count)], workload label)
+    "llama": (32, [(4096, 4096, 2), (1024, 4096, 2), (14336, 4096, 2), (4096, 14336, 1)],
+              "Llama-3-8B-shaped: 32 x {q,o 4096x4096; k,v 1024x4096; gate,up 14336x4096; down 4096x14336}"),
+    "gpt2": (12, [(768, 2304, 1), (768, 768, 1), (768, 3072, 1), (3072, 768, 1)],
+             "GPT-2-small-shaped: 12 x {768x2304, 768x768, 768x3072, 3072x768}"),
+    "moe": (16, [(64 * 1408, 2048, 0)], "MoE: 16 x {gate, up (64,1408,2048), down (64,2048,1408)}"),
+}
+
+
+def _shapes(config: str):
+    layers, per_layer, _ = CONFIGS[config]
+    if config == "moe":
+        return [(64, 1408, 2048)] * (2 * layers) + [(64, 2048, 1408)] * layers
+    out = []
+    for _ in range(layers):
+        for r, c, n in per_layer:
+            out += [(r, c)] * n
+    return out
+
+
+def orth_flops(shape, steps: int) -> float:
+    """Symmetric-minimal FLOPs of the iteration for one tensor: per matrix and step
+    m(m+1) n [X X^T] + m(m+1) m [A A] + 2 m^2 n [B X]."""
+    nb = 1
+    for d in shape[:-2]:
+        nb *= d
+    m, n = min(shape[-2:]), max(shape[-2:])
+    return nb * steps * (m * (m + 1) * n + m * (m + 1) * m + 2 * m * m * n)
+
+
+def cpu_baseline(max_seconds: float = 20.0) -> dict:
+    """The reference's per-parameter loop restated on the CPU (oracle.muon_ref), on a
+    bounded sample: k/v-shaped 1024x4096 bf16 steps (Polar Express 5), timed until
+    ~max_seconds of work; reported as the sample's orthogonalization TFLOP/s."""
+    import torch
+
+    from oracle import muon_ref
+
+    threads = len(os.sched_getaffinity(0))
+    threads = min(threads, int(os.environ.get("OMP_NUM_THREADS", threads)))
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(0)
+    shape = (1024, 4096)
+    p = torch.randn(shape, generator=gen).bfloat16()
+    ref = muon_ref.MuonRef([p], lr=1e-3, wd=0.1, strategy="polar_express")
+    g = (torch.randn(shape, generator=gen) * torch.exp(torch.randn(shape[0], 1, generator=gen))).bfloat16()
+    ref.step([g])  # warm-up
+    times = []
+    t_all = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_all < max_seconds and len(times) < 20):
+        t0 = time.perf_counter()
+        ref.step([g])
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_all > max_seconds and len(times) >= 1:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    flops = orth_flops(shape, 5)
+    try:
+        cpu = open("/proc/cpuinfo").read().split("model name")[1].split("\n")[0].strip(" :\t")
+    except Exception:
+        cpu = "unknown"
+    return {
+        "value": round(flops / med / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle per-parameter Muon step (bf16 Polar Express 5, cautious wd) on one "
+                   f"1024x4096 bf16 matrix, median of {len(times)} steps = {med * 1e3:.1f} ms; "
+                   f"CPU: {cpu}"),
+    }
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="llama", choices=sorted(CONFIGS))
+    ap.add_argument("--lp", default=None, choices=["8bit", "4bit", "fp8"])
+    ap.add_argument("--block-size", type=int, default=None)
+    ap.add_argument("--strategy", default=None)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build targets one GPU (no collectives); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from muonium_amd import Muon, _lib
+    from muonium_amd.optim import Muon4bit, Muon8bit, MuonFp8
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    shapes = _shapes(args.config)
+    strategy = args.strategy or ("newton_schulz" if args.config == "moe" else "polar_express")
+    print(f"[bench] config={args.config} tensors={len(shapes)} strategy={strategy} "
+          f"lp={args.lp}", file=sys.stderr, flush=True)
+
+    gen = torch.Generator(device=dev).manual_seed(0)
+    params = []
+    for s in shapes:
+        p = torch.empty(s, dtype=torch.bfloat16, device=dev)
+        p.normal_(0.0, 0.02, generator=gen)
+        q = torch.nn.Parameter(p)
+        rows = s[-2]
+        z = torch.randn(*s[:-2], rows, 1, device=dev, generator=gen)
+        g = torch.randn(s, device=dev, generator=gen) * torch.exp(z)
+        q.grad = g.to(torch.bfloat16)
+        del g, z
+        params.append(q)
+    numel = sum(p.numel() for p in params)
+    kw = dict(lr=1e-3, wd=0.1, use_cautious_wd=True, momentum=0.95, nesterov=True, ns_steps=5,
+              orthogonalization_strategy=strategy)
+    if args.lp:
+        cls = {"8bit": Muon8bit, "4bit": Muon4bit, "fp8": MuonFp8}[args.lp]
+        block = args.block_size or {"8bit": 256, "4bit": 128, "fp8": 256}[args.lp]
+        opt = cls(params, foreach=True, block_size=block, **kw)
+    else:
+        opt = Muon(params, foreach=True, **kw)
+    torch.cuda.synchronize()
+    print(f"[bench] params={numel / 1e9:.3f}e9, warmup {args.warmup}", file=sys.stderr, flush=True)
+
+    for i in range(args.warmup):
+        opt.step()
+        torch.cuda.synchronize()
+        print(f"[bench] warmup step {i} done", file=sys.stderr, flush=True)
+
+    _lib.timing_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(args.steps):
+        opt.step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern = _lib.timing_read()
+    _lib.timing_enable(False)
+    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    print(f"[bench] {args.steps} steps: {ms_per_step:.2f} ms/step (wall {wall:.2f}s)",
+          file=sys.stderr, flush=True)
+
+    flops_step = sum(orth_flops(s, 5) for s in shapes)
+    value = flops_step / (ms_per_step * 1e-3) / 1e12
+    orth_ms = sum(kern[k][0] for k in ("syrk_xx", "syrk_aa", "gemm_bx")) / args.steps
+    kernels = {}
+    for k, (ms, n, work) in kern.items():
+        if n == 0:
+            continue
+        entry = {"ms_per_step": round(ms / args.steps, 3), "launches_per_step": n // args.steps,
+                 "avg_launch_ms": round(ms / n, 4)}
+        if k in ("syrk_xx", "syrk_aa", "gemm_bx"):
+            tf = work / (ms * 1e-3) / 1e12
+            entry.update(tflops=round(tf, 1), frac=round(tf / PEAK_BF16_TFLOPS, 4))
+        elif k in ("prepass", "postpass", "lp_prepass"):
+            gbs = work / (ms * 1e-3) / 1e9
+            entry.update(gbs=round(gbs, 1), frac=round(gbs / PEAK_HBM_GBS, 4))
+        kernels[k] = entry
+
+    gms, gn, gwork = kern["gemm_bx"]
+    avg_ms = gms / max(gn, 1)
+    achieved = (gwork / max(gn, 1)) / (avg_ms * 1e-3) / 1e12
+    roofline = {
+        "bound": "mfma",
+        "kernel": "gemm_bf16_kernel<MODE_GEMM> (X' = a X + B X)",
+        "achieved": round(achieved, 1),
+        "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+        "traffic": None,
+        "avg_launch_ms": round(avg_ms, 4),
+        "flop_per_launch": gwork / max(gn, 1),
+    }
+    upd_ms = sum(kern[k][0] for k in ("prepass", "postpass", "lp_prepass")) / args.steps
+    upd_bytes = sum(kern[k][2] for k in ("prepass", "postpass", "lp_prepass")) / args.steps
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
+        cpu = cpu_baseline()
+
+    _, _, label = CONFIGS[args.config]
+    line = {
+        "metric": "Muon step ms + orthogonalization TFLOP/s, Llama-3-8B-shaped params, 1 GPU",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) gradients with per-row log-normal scales; random-init bf16 params)",
+        "config": {
+            "workload": label + (f"; MuonLP {args.lp}" if args.lp else ""),
+            "params": numel,
+            "strategy": strategy,
+            "ns_steps": 5,
+            "foreach": True,
+            "momentum_dtype": (args.lp or "fp32"),
+            "orth_tflop_per_step": round(flops_step / 1e12, 3),
+        },
+        "orth_kernel_ms_per_step": round(orth_ms, 3),
+        "orth_kernel_tflops": round(flops_step / (orth_ms * 1e-3) / 1e12, 1) if orth_ms else None,
+        "update_kernel_ms_per_step": round(upd_ms, 3),
+        "update_kernel_gbs": round(upd_bytes / (upd_ms * 1e-3) / 1e9, 1) if upd_ms else None,
+        "kernels": kernels,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -5,6 +5,8 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
+#include <vector>
 
 #include "common.h"
 
@@ -49,6 +51,59 @@ void muon_set_error(const char* fmt, ...) {
   vsnprintf(g_err, sizeof(g_err), fmt, ap);
   va_end(ap);
 }
+
+// ---- kernel timing (muon_timing_*) -------------------------------------------------
+namespace {
+struct TimingRec {
+  int kind;
+  double work;
+  hipEvent_t ev0, ev1;
+};
+struct TimingState {
+  std::mutex mu;
+  bool on = false;
+  std::vector<hipEvent_t> free_events;
+  std::vector<TimingRec> recs;
+};
+TimingState g_timing;
+const size_t kMaxTimedLaunches = 65536;
+
+hipEvent_t take_event() {
+  if (!g_timing.free_events.empty()) {
+    hipEvent_t e = g_timing.free_events.back();
+    g_timing.free_events.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Brackets the launches made during its lifetime with events on `s` when timing is on.
+class Timed {
+ public:
+  Timed(int kind, double work, hipStream_t s) : kind_(kind), work_(work), s_(s) {
+    if (!g_timing.on) return;
+    std::lock_guard<std::mutex> lock(g_timing.mu);
+    if (g_timing.recs.size() >= kMaxTimedLaunches) return;
+    ev0_ = take_event();
+    ev1_ = take_event();
+    if (ev0_ && ev1_ && hipEventRecord(ev0_, s_) != hipSuccess) ev0_ = nullptr;
+  }
+  ~Timed() {
+    if (!ev0_ || !ev1_) return;
+    if (hipEventRecord(ev1_, s_) != hipSuccess) return;
+    std::lock_guard<std::mutex> lock(g_timing.mu);
+    g_timing.recs.push_back({kind_, work_, ev0_, ev1_});
+  }
+
+ private:
+  int kind_;
+  double work_;
+  hipStream_t s_;
+  hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
+};
+}  // namespace
 
 // Padding granule of the workspace extents: the bf16 tile (256); fp32 tiles (128)
 // divide it.
@@ -191,6 +246,9 @@ int muon_prepass(int ntensors, void* const* grads, void* const* bufs, int g_dtyp
     return MUON_ERR_SHAPE;
   }
   OrthLayout L = muon_orth_layout(ws_dtype, ws_batch, rows, cols);
+  const int ges = g_dtype == MUON_DT_F32 ? 4 : 2, bes = buf_dtype == MUON_DT_F32 ? 4 : 2;
+  const double per_elem = ges + (bufs ? 2.0 * bes : 0.0) + L.es + (write_back_grad ? ges : 0);
+  Timed timed(MUON_K_PREPASS, per_elem * (double)ntensors * nb * rows * cols, s);
   for (int t0 = 0; t0 < ntensors; t0 += MUON_MAX_TENSORS) {
     const int cnt = std::min(MUON_MAX_TENSORS, ntensors - t0);
     int rc = muon_launch_prepass(cnt, grads + t0, bufs ? bufs + t0 : nullptr, g_dtype,
@@ -219,7 +277,11 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
   OrthLayout L = muon_orth_layout(ws_dtype, ws_batch, rows, cols);
   hipStream_t s = (hipStream_t)stream;
   char* w = (char*)ws;
-  int rc = muon_launch_finalize(L, ws, batch, prescale, eps, s);
+  int rc;
+  {
+    Timed t(MUON_K_OTHER, 0.0, s);
+    rc = muon_launch_finalize(L, ws, batch, prescale, eps, s);
+  }
   if (rc != MUON_OK) return rc;
   const float* scale = (const float*)(w + L.off_scale);
   char* X = w + L.off_x;
@@ -227,28 +289,41 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
   char* A = w + L.off_a;
   char* B = w + L.off_b;
   const int64_t mp = L.m_pad, np = L.n_pad;
-  if (steps == 0) return muon_launch_scale(L, L.tall ? XT[0] : X, ws_dtype, batch, scale, s);
+  if (steps == 0) {
+    Timed t(MUON_K_OTHER, 0.0, s);
+    return muon_launch_scale(L, L.tall ? XT[0] : X, ws_dtype, batch, scale, s);
+  }
+  const double bm = (double)batch, md = (double)L.m, nd = (double)L.n;
   for (int it = 0; it < steps; ++it) {
     const float a = (float)coeffs[3 * it], b = (float)coeffs[3 * it + 1],
                 c = (float)coeffs[3 * it + 2];
     const bool first = it == 0, last = it == steps - 1;
     // A = X X^T (the first iteration folds the Frobenius prescale s in as s^2)
+    {
+    Timed t(MUON_K_SYRK_XX, bm * md * (md + 1) * nd, s);
     rc = muon_launch_gemm(ws_dtype, MODE_SYRK, false, batch, mp, mp, np, X, np, mp * np, X, np,
                           mp * np, nullptr, 0, 0, A, mp, mp * mp, nullptr, 0, 0, L.m, L.m, 1.0f,
                           0.0f, scale, first ? 2 : 0, s);
+    }
     if (rc != MUON_OK) return rc;
     // B = b*A + c*(A A)
+    {
+    Timed t(MUON_K_SYRK_AA, bm * md * (md + 1) * md, s);
     rc = muon_launch_gemm(ws_dtype, MODE_SYRK, false, batch, mp, mp, mp, A, mp, mp * mp, A, mp,
                           mp * mp, A, mp, mp * mp, B, mp, mp * mp, nullptr, 0, 0, L.m, L.m, c, b,
                           nullptr, 0, s);
+    }
     if (rc != MUON_OK) return rc;
     // X' = a*X + B X, as B(i, k) . X^T(j, k); X is updated in place (its elements are
     // only touched by the epilogue of their own tile), X^T ping-pongs.
     void* out = (last && L.tall) ? nullptr : (void*)X;
     void* out_t = (last && !L.tall) ? nullptr : (void*)XT[(it + 1) & 1];
+    {
+    Timed t(MUON_K_GEMM_BX, bm * 2.0 * md * md * nd, s);
     rc = muon_launch_gemm(ws_dtype, MODE_GEMM, false, batch, mp, np, mp, B, mp, mp * mp,
                           XT[it & 1], mp, np * mp, X, np, mp * np, out, np, mp * np, out_t, mp,
                           np * mp, L.m, L.n, 1.0f, a, scale, first ? 1 : 0, s);
+    }
     if (rc != MUON_OK) return rc;
   }
   return MUON_OK;
@@ -309,7 +384,9 @@ int muon_postpass(int ntensors, void* const* params, int p_dtype, const void* u,
     udt = ws_dtype;
   }
   const int es = udt == MUON_DT_F32 ? 4 : 2;
+  const int pes = p_dtype == MUON_DT_F32 ? 4 : 2;
   hipStream_t s = (hipStream_t)stream;
+  Timed timed(MUON_K_POSTPASS, (es + 2.0 * pes) * (double)ntensors * nb * rows * cols, s);
   for (int t0 = 0; t0 < ntensors; t0 += MUON_MAX_TENSORS) {
     const int cnt = std::min(MUON_MAX_TENSORS, ntensors - t0);
     int rc = muon_launch_postpass(cnt, params + t0, adjusted_lrs + t0, p_dtype,
@@ -344,6 +421,11 @@ int muon_lp_prepass(int ntensors, void* const* grads, int g_dtype, void* const* 
   char* direct = w + (L.tall ? L.off_xt0 : L.off_x);
   const int64_t d_pitch = L.tall ? L.m_pad : L.n_pad;
   const int64_t mst = L.m_pad * L.n_pad;
+  {
+  const double ges = g_dtype == MUON_DT_F32 ? 4.0 : 2.0;
+  const double code_b = qformat == MUON_Q_4BIT ? 0.5 : 1.0;
+  const double per_elem = ges + 2.0 * code_b + 8.0 / (double)block + 2.0;
+  Timed timed(MUON_K_LP_PREPASS, per_elem * (double)ntensors * nb * rows * cols, s);
   for (int t0 = 0; t0 < ntensors; t0 += MUON_MAX_TENSORS) {
     const int cnt = std::min(MUON_MAX_TENSORS, ntensors - t0);
     rc = muon_launch_lp_prepass(cnt, grads + t0, g_dtype, codes + t0, scales + t0, qmap,
@@ -351,6 +433,8 @@ int muon_lp_prepass(int ntensors, void* const* grads, int g_dtype, void* const* 
                                 direct + (int64_t)t0 * nb * mst * L.es, d_pitch, mst, s);
     if (rc != MUON_OK) return rc;
   }
+  }
+  Timed timed_t(MUON_K_OTHER, 0.0, s);
   // Second layout and norm partials from the stored-layout X just written: a plain
   // (no momentum) prepass that reads the valid region of the workspace itself and
   // rewrites only its padding.
@@ -362,6 +446,41 @@ int muon_lp_prepass(int ntensors, void* const* grads, int g_dtype, void* const* 
     rc = muon_launch_prepass(cnt, srcs, nullptr, MUON_DT_BF16, MUON_DT_BF16, 1, rows, cols,
                              d_pitch, mst, 0.0f, 0, 0, 0, 2, L, ws, ws_dtype, m0, s);
     if (rc != MUON_OK) return rc;
+  }
+  return MUON_OK;
+}
+
+int muon_timing_enable(int on) {
+  std::lock_guard<std::mutex> lock(g_timing.mu);
+  for (auto& r : g_timing.recs) {
+    g_timing.free_events.push_back(r.ev0);
+    g_timing.free_events.push_back(r.ev1);
+  }
+  g_timing.recs.clear();
+  g_timing.on = on != 0;
+  return MUON_OK;
+}
+
+int muon_timing_read(double* ms, int64_t* launches, double* work) {
+  std::lock_guard<std::mutex> lock(g_timing.mu);
+  for (int k = 0; k < MUON_K_COUNT; ++k) {
+    ms[k] = 0.0;
+    launches[k] = 0;
+    work[k] = 0.0;
+  }
+  for (auto& r : g_timing.recs) {
+    if (hipEventSynchronize(r.ev1) != hipSuccess) {
+      muon_set_error("timing: hipEventSynchronize failed");
+      return MUON_ERR_DEVICE;
+    }
+    float t = 0.0f;
+    if (hipEventElapsedTime(&t, r.ev0, r.ev1) != hipSuccess) {
+      muon_set_error("timing: hipEventElapsedTime failed");
+      return MUON_ERR_DEVICE;
+    }
+    ms[r.kind] += t;
+    launches[r.kind] += 1;
+    work[r.kind] += r.work;
   }
   return MUON_OK;
 }

@@ -193,7 +193,9 @@ MUON_DEVICE float apply_elem(float p, float u, float wd, int cautious, float adj
     float step = adj * v;
     return p - step;
   }
-  float step = Elem<UDT>::round(adj * u);  // 0-dim fp32 * u keeps u's dtype
+  // 0-dim fp32 tensor * u: type promotion keeps u's dtype, so the scalar is cast to
+  // it first and the product is rounded to it (eager torch semantics).
+  float step = Elem<UDT>::round(Elem<UDT>::round(adj) * u);
   return p - step;
 }
 

@@ -58,6 +58,11 @@ _SIGNATURES = {
     ),
     "muon_lp_quantize": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp]),
     "muon_lp_dequantize": (_c_int, [_vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _vp]),
+    "muon_timing_enable": (_c_int, [_c_int]),
+    "muon_timing_read": (
+        _c_int,
+        [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_i64), ctypes.POINTER(ctypes.c_double)],
+    ),
     "muon_lp_prepass": (
         _c_int,
         [_c_int, _pp, _c_int, _pp, _pp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32,
@@ -123,6 +128,24 @@ def ensure_device(device: torch.device) -> None:
     with torch.cuda.device(idx):
         check(lib.muon_amd_init(), "muon_amd_init")
     _initialized_devices.add(idx)
+
+
+KERNEL_KINDS = ("syrk_xx", "syrk_aa", "gemm_bx", "prepass", "postpass", "lp_prepass", "other")
+
+
+def timing_enable(on: bool) -> None:
+    """Bracket every launch of the step entry points with hipEvents (or stop)."""
+    check(load().muon_timing_enable(int(on)), "muon_timing_enable")
+
+
+def timing_read() -> dict[str, tuple[float, int, float]]:
+    """{kind: (total ms, launches, algorithmic work)} since timing was enabled."""
+    n = len(KERNEL_KINDS)
+    ms = (ctypes.c_double * n)()
+    cnt = (ctypes.c_int64 * n)()
+    work = (ctypes.c_double * n)()
+    check(load().muon_timing_read(ms, cnt, work), "muon_timing_read")
+    return {k: (ms[i], cnt[i], work[i]) for i, k in enumerate(KERNEL_KINDS)}
 
 
 def dtype_code(dtype: torch.dtype) -> int:

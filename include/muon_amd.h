@@ -92,6 +92,8 @@ int muon_orth_result(int dtype, int64_t batch, int64_t rows, int64_t cols, int s
  * write_back_grad stores g' into grad (the foreach driver's in-place Nesterov
  * update of the gradient list, muon.py:117-118). The sum of squares of the cast
  * values is accumulated per matrix for the Frobenius prescale (polar_express.py:89).
+ * With ws == NULL only the momentum step runs (buf' in place, g' into grad when
+ * write_back_grad): for a caller-supplied orthogonalizer that needs g' as a tensor.
  * Replaces: muonium/optim/algorithms/muon.py:39-56 and :108-119, plus the
  * `torch.stack(...).bfloat16()` of orthogonalize.py:159-161. */
 int muon_prepass(int ntensors, void* const* grads, void* const* bufs, int g_dtype,
@@ -122,8 +124,9 @@ int muon_orth_extract(const void* ws, int ws_dtype, int64_t ws_batch, int64_t ba
  * contiguous tensor u of u_dtype holding ntensors*nb*rows*cols elements):
  *   v = wd != 0 ? (cautious ? u + (wd*p)*(u*p > 0) : u + wd*p) : u    (muon.py:62-69)
  *   p = round(p - adjusted_lrs[t] * v)                                 (muon.py:71-77)
- * in fp32 with no contraction; when wd == 0 the product adjusted_lr*u is rounded to
- * u's dtype first (eager type promotion of a 0-dim fp32 tensor times a bf16 tensor).
+ * in fp32 with no contraction; when wd == 0 the product adjusted_lr*u keeps u's dtype
+ * (eager type promotion of a 0-dim fp32 tensor times a bf16 tensor: adjusted_lr is cast
+ * to u's dtype, the product rounded to it).
  * Replaces: muonium/optim/algorithms/muon.py:59-77 and :121-140. */
 int muon_postpass(int ntensors, void* const* params, int p_dtype, const void* u, int u_dtype,
                   const void* ws, int ws_dtype, int64_t ws_batch, int steps, int64_t nb,
@@ -152,6 +155,23 @@ int muon_lp_prepass(int ntensors, void* const* grads, int g_dtype, void* const* 
                     void* const* scales, const float* qmap, int qformat, int64_t block,
                     int64_t nb, int64_t rows, int64_t cols, float momentum, int nesterov,
                     int maximize, void* ws, int ws_dtype, int64_t ws_batch, void* stream);
+
+/* ---- Kernel timing (measurement support) ------------------------------------------
+ * No counterpart in the reference. While enabled, every kernel the step entry points
+ * launch is bracketed by hipEvents on its own stream; muon_timing_read() waits for
+ * the last event and returns, per kernel kind (MUON_K_*), the summed duration in ms,
+ * the launch count and the summed algorithmic work (FLOP for the products, bytes for
+ * the elementwise passes, as documented per kind). Capacity: 65536 launches. */
+#define MUON_K_SYRK_XX 0   /* A = X X^T: m(m+1) n FLOP per matrix (upper triangle) */
+#define MUON_K_SYRK_AA 1   /* B = b A + c A A: m(m+1) m FLOP per matrix */
+#define MUON_K_GEMM_BX 2   /* X = a X + B X: 2 m^2 n FLOP per matrix */
+#define MUON_K_PREPASS 3   /* bytes: grad + 2 * buffer + one bf16 X per element */
+#define MUON_K_POSTPASS 4  /* bytes: u + 2 * param per element */
+#define MUON_K_LP_PREPASS 5 /* bytes: grad + 2 * codes + 2 * scales + one bf16 X */
+#define MUON_K_OTHER 6     /* finalize / transpose / scale / extract (no work counted) */
+#define MUON_K_COUNT 7
+int muon_timing_enable(int on);
+int muon_timing_read(double* ms, int64_t* launches, double* work);
 
 #ifdef __cplusplus
 }

@@ -21,7 +21,7 @@ from oracle import muon_ref
 pytestmark = pytest.mark.gpu
 
 BF16_TOL = 1e-2   # HIP bf16 vs the oracle at the same storage points
-FP64_TOL = 2e-2   # HIP bf16 vs the exact (fp64) iteration
+FP64_SLACK = 1.25  # HIP bf16 vs fp64: within 1.25x the fused-bf16 oracle's own distance
 TRITON_TOL = 4e-2  # HIP bf16 vs the reference's pe_loop_triton rounding points
 FP32_TOL = 1e-5   # HIP fp32 iteration vs the fp64 iteration (non-square inputs)
 FP32_TOL_SQUARE = 3e-5  # square Gaussian inputs: the fp32 iteration itself is ~1.3e-5 off
@@ -47,7 +47,8 @@ def test_bf16_iteration_matches_oracle(shape, steps, strategy):
     ref = muon_ref.polar_iteration_bf16(X, coeffs, prescale=prescale, eps=1e-7)
     assert rel_fro(got, ref) <= BF16_TOL, f"vs fused-bf16 oracle {rel_fro(got, ref):.3e}"
     exact = muon_ref.polar_iteration(X.bfloat16().double(), coeffs, prescale=prescale, eps=1e-7)
-    assert rel_fro(got, exact) <= FP64_TOL, f"vs fp64 {rel_fro(got, exact):.3e}"
+    bound = FP64_SLACK * rel_fro(ref, exact) + 2e-3
+    assert rel_fro(got, exact) <= bound, f"vs fp64 {rel_fro(got, exact):.3e} > {bound:.3e}"
     tri = muon_ref.polar_iteration_bf16(X, coeffs, prescale=prescale, eps=1e-7, rounding="triton")
     assert rel_fro(got, tri) <= TRITON_TOL, f"vs triton rounding {rel_fro(got, tri):.3e}"
 

@@ -16,7 +16,7 @@ import torch
 import torch.nn as nn
 
 import muonium_amd.optim.algorithms.base as algo_base
-from helpers import rel_fro
+from helpers import assert_close_pct, rel_fro
 from muonium_amd import Muon
 from muonium_amd.orthogonalize import zeropower
 from oracle import muon_ref
@@ -216,7 +216,14 @@ def test_fused_step_matches_oracle_update(case, hp):
     ref_p, _, _, _ = _oracle_step(p0, g0, buf0, hp, orth=orth)
     d_got = p.detach().cpu().double() - p0.double()
     d_ref = ref_p.double() - p0.double()
-    assert rel_fro(d_got, d_ref) <= 2e-2
+    if hp["use_cautious_wd"] and hp["wd"] != 0:
+        # the cautious mask [u*p > 0] is discrete: elements with u near 0 may flip, so
+        # compare elementwise with a mismatch budget (the reference's foreach-vs-per-param
+        # bar, test_optim_foreach.py:64-66)
+        assert_close_pct(d_got, d_ref, rtol=1e-2, atol=3e-2 * d_ref.abs().max().item(),
+                         max_mismatch_pct=5.0)
+    else:
+        assert rel_fro(d_got, d_ref) <= 2e-2
 
 
 def test_foreach_equals_per_param_and_mutates_grads_under_nesterov():
@@ -299,7 +306,8 @@ def test_state_dict_round_trip_continuity():
     oc.step()
     assert torch.equal(a, c)
     for key in ["step", "momentum_buffer", "lr_ratio"]:
-        assert torch.equal(oa.state[a][key], oc.state[c][key])
+        # torch's load_state_dict moves non-"step" state to the param's device
+        assert torch.equal(oa.state[a][key].cpu(), oc.state[c][key].cpu())
 
 
 @pytest.mark.parametrize("foreach", [True, False])
