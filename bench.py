@@ -63,10 +63,13 @@ def orth_flops(shape, steps: int) -> float:
     return nb * steps * (m * (m + 1) * n + m * (m + 1) * m + 2 * m * m * n)
 
 
-def cpu_baseline(max_seconds: float = 20.0) -> dict:
+def cpu_baseline(config: str = "llama", min_seconds: float = 10.0) -> dict:
     """The reference's per-parameter loop restated on the CPU (oracle.muon_ref), on a
-    bounded sample: k/v-shaped 1024x4096 bf16 steps (Polar Express 5), timed until
-    ~max_seconds of work; reported as the sample's orthogonalization TFLOP/s."""
+    bounded sample: steps of ONE matrix of each distinct shape of the workload (bf16
+    Polar Express 5, cautious wd, Nesterov), whole passes over the shapes until at
+    least min_seconds (10-30 s of CPU work on the bench host). Reported
+    as the sample's orthogonalization TFLOP/s, plus the full-step time extrapolated
+    by weighting each shape's time with its count in the workload."""
     import torch
 
     from oracle import muon_ref
@@ -75,34 +78,49 @@ def cpu_baseline(max_seconds: float = 20.0) -> dict:
     threads = min(threads, int(os.environ.get("OMP_NUM_THREADS", threads)))
     torch.set_num_threads(threads)
     gen = torch.Generator().manual_seed(0)
-    shape = (1024, 4096)
-    p = torch.randn(shape, generator=gen).bfloat16()
-    ref = muon_ref.MuonRef([p], lr=1e-3, wd=0.1, strategy="polar_express")
-    g = (torch.randn(shape, generator=gen) * torch.exp(torch.randn(shape[0], 1, generator=gen))).bfloat16()
-    ref.step([g])  # warm-up
-    times = []
-    t_all = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - t_all < max_seconds and len(times) < 20):
-        t0 = time.perf_counter()
-        ref.step([g])
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_all > max_seconds and len(times) >= 1:
-            break
-    times.sort()
-    med = times[len(times) // 2]
-    flops = orth_flops(shape, 5)
+    shapes = _shapes(config)
+    counts: dict[tuple, int] = {}
+    for s in shapes:  # a stacked (experts, rows, cols) tensor counts as its matrices
+        key = tuple(s[-2:])
+        counts[key] = counts.get(key, 0) + math.prod(s[:-2])
+    warm = torch.randn(256, 512, generator=gen).bfloat16()
+    muon_ref.MuonRef([warm], lr=1e-3, wd=0.1, strategy="polar_express").step([warm.clone()])
+    cases = []
+    for shape in counts:
+        p = torch.randn(shape, generator=gen).bfloat16()
+        z = torch.randn(*shape[:-1], 1, generator=gen)
+        g = (torch.randn(shape, generator=gen) * torch.exp(z)).bfloat16()
+        cases.append((shape, muon_ref.MuonRef([p], lr=1e-3, wd=0.1, strategy="polar_express"), g))
+    # Whole passes over the distinct shapes until at least min_seconds of CPU work.
+    per_shape = {shape: [] for shape in counts}
+    total_s, total_flops, passes = 0.0, 0.0, 0
+    while passes < 1 or (total_s < min_seconds and passes < 10):
+        for shape, ref, g in cases:
+            t0 = time.perf_counter()
+            ref.step([g])
+            dt = time.perf_counter() - t0
+            per_shape[shape].append(dt)
+            total_s += dt
+            total_flops += orth_flops(shape, 5)
+        passes += 1
+    full_s, parts = 0.0, []
+    for shape, count in counts.items():
+        mean = sum(per_shape[shape]) / len(per_shape[shape])
+        full_s += mean * count
+        parts.append(f"{'x'.join(map(str, shape))}: {mean * 1e3:.0f} ms")
     try:
         cpu = open("/proc/cpuinfo").read().split("model name")[1].split("\n")[0].strip(" :\t")
     except Exception:
         cpu = "unknown"
     return {
-        "value": round(flops / med / 1e12, 6),
+        "value": round(total_flops / total_s / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle per-parameter Muon step (bf16 Polar Express 5, cautious wd) on one "
-                   f"1024x4096 bf16 matrix, median of {len(times)} steps = {med * 1e3:.1f} ms; "
-                   f"CPU: {cpu}"),
+        "sample": (f"oracle per-parameter Muon step (bf16 Polar Express 5, cautious wd, "
+                   f"Nesterov) on one bf16 matrix of each distinct shape, {passes} passes "
+                   f"({'; '.join(parts)} mean per step; {total_s:.1f} s); CPU: {cpu}"),
+        "extrapolated_ms_per_step": round(full_s * 1e3, 1),
     }
 
 
@@ -219,7 +237,7 @@ def main() -> None:
     cpu = None
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
-        cpu = cpu_baseline()
+        cpu = cpu_baseline(args.config)
 
     _, _, label = CONFIGS[args.config]
     line = {

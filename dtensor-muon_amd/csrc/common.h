@@ -67,6 +67,62 @@ struct Elem<MUON_DT_F16> {
   static MUON_DEVICE float round(float v) { return f16_to_f32(f32_to_f16(v)); }
 };
 
+// Eight consecutive elements as floats through one or two 16-byte accesses. The
+// caller guarantees 16-byte alignment of element i.
+template <int DT>
+struct Vec8;
+template <>
+struct Vec8<MUON_DT_F32> {
+  static MUON_DEVICE void load(const void* p, int64_t i, float (&v)[8]) {
+    const float4 a = ((const float4*)((const float*)p + i))[0];
+    const float4 b = ((const float4*)((const float*)p + i))[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  static MUON_DEVICE void store(void* p, int64_t i, const float (&v)[8]) {
+    ((float4*)((float*)p + i))[0] = make_float4(v[0], v[1], v[2], v[3]);
+    ((float4*)((float*)p + i))[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+};
+template <>
+struct Vec8<MUON_DT_BF16> {
+  static MUON_DEVICE void load(const void* p, int64_t i, float (&v)[8]) {
+    const uint4 w = *(const uint4*)((const bf16_t*)p + i);
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[2 * k] = bf16_to_f32((bf16_t)(u[k] & 0xffffu));
+      v[2 * k + 1] = bf16_to_f32((bf16_t)(u[k] >> 16));
+    }
+  }
+  static MUON_DEVICE void store(void* p, int64_t i, const float (&v)[8]) {
+    uint32_t u[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      u[k] = (uint32_t)f32_to_bf16(v[2 * k]) | ((uint32_t)f32_to_bf16(v[2 * k + 1]) << 16);
+    *(uint4*)((bf16_t*)p + i) = make_uint4(u[0], u[1], u[2], u[3]);
+  }
+};
+template <>
+struct Vec8<MUON_DT_F16> {
+  static MUON_DEVICE void load(const void* p, int64_t i, float (&v)[8]) {
+    const uint4 w = *(const uint4*)((const uint16_t*)p + i);
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[2 * k] = f16_to_f32((uint16_t)(u[k] & 0xffffu));
+      v[2 * k + 1] = f16_to_f32((uint16_t)(u[k] >> 16));
+    }
+  }
+  static MUON_DEVICE void store(void* p, int64_t i, const float (&v)[8]) {
+    uint32_t u[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      u[k] = (uint32_t)f32_to_f16(v[2 * k]) | ((uint32_t)f32_to_f16(v[2 * k + 1]) << 16);
+    *(uint4*)((uint16_t*)p + i) = make_uint4(u[0], u[1], u[2], u[3]);
+  }
+};
+
 // fp32 -> float8_e4m3fn (bias 7, no infinities, 0x7f/0xff are NaN, max 448).
 // Written from the format definition: exact round-to-nearest-even onto the e4m3fn
 // grid; a magnitude that rounds above 448 becomes NaN (matching torch's cast).

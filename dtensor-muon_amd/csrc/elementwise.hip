@@ -67,6 +67,71 @@ __global__ __launch_bounds__(256) void prepass_kernel(PrepassArgs a) {
   constexpr int TPR = TILE / VEC;          // threads per row
   constexpr int RPP = 256 / TPR;           // rows per pass
   const int cl = (tid % TPR) * VEC;
+  if constexpr (VEC == 8) {
+    // 16-byte accesses: the host guarantees cols % 8 == 0, a pitch multiple of 8 and
+    // 16-byte aligned tensors, so each 8-column chunk is wholly valid or wholly padding
+#pragma unroll
+    for (int rp = 0; rp < TILE / RPP; ++rp) {
+      const int rl = rp * RPP + tid / TPR;
+      const int64_t r = r0 + rl;
+      const int64_t c = c0 + cl;
+      const bool valid = r < a.rows && c < a.cols;
+      float xv[8];
+      if (valid) {
+        const int64_t idx = base + r * a.s_pitch + c;
+        float g[8];
+        Vec8<GDT>::load(gp, idx, g);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (a.maximize) g[e] = -g[e];
+        float gq[8];
+        if (a.has_buf) {
+          float b[8], nb[8];
+          Vec8<BDT>::load(bp, idx, b);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float m = b[e] * a.momentum;
+            nb[e] = m + g[e];
+          }
+          Vec8<BDT>::store(bp, idx, nb);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            if (a.nesterov) {
+              float tt = nb[e] * a.momentum;
+              gq[e] = g[e] + tt;
+            } else {
+              gq[e] = nb[e];
+            }
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) gq[e] = g[e];
+        }
+        if (a.write_grad) Vec8<GDT>::store(gp, idx, gq);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          xv[e] = Elem<WDT>::round(gq[e]);
+          ss += xv[e] * xv[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[e] = 0.0f;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tile[rl][cl + e] = xv[e];
+      if (a.write_direct == 1 || (a.write_direct == 2 && !valid))
+        Vec8<WDT>::store(a.direct, (int64_t)mat * a.d_mstride + r * a.d_pitch + c, xv);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rp = 0; rp < TILE / RPP; ++rp) {
+      const int cc = rp * RPP + tid / TPR;
+      float tv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tv[e] = tile[cl + e][cc];
+      Vec8<WDT>::store(a.trans, (int64_t)mat * a.t_mstride + (c0 + cc) * a.t_pitch + r0 + cl, tv);
+    }
+  } else {
 #pragma unroll
   for (int rp = 0; rp < TILE / RPP; ++rp) {
     const int rl = rp * RPP + tid / TPR;
@@ -103,6 +168,7 @@ __global__ __launch_bounds__(256) void prepass_kernel(PrepassArgs a) {
     const int64_t o = (int64_t)mat * a.t_mstride + (c0 + cc) * a.t_pitch + r0 + cl;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) Elem<WDT>::store(a.trans, o + e, tile[cl + e][cc]);
+  }
   }
   ss = warp_sum(ss);
   if ((tid & 63) == 0) wsum[tid >> 6] = ss;
@@ -217,15 +283,28 @@ __global__ __launch_bounds__(256) void postpass_kernel(PostArgs a) {
   for (int rp = 0; rp < TILE / RPP; ++rp) {
     const int64_t r = r0 + rp * RPP + tid / TPR;
     if (r >= a.rows) continue;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const int64_t c = c0 + cl + e;
+    if constexpr (VEC == 8) {
+      const int64_t c = c0 + cl;
       if (c >= a.cols) continue;
       const int64_t pi = mb * a.rows * a.cols + r * a.cols + c;
       const int64_t ui = (int64_t)mat * a.u_mstride + r * a.u_pitch + c;
-      const float p = Elem<PDT>::load(pp, pi);
-      const float u = Elem<UDT>::load(a.u, ui);
-      Elem<PDT>::store(pp, pi, apply_elem<PDT, UDT>(p, u, a.wd, a.cautious, adj));
+      float p[8], u[8], o[8];
+      Vec8<PDT>::load(pp, pi, p);
+      Vec8<UDT>::load(a.u, ui, u);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = apply_elem<PDT, UDT>(p[e], u[e], a.wd, a.cautious, adj);
+      Vec8<PDT>::store(pp, pi, o);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const int64_t c = c0 + cl + e;
+        if (c >= a.cols) continue;
+        const int64_t pi = mb * a.rows * a.cols + r * a.cols + c;
+        const int64_t ui = (int64_t)mat * a.u_mstride + r * a.u_pitch + c;
+        const float p = Elem<PDT>::load(pp, pi);
+        const float u = Elem<UDT>::load(a.u, ui);
+        Elem<PDT>::store(pp, pi, apply_elem<PDT, UDT>(p, u, a.wd, a.cautious, adj));
+      }
     }
   }
 }
@@ -245,49 +324,49 @@ __global__ __launch_bounds__(256) void extract_kernel(const void* src, int64_t p
 }
 
 template <int GDT, int BDT, int WDT>
-void launch_prepass_t(const PrepassArgs& a, dim3 grid, bool vec4, hipStream_t s) {
-  if (vec4)
-    hipLaunchKernelGGL((prepass_kernel<GDT, BDT, WDT, 4>), grid, dim3(256), 0, s, a);
+void launch_prepass_t(const PrepassArgs& a, dim3 grid, bool vec8, hipStream_t s) {
+  if (vec8)
+    hipLaunchKernelGGL((prepass_kernel<GDT, BDT, WDT, 8>), grid, dim3(256), 0, s, a);
   else
     hipLaunchKernelGGL((prepass_kernel<GDT, BDT, WDT, 1>), grid, dim3(256), 0, s, a);
 }
 
 template <int GDT, int BDT>
-int launch_prepass_w(int wdt, const PrepassArgs& a, dim3 grid, bool vec4, hipStream_t s) {
+int launch_prepass_w(int wdt, const PrepassArgs& a, dim3 grid, bool vec8, hipStream_t s) {
   if (wdt == MUON_DT_BF16)
-    launch_prepass_t<GDT, BDT, MUON_DT_BF16>(a, grid, vec4, s);
+    launch_prepass_t<GDT, BDT, MUON_DT_BF16>(a, grid, vec8, s);
   else if (wdt == MUON_DT_F32)
-    launch_prepass_t<GDT, BDT, MUON_DT_F32>(a, grid, vec4, s);
+    launch_prepass_t<GDT, BDT, MUON_DT_F32>(a, grid, vec8, s);
   else
     return MUON_ERR_DTYPE;
   return MUON_OK;
 }
 
 template <int GDT>
-int launch_prepass_b(int bdt, int wdt, const PrepassArgs& a, dim3 grid, bool vec4,
+int launch_prepass_b(int bdt, int wdt, const PrepassArgs& a, dim3 grid, bool vec8,
                      hipStream_t s) {
   switch (bdt) {
-    case MUON_DT_F32: return launch_prepass_w<GDT, MUON_DT_F32>(wdt, a, grid, vec4, s);
-    case MUON_DT_BF16: return launch_prepass_w<GDT, MUON_DT_BF16>(wdt, a, grid, vec4, s);
-    case MUON_DT_F16: return launch_prepass_w<GDT, MUON_DT_F16>(wdt, a, grid, vec4, s);
+    case MUON_DT_F32: return launch_prepass_w<GDT, MUON_DT_F32>(wdt, a, grid, vec8, s);
+    case MUON_DT_BF16: return launch_prepass_w<GDT, MUON_DT_BF16>(wdt, a, grid, vec8, s);
+    case MUON_DT_F16: return launch_prepass_w<GDT, MUON_DT_F16>(wdt, a, grid, vec8, s);
   }
   return MUON_ERR_DTYPE;
 }
 
 template <int PDT, int UDT>
-void launch_post_t(const PostArgs& a, dim3 grid, bool vec4, hipStream_t s) {
-  if (vec4)
-    hipLaunchKernelGGL((postpass_kernel<PDT, UDT, 4>), grid, dim3(256), 0, s, a);
+void launch_post_t(const PostArgs& a, dim3 grid, bool vec8, hipStream_t s) {
+  if (vec8)
+    hipLaunchKernelGGL((postpass_kernel<PDT, UDT, 8>), grid, dim3(256), 0, s, a);
   else
     hipLaunchKernelGGL((postpass_kernel<PDT, UDT, 1>), grid, dim3(256), 0, s, a);
 }
 
 template <int PDT>
-int launch_post_u(int udt, const PostArgs& a, dim3 grid, bool vec4, hipStream_t s) {
+int launch_post_u(int udt, const PostArgs& a, dim3 grid, bool vec8, hipStream_t s) {
   switch (udt) {
-    case MUON_DT_F32: launch_post_t<PDT, MUON_DT_F32>(a, grid, vec4, s); return MUON_OK;
-    case MUON_DT_BF16: launch_post_t<PDT, MUON_DT_BF16>(a, grid, vec4, s); return MUON_OK;
-    case MUON_DT_F16: launch_post_t<PDT, MUON_DT_F16>(a, grid, vec4, s); return MUON_OK;
+    case MUON_DT_F32: launch_post_t<PDT, MUON_DT_F32>(a, grid, vec8, s); return MUON_OK;
+    case MUON_DT_BF16: launch_post_t<PDT, MUON_DT_BF16>(a, grid, vec8, s); return MUON_OK;
+    case MUON_DT_F16: launch_post_t<PDT, MUON_DT_F16>(a, grid, vec8, s); return MUON_OK;
   }
   return MUON_ERR_DTYPE;
 }
@@ -356,13 +435,15 @@ int muon_launch_prepass(int ntensors, void* const* grads, void* const* bufs, int
   a.has_buf = bufs != nullptr;
   a.write_grad = write_grad;
   a.write_direct = write_direct;
-  const bool vec4 = (cols % 4) == 0 && (s_pitch % 4) == 0;
+  bool vec8 = (cols % 8) == 0 && (s_pitch % 8) == 0 && (nb == 1 || (s_mstride % 8) == 0);
+  for (int i = 0; i < ntensors; ++i)
+    if (((uintptr_t)grads[i] & 15) || (bufs && ((uintptr_t)bufs[i] & 15))) vec8 = false;
   dim3 grid((unsigned)((rows_pad / TILE) * (cols_pad / TILE)), (unsigned)(ntensors * nb));
   int rc;
   switch (gdt) {
-    case MUON_DT_F32: rc = launch_prepass_b<MUON_DT_F32>(bdt, wdt, a, grid, vec4, s); break;
-    case MUON_DT_BF16: rc = launch_prepass_b<MUON_DT_BF16>(bdt, wdt, a, grid, vec4, s); break;
-    case MUON_DT_F16: rc = launch_prepass_b<MUON_DT_F16>(bdt, wdt, a, grid, vec4, s); break;
+    case MUON_DT_F32: rc = launch_prepass_b<MUON_DT_F32>(bdt, wdt, a, grid, vec8, s); break;
+    case MUON_DT_BF16: rc = launch_prepass_b<MUON_DT_BF16>(bdt, wdt, a, grid, vec8, s); break;
+    case MUON_DT_F16: rc = launch_prepass_b<MUON_DT_F16>(bdt, wdt, a, grid, vec8, s); break;
     default: rc = MUON_ERR_DTYPE;
   }
   if (rc != MUON_OK) {
@@ -458,13 +539,16 @@ int muon_launch_postpass(int ntensors, void* const* params, const float* adj, in
   a.cautious = cautious;
   const int64_t tiles_r = (rows + TILE - 1) / TILE, tiles_c = (cols + TILE - 1) / TILE;
   a.tiles_c = (int)tiles_c;
-  const bool vec4 = (cols % 4) == 0 && (u_pitch % 4) == 0;
+  bool vec8 = (cols % 8) == 0 && (u_pitch % 8) == 0 && (u_mstride % 8) == 0 &&
+              !((uintptr_t)u & 15);
+  for (int i = 0; i < ntensors; ++i)
+    if ((uintptr_t)params[i] & 15) vec8 = false;
   dim3 grid((unsigned)(tiles_r * tiles_c), (unsigned)(ntensors * nb));
   int rc;
   switch (pdt) {
-    case MUON_DT_F32: rc = launch_post_u<MUON_DT_F32>(udt, a, grid, vec4, s); break;
-    case MUON_DT_BF16: rc = launch_post_u<MUON_DT_BF16>(udt, a, grid, vec4, s); break;
-    case MUON_DT_F16: rc = launch_post_u<MUON_DT_F16>(udt, a, grid, vec4, s); break;
+    case MUON_DT_F32: rc = launch_post_u<MUON_DT_F32>(udt, a, grid, vec8, s); break;
+    case MUON_DT_BF16: rc = launch_post_u<MUON_DT_BF16>(udt, a, grid, vec8, s); break;
+    case MUON_DT_F16: rc = launch_post_u<MUON_DT_F16>(udt, a, grid, vec8, s); break;
     default: rc = MUON_ERR_DTYPE;
   }
   if (rc != MUON_OK) {

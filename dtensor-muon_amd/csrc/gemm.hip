@@ -195,16 +195,24 @@ MUON_DEVICE void epilogue(const GemmArgs& g, int mode, int bidx, int64_t row0, i
 }
 
 // ----------------------------------------------------------------------------------
-// bf16: 256 x 256 x 64 tile, 4 wavefronts in 2 x 2, each 128 x 128 (4 x 4 MFMA
-// 32x32x16 blocks, 256 fp32 accumulators per lane). LDS: double-buffered operand
-// panels with an 8-element row pad (row pitch 144 B) so the 16-byte fragment reads
-// of 32 consecutive rows hit distinct banks. Global loads for tile k+1 are issued
-// before the MFMAs of tile k and parked in registers until the LDS slot frees up.
+// bf16: 256 x 256 x 64 tile over a WGM x WGN grid of wavefronts, each owning a
+// (256/WGM) x (256/WGN) block of 32x32x16 MFMA accumulators. With 4 wavefronts
+// (2 x 2) each holds 128 x 128 (256 fp32 accumulators per lane, one wave per SIMD);
+// with 8 (2 x 4) each holds 128 x 64 and two waves share a SIMD, hiding each
+// other's LDS and memory latency. LDS: double-buffered operand panels with an
+// 8-element row pad (row pitch 144 B) so the 16-byte fragment reads of consecutive
+// rows hit distinct banks. Global loads for tile k+1 are issued before the MFMAs of
+// tile k and parked in registers until the LDS slot frees up.
 constexpr int BF_BM = 256, BF_BN = 256, BF_BK = 64, BF_LDSP = BF_BK + 8;
 constexpr int BF_SMEM = 2 * (BF_BM + BF_BN) * BF_LDSP * 2;
 
-template <int MODE, bool MASKED>
-__global__ __launch_bounds__(256, 1) void gemm_bf16_kernel(GemmArgs g) {
+template <int MODE, bool MASKED, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_bf16_kernel(GemmArgs g) {
+  constexpr int NT = 64 * WGM * WGN;
+  constexpr int WM = BF_BM / WGM, WN = BF_BN / WGN;
+  constexpr int FM = WM / 32, FN = WN / 32;
+  constexpr int CPT = (BF_BM * BF_BK / 8) / NT;  // 16-byte chunks per thread per operand
+  constexpr int RPQ = NT / 8;                      // rows covered by one chunk pass
   extern __shared__ __align__(16) uint8_t smem[];
   bf16_t* As = (bf16_t*)smem;
   bf16_t* Bs = As + 2 * BF_BM * BF_LDSP;
@@ -212,7 +220,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_kernel(GemmArgs g) {
   int bidx, tm, tn;
   map_tile(g, MODE, bidx, tm, tn);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
 
   const bf16_t* A = (const bf16_t*)g.a + (int64_t)bidx * g.sa;
   const bf16_t* B = (const bf16_t*)g.b + (int64_t)bidx * g.sb;
@@ -227,21 +235,19 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_kernel(GemmArgs g) {
       (void*)(B + brow0 * g.ldb), 0, 0x7fffffff, 0x00020000);
   const int voa = (int)((tid >> 3) * lda_b + (tid & 7) * 16);
   const int vob = (int)((tid >> 3) * ldb_b + (tid & 7) * 16);
-  uint4 ra[8], rb[8];
+  uint4 ra[CPT], rb[CPT];
   auto gload = [&](int64_t k0) {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int c = q * 256 + tid;
-      const int r = c >> 3, cc = (c & 7) * 8;
+    for (int q = 0; q < CPT; ++q) {
       if (!MASKED) {
         typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
-        u32x4 va = __builtin_amdgcn_raw_buffer_load_b128(rsa, voa, (int)(q * 32 * lda_b + k0 * 2), 0);
-        u32x4 vb = __builtin_amdgcn_raw_buffer_load_b128(rsb, vob, (int)(q * 32 * ldb_b + k0 * 2), 0);
+        u32x4 va = __builtin_amdgcn_raw_buffer_load_b128(rsa, voa, (int)(q * RPQ * lda_b + k0 * 2), 0);
+        u32x4 vb = __builtin_amdgcn_raw_buffer_load_b128(rsb, vob, (int)(q * RPQ * ldb_b + k0 * 2), 0);
         ra[q] = make_uint4(va.x, va.y, va.z, va.w);
         rb[q] = make_uint4(vb.x, vb.y, vb.z, vb.w);
-        (void)r;
-        (void)cc;
       } else {
+        const int c = q * NT + tid;
+        const int r = c >> 3, cc = (c & 7) * 8;
         uint16_t ta[8], tb[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -259,19 +265,19 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_kernel(GemmArgs g) {
     bf16_t* as = As + buf * BF_BM * BF_LDSP;
     bf16_t* bs = Bs + buf * BF_BN * BF_LDSP;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int c = q * 256 + tid;
+    for (int q = 0; q < CPT; ++q) {
+      const int c = q * NT + tid;
       const int r = c >> 3, cc = (c & 7) * 8;
       *(uint4*)(as + r * BF_LDSP + cc) = ra[q];
       *(uint4*)(bs + r * BF_LDSP + cc) = rb[q];
     }
   };
 
-  f32x16 acc[4][4];
+  f32x16 acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
@@ -283,30 +289,182 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_kernel(GemmArgs g) {
   for (int kt = 0; kt < KT; ++kt) {
     const int cur = kt & 1;
     if (kt + 1 < KT) gload((int64_t)(kt + 1) * BF_BK);
-    const bf16_t* as = As + cur * BF_BM * BF_LDSP + (wm * 128 + frow) * BF_LDSP + fk;
-    const bf16_t* bs = Bs + cur * BF_BN * BF_LDSP + (wn * 128 + frow) * BF_LDSP + fk;
+    const bf16_t* as = As + cur * BF_BM * BF_LDSP + (wm * WM + frow) * BF_LDSP + fk;
+    const bf16_t* bs = Bs + cur * BF_BN * BF_LDSP + (wn * WN + frow) * BF_LDSP + fk;
 #pragma unroll
     for (int ks = 0; ks < BF_BK / 16; ++ks) {
-      bf16x8_mfma af[4], bfr[4];
+      bf16x8_mfma af[FM], bfr[FN];
 #pragma unroll
-      for (int f = 0; f < 4; ++f) {
-        uint4 va = *(const uint4*)(as + f * 32 * BF_LDSP + ks * 16);
-        uint4 vb = *(const uint4*)(bs + f * 32 * BF_LDSP + ks * 16);
-        af[f] = __builtin_bit_cast(bf16x8_mfma, va);
-        bfr[f] = __builtin_bit_cast(bf16x8_mfma, vb);
-      }
+      for (int f = 0; f < FM; ++f)
+        af[f] = __builtin_bit_cast(bf16x8_mfma, *(const uint4*)(as + f * 32 * BF_LDSP + ks * 16));
 #pragma unroll
-      for (int fm = 0; fm < 4; ++fm)
+      for (int f = 0; f < FN; ++f)
+        bfr[f] = __builtin_bit_cast(bf16x8_mfma, *(const uint4*)(bs + f * 32 * BF_LDSP + ks * 16));
 #pragma unroll
-        for (int fn = 0; fn < 4; ++fn)
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
           acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[fm], bfr[fn], acc[fm][fn], 0, 0, 0);
     }
     if (kt + 1 < KT) sstore(cur ^ 1);
     __syncthreads();
   }
 
-  epilogue<bf16_t, 4, 4, MASKED>(g, MODE, bidx, arow0 + wm * 128, brow0 + wn * 128, acc, lane,
-                         MODE == MODE_SYRK && tm == tn);
+  epilogue<bf16_t, FM, FN, MASKED>(g, MODE, bidx, arow0 + wm * WM, brow0 + wn * WN, acc, lane,
+                                   MODE == MODE_SYRK && tm == tn);
+}
+
+// ----------------------------------------------------------------------------------
+// bf16, software-pipelined: 256 x 256 x 64 tile, 4 wavefronts (2 x 2), each 128 x 128
+// (one wave per SIMD, 256 accumulators in AGPRs). The largest per-wave tile keeps
+// LDS traffic per MFMA at its minimum (8 fragment reads per 16 MFMAs); a single wave
+// per SIMD then hides latency by explicit pipelining instead of by wave switching:
+//   * fragments are double-buffered: the 8 LDS reads of k-substep s+1 are issued
+//     between the 16 MFMAs of substep s;
+//   * global loads run two K-tiles ahead (issued in substep 3 of tile k for tile k+2,
+//     parked in registers) and are written to LDS in substep 2 of tile k+1, spread
+//     between that substep's MFMAs;
+//   * one barrier per K-tile, placed before substep 3 so that substep's MFMAs (whose
+//     fragments are already in registers) overlap the barrier and the first reads of
+//     the next tile.
+// sched_group_barrier pins the interleaving so the compiler cannot hoist all loads
+// ahead of the MFMAs.
+#define SG_MFMA 0x008
+#define SG_VMEM_READ 0x020
+#define SG_DS_READ 0x100
+#define SG_DS_WRITE 0x200
+
+template <int MODE>
+__global__ __launch_bounds__(256, 1) void gemm_bf16_pipe_kernel(GemmArgs g) {
+  constexpr int NT = 256, FM = 4, FN = 4, CPT = 8, RPQ = 32;
+  extern __shared__ __align__(16) uint8_t smem[];
+  bf16_t* As = (bf16_t*)smem;
+  bf16_t* Bs = As + 2 * BF_BM * BF_LDSP;
+
+  int bidx, tm, tn;
+  map_tile(g, MODE, bidx, tm, tn);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const bf16_t* A = (const bf16_t*)g.a + (int64_t)bidx * g.sa;
+  const bf16_t* B = (const bf16_t*)g.b + (int64_t)bidx * g.sb;
+  const int64_t arow0 = (int64_t)tm * BF_BM, brow0 = (int64_t)tn * BF_BN;
+  const int64_t lda_b = g.lda * 2, ldb_b = g.ldb * 2;
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(A + arow0 * g.lda), 0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(B + brow0 * g.ldb), 0, 0x7fffffff, 0x00020000);
+  const int voa = (int)((tid >> 3) * lda_b + (tid & 7) * 16);
+  const int vob = (int)((tid >> 3) * ldb_b + (tid & 7) * 16);
+  typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+  u32x4 ra[CPT], rb[CPT];
+  auto gload = [&](int64_t k0) {
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+      ra[q] = __builtin_amdgcn_raw_buffer_load_b128(rsa, voa, (int)(q * RPQ * lda_b + k0 * 2), 0);
+      rb[q] = __builtin_amdgcn_raw_buffer_load_b128(rsb, vob, (int)(q * RPQ * ldb_b + k0 * 2), 0);
+    }
+  };
+  // LDS write address of this thread's chunk q: row q*32 + tid/8, column (tid%8)*8
+  const int swr = (tid >> 3) * BF_LDSP + (tid & 7) * 8;
+  auto sstore = [&](int buf) {
+    bf16_t* as = As + buf * BF_BM * BF_LDSP + swr;
+    bf16_t* bs = Bs + buf * BF_BN * BF_LDSP + swr;
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+      *(u32x4*)(as + q * RPQ * BF_LDSP) = ra[q];
+      *(u32x4*)(bs + q * RPQ * BF_LDSP) = rb[q];
+    }
+  };
+
+  const int frow = lane & 31, fk = (lane >> 5) * 8;
+  const int afo = (wm * 128 + frow) * BF_LDSP + fk;
+  const int bfo = (wn * 128 + frow) * BF_LDSP + fk;
+  bf16x8_mfma af[2][FM], bfr[2][FN];
+  auto fload = [&](int buf, int ks, int set) {
+    const bf16_t* as = As + buf * BF_BM * BF_LDSP + afo + ks * 16;
+    const bf16_t* bs = Bs + buf * BF_BN * BF_LDSP + bfo + ks * 16;
+#pragma unroll
+    for (int f = 0; f < FM; ++f) af[set][f] = *(const bf16x8_mfma*)(as + f * 32 * BF_LDSP);
+#pragma unroll
+    for (int f = 0; f < FN; ++f) bfr[set][f] = *(const bf16x8_mfma*)(bs + f * 32 * BF_LDSP);
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  auto mfmas = [&](int set) {
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+        acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[set][fm], bfr[set][fn],
+                                                               acc[fm][fn], 0, 0, 0);
+  };
+
+  const int KT = (int)(g.K / BF_BK);
+  // prologue: tile 0 into LDS, tile 1 into registers, substep-0 fragments of tile 0
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  gload(KT > 1 ? BF_BK : 0);
+  fload(0, 0, 0);
+
+  // The loop body is branch-free so each substep is one scheduling region: in the
+  // last two iterations the loads fetch a clamped (valid) K-tile and the stores fill
+  // a buffer that is never read again.
+  const int64_t klast = (int64_t)(KT - 1) * BF_BK;
+  for (int kt = 0; kt < KT; ++kt) {
+    const int buf = kt & 1;
+    // substep 0: read fragments of substep 1
+    fload(buf, 1, 1);
+    mfmas(0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+    }
+    // substep 1: read fragments of substep 2
+    fload(buf, 2, 0);
+    mfmas(1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+    }
+    // substep 2: read fragments of substep 3, write tile kt+1 into the other buffer
+    fload(buf, 3, 1);
+    sstore(buf ^ 1);
+    mfmas(0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_DS_WRITE, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+    }
+    // substep 3: barrier (tile kt+1 is in LDS, nobody reads tile kt's buffer any more),
+    // then substep-0 fragments of tile kt+1 and global loads of tile kt+2 between the
+    // MFMAs that finish tile kt
+    __syncthreads();
+    fload(buf ^ 1, 0, 0);
+    gload(min((int64_t)(kt + 2) * BF_BK, klast));
+    mfmas(1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_VMEM_READ, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+    }
+  }
+
+  epilogue<bf16_t, FM, FN, false>(g, MODE, bidx, arow0 + wm * 128, brow0 + wn * 128, acc, lane,
+                                  MODE == MODE_SYRK && tm == tn);
 }
 
 // ----------------------------------------------------------------------------------
@@ -399,16 +557,29 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
                         MODE == MODE_SYRK && tm == tn);
 }
 
+// Wave grid of the bf16 tile used by the library: 4 x 2 wavefronts (each 64 x 128,
+// two waves per SIMD). Measured on MI355X at the Llama step shapes, it runs the B X
+// GEMM at 760-770 TFLOP/s and the SYRKs at 810-850, against 560-770 for 2 x 2 and
+// 620-830 for the software-pipelined single-wave variant.
+#ifndef MUON_BF16_WGM
+#define MUON_BF16_WGM 4
+#endif
+#ifndef MUON_BF16_WGN
+#define MUON_BF16_WGN 2
+#endif
+constexpr int BF_WGM = MUON_BF16_WGM, BF_WGN = MUON_BF16_WGN;
+constexpr int BF_NT = 64 * BF_WGM * BF_WGN;
+
 // The bf16 kernels need more than the default 64 KiB of dynamic LDS; raise the
 // per-kernel limit once per process for every instantiation.
 int reserve_bf16_lds() {
   static int status = -1;
   static std::once_flag once;
   std::call_once(once, [] {
-    const void* ks[4] = {(const void*)gemm_bf16_kernel<MODE_GEMM, false>,
-                         (const void*)gemm_bf16_kernel<MODE_GEMM, true>,
-                         (const void*)gemm_bf16_kernel<MODE_SYRK, false>,
-                         (const void*)gemm_bf16_kernel<MODE_SYRK, true>};
+    const void* ks[4] = {(const void*)gemm_bf16_kernel<MODE_GEMM, false, BF_WGM, BF_WGN>,
+                         (const void*)gemm_bf16_kernel<MODE_GEMM, true, BF_WGM, BF_WGN>,
+                         (const void*)gemm_bf16_kernel<MODE_SYRK, false, BF_WGM, BF_WGN>,
+                         (const void*)gemm_bf16_kernel<MODE_SYRK, true, BF_WGM, BF_WGN>};
     status = 0;
     for (const void* k : ks)
       if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, BF_SMEM) !=
@@ -484,7 +655,8 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
     }
 #define LAUNCH_BF(MODE_, MASK_)                                                        \
   do {                                                                                 \
-    hipLaunchKernelGGL((gemm_bf16_kernel<MODE_, MASK_>), grid, block, BF_SMEM, stream, g); \
+    hipLaunchKernelGGL((gemm_bf16_kernel<MODE_, MASK_, BF_WGM, BF_WGN>), grid, dim3(BF_NT), \
+                       BF_SMEM, stream, g);                                                \
   } while (0)
     if (mode == MODE_SYRK) {
       if (masked) LAUNCH_BF(MODE_SYRK, true); else LAUNCH_BF(MODE_SYRK, false);
