@@ -315,159 +315,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_bf16_kernel(GemmArgs g
 }
 
 // ----------------------------------------------------------------------------------
-// bf16, software-pipelined: 256 x 256 x 64 tile, 4 wavefronts (2 x 2), each 128 x 128
-// (one wave per SIMD, 256 accumulators in AGPRs). The largest per-wave tile keeps
-// LDS traffic per MFMA at its minimum (8 fragment reads per 16 MFMAs); a single wave
-// per SIMD then hides latency by explicit pipelining instead of by wave switching:
-//   * fragments are double-buffered: the 8 LDS reads of k-substep s+1 are issued
-//     between the 16 MFMAs of substep s;
-//   * global loads run two K-tiles ahead (issued in substep 3 of tile k for tile k+2,
-//     parked in registers) and are written to LDS in substep 2 of tile k+1, spread
-//     between that substep's MFMAs;
-//   * one barrier per K-tile, placed before substep 3 so that substep's MFMAs (whose
-//     fragments are already in registers) overlap the barrier and the first reads of
-//     the next tile.
-// sched_group_barrier pins the interleaving so the compiler cannot hoist all loads
-// ahead of the MFMAs.
-#define SG_MFMA 0x008
-#define SG_VMEM_READ 0x020
-#define SG_DS_READ 0x100
-#define SG_DS_WRITE 0x200
-
-template <int MODE>
-__global__ __launch_bounds__(256, 1) void gemm_bf16_pipe_kernel(GemmArgs g) {
-  constexpr int NT = 256, FM = 4, FN = 4, CPT = 8, RPQ = 32;
-  extern __shared__ __align__(16) uint8_t smem[];
-  bf16_t* As = (bf16_t*)smem;
-  bf16_t* Bs = As + 2 * BF_BM * BF_LDSP;
-
-  int bidx, tm, tn;
-  map_tile(g, MODE, bidx, tm, tn);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  const bf16_t* A = (const bf16_t*)g.a + (int64_t)bidx * g.sa;
-  const bf16_t* B = (const bf16_t*)g.b + (int64_t)bidx * g.sb;
-  const int64_t arow0 = (int64_t)tm * BF_BM, brow0 = (int64_t)tn * BF_BN;
-  const int64_t lda_b = g.lda * 2, ldb_b = g.ldb * 2;
-  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(A + arow0 * g.lda), 0, 0x7fffffff, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(B + brow0 * g.ldb), 0, 0x7fffffff, 0x00020000);
-  const int voa = (int)((tid >> 3) * lda_b + (tid & 7) * 16);
-  const int vob = (int)((tid >> 3) * ldb_b + (tid & 7) * 16);
-  typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
-  u32x4 ra[CPT], rb[CPT];
-  auto gload = [&](int64_t k0) {
-#pragma unroll
-    for (int q = 0; q < CPT; ++q) {
-      ra[q] = __builtin_amdgcn_raw_buffer_load_b128(rsa, voa, (int)(q * RPQ * lda_b + k0 * 2), 0);
-      rb[q] = __builtin_amdgcn_raw_buffer_load_b128(rsb, vob, (int)(q * RPQ * ldb_b + k0 * 2), 0);
-    }
-  };
-  // LDS write address of this thread's chunk q: row q*32 + tid/8, column (tid%8)*8
-  const int swr = (tid >> 3) * BF_LDSP + (tid & 7) * 8;
-  auto sstore = [&](int buf) {
-    bf16_t* as = As + buf * BF_BM * BF_LDSP + swr;
-    bf16_t* bs = Bs + buf * BF_BN * BF_LDSP + swr;
-#pragma unroll
-    for (int q = 0; q < CPT; ++q) {
-      *(u32x4*)(as + q * RPQ * BF_LDSP) = ra[q];
-      *(u32x4*)(bs + q * RPQ * BF_LDSP) = rb[q];
-    }
-  };
-
-  const int frow = lane & 31, fk = (lane >> 5) * 8;
-  const int afo = (wm * 128 + frow) * BF_LDSP + fk;
-  const int bfo = (wn * 128 + frow) * BF_LDSP + fk;
-  bf16x8_mfma af[2][FM], bfr[2][FN];
-  auto fload = [&](int buf, int ks, int set) {
-    const bf16_t* as = As + buf * BF_BM * BF_LDSP + afo + ks * 16;
-    const bf16_t* bs = Bs + buf * BF_BN * BF_LDSP + bfo + ks * 16;
-#pragma unroll
-    for (int f = 0; f < FM; ++f) af[set][f] = *(const bf16x8_mfma*)(as + f * 32 * BF_LDSP);
-#pragma unroll
-    for (int f = 0; f < FN; ++f) bfr[set][f] = *(const bf16x8_mfma*)(bs + f * 32 * BF_LDSP);
-  };
-
-  f32x16 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  auto mfmas = [&](int set) {
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
-        acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[set][fm], bfr[set][fn],
-                                                               acc[fm][fn], 0, 0, 0);
-  };
-
-  const int KT = (int)(g.K / BF_BK);
-  // prologue: tile 0 into LDS, tile 1 into registers, substep-0 fragments of tile 0
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  gload(KT > 1 ? BF_BK : 0);
-  fload(0, 0, 0);
-
-  // The loop body is branch-free so each substep is one scheduling region: in the
-  // last two iterations the loads fetch a clamped (valid) K-tile and the stores fill
-  // a buffer that is never read again.
-  const int64_t klast = (int64_t)(KT - 1) * BF_BK;
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    // substep 0: read fragments of substep 1
-    fload(buf, 1, 1);
-    mfmas(0);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
-    }
-    // substep 1: read fragments of substep 2
-    fload(buf, 2, 0);
-    mfmas(1);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
-    }
-    // substep 2: read fragments of substep 3, write tile kt+1 into the other buffer
-    fload(buf, 3, 1);
-    sstore(buf ^ 1);
-    mfmas(0);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_DS_WRITE, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-    }
-    // substep 3: barrier (tile kt+1 is in LDS, nobody reads tile kt's buffer any more),
-    // then substep-0 fragments of tile kt+1 and global loads of tile kt+2 between the
-    // MFMAs that finish tile kt
-    __syncthreads();
-    fload(buf ^ 1, 0, 0);
-    gload(min((int64_t)(kt + 2) * BF_BK, klast));
-    mfmas(1);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_VMEM_READ, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
-    }
-  }
-
-  epilogue<bf16_t, FM, FN, false>(g, MODE, bidx, arow0 + wm * 128, brow0 + wn * 128, acc, lane,
-                                  MODE == MODE_SYRK && tm == tn);
-}
-
-// ----------------------------------------------------------------------------------
 // fp32: 128 x 128 x 16 tile, 4 wavefronts in 2 x 2, each 64 x 64 (2 x 2 MFMA
 // 32x32x2 f32 blocks). Used for the fp32 iteration mode and fp32 gram_.
 constexpr int F_BM = 128, F_BN = 128, F_BK = 16, F_LDSP = F_BK + 4;
@@ -557,10 +404,304 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
                         MODE == MODE_SYRK && tm == tn);
 }
 
-// Wave grid of the bf16 tile used by the library: 4 x 2 wavefronts (each 64 x 128,
-// two waves per SIMD). Measured on MI355X at the Llama step shapes, it runs the B X
-// GEMM at 760-770 TFLOP/s and the SYRKs at 810-850, against 560-770 for 2 x 2 and
-// 620-830 for the software-pipelined single-wave variant.
+// ----------------------------------------------------------------------------------
+// bf16, direct-to-LDS: the unmasked workhorse of the iteration.
+//
+// Main loop. 256 x 256 x 64 tile, 8 wavefronts in 4 x 2 (each 64 x 128, two waves per
+// SIMD). Operands stream HBM/L2 -> LDS with `buffer_load_dwordx4 ... lds` (no VGPR
+// staging, no ds_write), double-buffered: the loads of tile k+1 are issued right
+// after the barrier that opens tile k and land while tile k's MFMAs run. Each load
+// instruction fills 1 KB of LDS (64 lanes x 16 B), i.e. 8 rows of 128 B; the lane ->
+// global-address map stores 16-byte chunk c of row r at chunk position c ^ (r & 7),
+// which makes the MFMA fragment reads (rows r..r+7 at one chunk) bank-conflict free.
+// The barrier is an LDS-only wait plus s_barrier: a full __syncthreads would also
+// wait for the in-flight prefetch.
+//
+// Software pipeline. Each k-substep (16 of the 64 k) is one inline-asm block: the 8
+// MFMAs of the current fragments interleaved with the 6 LDS reads of the next
+// substep's fragments, ending with those reads complete, so LDS latency hides behind
+// MFMAs instead of stalling them (the compiler otherwise reorders the MFMAs of the
+// next substep up against their own loads). Per tile:
+//   substeps 0-2 (reading substeps 1-3 of this tile), [beta term], wait for tile k+1's
+//   DMA, barrier, issue DMA of tile k+2 into this tile's stage, substep 3 (reading
+//   substep 0 of tile k+1).
+// The loop body has no branch around the MFMAs, which keeps the accumulators in one
+// register assignment (a branch there made the allocator copy and spill them); the
+// last tile's extra fragment reads hit a stale stage and are discarded.
+//
+// The beta term. Both uses of beta read the transpose of the b operand:
+//   GEMM  X' = a X + B X      with b = X^T   (cin = X   = b^T)
+//   SYRK  B  = c A A + b A    with b = A     (cin = A   = A^T, A symmetric)
+// so cin(i, j) = b(j, i), and during the K-tile whose k range covers a wave's output
+// rows i the needed values sit in the b panel in LDS. The wave adds (beta/alpha) *
+// cin into its accumulators there and never reads cin from memory.
+//
+// Epilogue. The finished tile is staged through LDS (the operand buffers are dead by
+// then) so every global store is a coalesced 16-byte row chunk:
+//   * transposed stores (GEMM out_t, the mirror half of an off-diagonal SYRK tile):
+//     the accumulators hold 4 consecutive rows of one column per lane, written to a
+//     transposed LDS tile with 8-byte ds_writes and read back as rows;
+//   * row-major stores: written element-wise to a row-major LDS tile.
+// Diagonal SYRK tiles store only their upper triangle, mirrored in place, so the
+// output is exactly symmetric.
+constexpr int V2_BK = 64, V2_ROWB = V2_BK * 2, V2_TILEB = 256 * V2_ROWB;
+constexpr int V2_STAGEB = 2 * V2_TILEB;
+constexpr int V2_EP_PITCH = 256 + 8;  // staging row pitch (elements)
+constexpr int V2_SMEM = (2 * V2_STAGEB > 256 * V2_EP_PITCH * 2) ? 2 * V2_STAGEB
+                                                                   : 256 * V2_EP_PITCH * 2;
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+MUON_DEVICE void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+MUON_DEVICE void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
+
+#define MUON_MFMA(C, A, B) "v_mfma_f32_32x32x16_bf16 %[" #C "], %[" #A "], %[" #B "], %[" #C "]\n\t"
+// One k-substep of a 64 x 128 wave tile (2 x 4 accumulators of 32 x 32): 8 MFMAs on
+// the current fragments (ca, cb), interleaved with the LDS reads of the next
+// fragments (na from aa, aa + 4 KB; nb from ba + 0/4/8/12 KB), which are complete
+// when the block ends.
+MUON_DEVICE void mfma_substep(f32x16 (&acc)[2][4], const bf16x8_mfma (&ca)[2],
+                              const bf16x8_mfma (&cb)[4], bf16x8_mfma (&na)[2],
+                              bf16x8_mfma (&nb)[4], uint32_t aa, uint32_t ba) {
+  asm volatile(
+      "ds_read_b128 %[na0], %[aa]\n\t"
+      MUON_MFMA(c00, ca0, cb0)
+      "ds_read_b128 %[nb0], %[ba]\n\t"
+      MUON_MFMA(c01, ca0, cb1)
+      "ds_read_b128 %[na1], %[aa] offset:4096\n\t"
+      MUON_MFMA(c02, ca0, cb2)
+      "ds_read_b128 %[nb1], %[ba] offset:4096\n\t"
+      MUON_MFMA(c03, ca0, cb3)
+      "ds_read_b128 %[nb2], %[ba] offset:8192\n\t"
+      MUON_MFMA(c10, ca1, cb0)
+      "ds_read_b128 %[nb3], %[ba] offset:12288\n\t"
+      MUON_MFMA(c11, ca1, cb1)
+      MUON_MFMA(c12, ca1, cb2)
+      MUON_MFMA(c13, ca1, cb3)
+      "s_waitcnt lgkmcnt(0)"
+      : [c00] "+v"(acc[0][0]), [c01] "+v"(acc[0][1]), [c02] "+v"(acc[0][2]),
+        [c03] "+v"(acc[0][3]), [c10] "+v"(acc[1][0]), [c11] "+v"(acc[1][1]),
+        [c12] "+v"(acc[1][2]), [c13] "+v"(acc[1][3]), [na0] "=&v"(na[0]), [na1] "=&v"(na[1]),
+        [nb0] "=&v"(nb[0]), [nb1] "=&v"(nb[1]), [nb2] "=&v"(nb[2]), [nb3] "=&v"(nb[3])
+      : [ca0] "v"(ca[0]), [ca1] "v"(ca[1]), [cb0] "v"(cb[0]), [cb1] "v"(cb[1]),
+        [cb2] "v"(cb[2]), [cb3] "v"(cb[3]), [aa] "v"(aa), [ba] "v"(ba));
+}
+#undef MUON_MFMA
+
+MUON_DEVICE void frag_load(bf16x8_mfma (&na)[2], bf16x8_mfma (&nb)[4], uint32_t aa, uint32_t ba) {
+  asm volatile(
+      "ds_read_b128 %[na0], %[aa]\n\t"
+      "ds_read_b128 %[na1], %[aa] offset:4096\n\t"
+      "ds_read_b128 %[nb0], %[ba]\n\t"
+      "ds_read_b128 %[nb1], %[ba] offset:4096\n\t"
+      "ds_read_b128 %[nb2], %[ba] offset:8192\n\t"
+      "ds_read_b128 %[nb3], %[ba] offset:12288\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : [na0] "=&v"(na[0]), [na1] "=&v"(na[1]), [nb0] "=&v"(nb[0]), [nb1] "=&v"(nb[1]),
+        [nb2] "=&v"(nb[2]), [nb3] "=&v"(nb[3])
+      : [aa] "v"(aa), [ba] "v"(ba));
+}
+
+// The MFMAs run inside inline asm, which the compiler's hazard recognizer does not
+// see: VALU access to their accumulators needs the XDL result latency (at most 19
+// wait states on gfx950 for a 32x32 MFMA) in between, and an MFMA reading srcC
+// written by VALU needs 2.
+MUON_DEVICE void mfma_to_valu_wait() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
+MUON_DEVICE void valu_to_mfma_wait() { asm volatile("s_nop 4" ::: "memory"); }
+
+template <int MODE>
+__global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
+  constexpr int NW = 8, WGN = 2, WM = 64, WN = 128, FM = 2, FN = 4;
+  constexpr int SPW = (V2_TILEB / 1024) / NW;  // 1 KB load slabs per wave per operand
+  extern __shared__ __align__(16) uint8_t smem[];
+
+  int bidx, tm, tn;
+  map_tile(g, MODE, bidx, tm, tn);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+  const bf16_t* A = (const bf16_t*)g.a + (int64_t)bidx * g.sa;
+  const bf16_t* B = (const bf16_t*)g.b + (int64_t)bidx * g.sb;
+  const int64_t arow0 = (int64_t)tm * 256, brow0 = (int64_t)tn * 256;
+  const int lda_b = (int)(g.lda * 2), ldb_b = (int)(g.ldb * 2);
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(A + arow0 * g.lda), 0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(B + brow0 * g.ldb), 0, 0x7fffffff, 0x00020000);
+  // load slab q*NW + wave = rows (q*NW + wave)*8 .. +7; lane -> row lane/8, chunk
+  // position lane%8, which holds logical chunk (lane%8) ^ (row & 7)
+  const int r_in = wave * 8 + (lane >> 3);
+  const int lch = (lane & 7) ^ (r_in & 7);
+  const int voa = r_in * lda_b + lch * 16;
+  const int vob = r_in * ldb_b + lch * 16;
+  auto issue = [&](int kt, int st) {
+    uint8_t* sa = smem + st * V2_STAGEB;
+    uint8_t* sb = sa + V2_TILEB;
+#pragma unroll
+    for (int q = 0; q < SPW; ++q) {
+      const int slab = q * NW + wave;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(sa + slab * 1024), 16, voa,
+                                               q * NW * 8 * lda_b + kt * V2_ROWB, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_ptr_t)(sb + slab * 1024), 16, vob,
+                                               q * NW * 8 * ldb_b + kt * V2_ROWB, 0, 0);
+    }
+  };
+
+  // MFMA fragment read offsets: lane -> row lane%32 of the fragment, logical chunk
+  // 2*ks + lane/32 for k-substep ks
+  const int fr = lane & 31, fh = lane >> 5;
+  int foff[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) foff[ks] = fr * V2_ROWB + (((ks * 2 + fh) ^ (fr & 7)) << 4);
+  const int abase = wm * WM * V2_ROWB, bbase = V2_TILEB + wn * WN * V2_ROWB;
+
+  float alpha = g.alpha, beta = g.beta;
+  if (g.scale_mode != 0) {
+    const float s = g.scale[bidx];
+    if (g.scale_mode == 1) {
+      alpha *= s;
+      beta *= s;
+    } else {
+      alpha *= s * s;
+    }
+  }
+  const float ratio = beta != 0.0f ? beta / alpha : 0.0f;
+  // K-tile whose k range equals this wave's output rows (WM == BK)
+  const int kdiag = ratio != 0.0f ? (int)((arow0 + wm * WM) / V2_BK) : -1;
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int KT = (int)(g.K / V2_BK);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  auto aaddr = [&](int st, int ks) -> uint32_t { return lds0 + st * V2_STAGEB + abase + foff[ks]; };
+  auto baddr = [&](int st, int ks) -> uint32_t { return lds0 + st * V2_STAGEB + bbase + foff[ks]; };
+  bf16x8_mfma a0[FM], b0[FN], a1[FM], b1[FN];
+  issue(0, 0);
+  wait_vmcnt0();
+  lds_barrier();
+  if (KT > 1) issue(1, 1);
+  frag_load(a0, b0, aaddr(0, 0), baddr(0, 0));
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cs = kt & 1;
+    mfma_substep(acc, a0, b0, a1, b1, aaddr(cs, 1), baddr(cs, 1));
+    mfma_substep(acc, a1, b1, a0, b0, aaddr(cs, 2), baddr(cs, 2));
+    mfma_substep(acc, a0, b0, a1, b1, aaddr(cs, 3), baddr(cs, 3));
+    if (kt == kdiag) {
+      // cin(i, j) = b(j, i): row j of the b panel, k offset i - kt*BK (4 consecutive
+      // rows i of one accumulator group are 8 contiguous bytes of that row)
+      mfma_to_valu_wait();
+      const uint8_t* sb = smem + cs * V2_STAGEB + bbase;
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+          for (int rg = 0; rg < 4; ++rg) {
+            const int jl = fn * 32 + fr;  // row within this wave's b rows
+            const int kl = fm * 32 + rg * 8 + fh * 4;
+            const uint2 w = *(const uint2*)(sb + jl * V2_ROWB +
+                                            ((((kl >> 3) ^ (jl & 7))) << 4) + (kl & 7) * 2);
+            acc[fm][fn][rg * 4 + 0] += ratio * bf16_to_f32((bf16_t)(w.x & 0xffffu));
+            acc[fm][fn][rg * 4 + 1] += ratio * bf16_to_f32((bf16_t)(w.x >> 16));
+            acc[fm][fn][rg * 4 + 2] += ratio * bf16_to_f32((bf16_t)(w.y & 0xffffu));
+            acc[fm][fn][rg * 4 + 3] += ratio * bf16_to_f32((bf16_t)(w.y >> 16));
+          }
+      valu_to_mfma_wait();
+    }
+    wait_vmcnt0();
+    lds_barrier();
+    if (kt + 2 < KT) issue(kt + 2, cs);
+    mfma_substep(acc, a1, b1, a0, b0, aaddr(cs ^ 1, 0), baddr(cs ^ 1, 0));
+  }
+  mfma_to_valu_wait();
+
+  // ---- epilogue: stage through LDS, store 16-byte row chunks ----
+  bf16_t* T = (bf16_t*)smem;
+  const bool diag = MODE == MODE_SYRK && tm == tn;
+  const int row0w = wm * WM, col0w = wn * WN;  // wave origin within the tile
+  auto val = [&](int fm, int fn, int r) -> float {
+    const int64_t i = arow0 + row0w + fm * 32 + (r >> 2) * 8 + fh * 4 + (r & 3);
+    const int64_t j = brow0 + col0w + fn * 32 + fr;
+    return (i < g.Mv && j < g.Nv) ? alpha * acc[fm][fn][r] : 0.0f;
+  };
+  bf16_t* out = g.out ? (bf16_t*)g.out + (int64_t)bidx * g.so : nullptr;
+  bf16_t* out_t = g.out_t ? (bf16_t*)g.out_t + (int64_t)bidx * g.st : nullptr;
+  const int64_t ldt = MODE == MODE_SYRK ? g.ldo : g.ldt;
+  if (MODE == MODE_SYRK && !diag) out_t = out;  // mirror half of the symmetric output
+  const bool do_t = out_t != nullptr && !diag;
+  const bool do_o = out != nullptr;
+
+  if (do_t) {
+    // transposed stage: T[j][i], 4 consecutive i per lane -> one 8-byte write
+    lds_barrier();
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const int jl = col0w + fn * 32 + fr;
+          const int il = row0w + fm * 32 + rg * 8 + fh * 4;
+          uint2 w;
+          w.x = (uint32_t)f32_to_bf16(val(fm, fn, rg * 4)) |
+                ((uint32_t)f32_to_bf16(val(fm, fn, rg * 4 + 1)) << 16);
+          w.y = (uint32_t)f32_to_bf16(val(fm, fn, rg * 4 + 2)) |
+                ((uint32_t)f32_to_bf16(val(fm, fn, rg * 4 + 3)) << 16);
+          *(uint2*)(T + jl * V2_EP_PITCH + il) = w;
+        }
+    lds_barrier();
+#pragma unroll 4
+    for (int it = 0; it < 16; ++it) {
+      const int id = it * 512 + tid;
+      const int jl = id >> 5, c = (id & 31) * 8;
+      const uint4 w = *(const uint4*)(T + jl * V2_EP_PITCH + c);
+      *(uint4*)(out_t + (brow0 + jl) * ldt + arow0 + c) = w;
+    }
+  }
+  if (do_o) {
+    // row-major stage: T[i][j]
+    lds_barrier();
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int il = row0w + fm * 32 + (r >> 2) * 8 + fh * 4 + (r & 3);
+          const int jl = col0w + fn * 32 + fr;
+          T[il * V2_EP_PITCH + jl] = f32_to_bf16(val(fm, fn, r));
+        }
+    lds_barrier();
+#pragma unroll 4
+    for (int it = 0; it < 16; ++it) {
+      const int id = it * 512 + tid;
+      const int il = id >> 5, c = (id & 31) * 8;
+      uint4 w;
+      if (!diag || c >= il) {
+        w = *(const uint4*)(T + il * V2_EP_PITCH + c);
+      } else {
+        // diagonal tile, chunk reaching below the diagonal: those columns come from
+        // the computed (upper) element of the mirror position
+        uint16_t e[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          e[q] = (c + q < il) ? T[(c + q) * V2_EP_PITCH + il] : T[il * V2_EP_PITCH + c + q];
+        __builtin_memcpy(&w, e, 16);
+      }
+      *(uint4*)(out + (arow0 + il) * g.ldo + brow0 + c) = w;
+    }
+  }
+}
+
+// Wave grid of the register-staged bf16 kernel (gemm_bf16_kernel), which serves the
+// masked gram_ path and products whose beta term has no alpha to fold into: 4 x 2
+// wavefronts, each 64 x 128, two waves per SIMD.
 #ifndef MUON_BF16_WGM
 #define MUON_BF16_WGM 4
 #endif
@@ -580,9 +721,15 @@ int reserve_bf16_lds() {
                          (const void*)gemm_bf16_kernel<MODE_GEMM, true, BF_WGM, BF_WGN>,
                          (const void*)gemm_bf16_kernel<MODE_SYRK, false, BF_WGM, BF_WGN>,
                          (const void*)gemm_bf16_kernel<MODE_SYRK, true, BF_WGM, BF_WGN>};
+    const void* ks2[2] = {(const void*)gemm_bf16_v2_kernel<MODE_GEMM>,
+                          (const void*)gemm_bf16_v2_kernel<MODE_SYRK>};
     status = 0;
     for (const void* k : ks)
       if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, BF_SMEM) !=
+          hipSuccess)
+        status = -1;
+    for (const void* k : ks2)
+      if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, V2_SMEM) !=
           hipSuccess)
         status = -1;
   });
@@ -593,7 +740,9 @@ int reserve_bf16_lds() {
 
 // Launch one batched product. `dtype` selects bf16 (256-tiles) or fp32 (128-tiles).
 // M/N are the (padded) row extents of the a/b operands; they must be multiples of
-// the tile unless `masked`.
+// the tile unless `masked`. The unmasked bf16 path (gemm_bf16_v2_kernel) takes the
+// beta term from the b operand: with beta != 0 the caller guarantees
+// cin(i, j) == b(j, i) (true of every product of the iteration).
 int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M, int64_t N,
                      int64_t K, const void* a, int64_t lda, int64_t sa, const void* b,
                      int64_t ldb, int64_t sb, const void* cin, int64_t ldc, int64_t sc,
@@ -658,7 +807,12 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
     hipLaunchKernelGGL((gemm_bf16_kernel<MODE_, MASK_, BF_WGM, BF_WGN>), grid, dim3(BF_NT), \
                        BF_SMEM, stream, g);                                                \
   } while (0)
-    if (mode == MODE_SYRK) {
+    if (!masked && (alpha != 0.0f || beta == 0.0f)) {
+      if (mode == MODE_SYRK)
+        hipLaunchKernelGGL(gemm_bf16_v2_kernel<MODE_SYRK>, grid, dim3(512), V2_SMEM, stream, g);
+      else
+        hipLaunchKernelGGL(gemm_bf16_v2_kernel<MODE_GEMM>, grid, dim3(512), V2_SMEM, stream, g);
+    } else if (mode == MODE_SYRK) {
       if (masked) LAUNCH_BF(MODE_SYRK, true); else LAUNCH_BF(MODE_SYRK, false);
     } else {
       if (masked) LAUNCH_BF(MODE_GEMM, true); else LAUNCH_BF(MODE_GEMM, false);
