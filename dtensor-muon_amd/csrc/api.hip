@@ -20,8 +20,9 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
 int muon_launch_prepass(int ntensors, void* const* grads, void* const* bufs, int gdt, int bdt,
                         int64_t nb, int64_t rows, int64_t cols, int64_t s_pitch,
                         int64_t s_mstride, float momentum, int nesterov, int maximize,
-                        int write_grad, int write_direct, const OrthLayout& L, void* ws,
-                        int wdt, int64_t mat0, hipStream_t s);
+                        int write_grad, int write_direct, void* direct, int64_t d_pitch,
+                        void* trans, const OrthLayout& L, void* ws, int wdt, int64_t mat0,
+                        hipStream_t s);
 int muon_launch_finalize(const OrthLayout& L, void* ws, int64_t batch, float prescale,
                          float eps, hipStream_t s);
 int muon_launch_momentum(int ntensors, void* const* grads, void* const* bufs, int gdt, int bdt,
@@ -29,6 +30,8 @@ int muon_launch_momentum(int ntensors, void* const* grads, void* const* bufs, in
                          int write_grad, hipStream_t s);
 int muon_launch_scale(const OrthLayout& L, void* x, int wdt, int64_t batch, const float* scale,
                       hipStream_t s);
+int muon_launch_scale_transpose(const OrthLayout& L, const void* x, void* xt, int wdt,
+                                int64_t batch, const float* scale, hipStream_t s);
 int muon_launch_postpass(int ntensors, void* const* params, const float* adj, int pdt,
                          const void* u, int udt, int64_t u_pitch, int64_t u_mstride, int64_t nb,
                          int64_t rows, int64_t cols, float wd, int cautious, hipStream_t s);
@@ -130,9 +133,8 @@ OrthLayout muon_orth_layout(int dtype, int64_t batch, int64_t rows, int64_t cols
   };
   const size_t xs = (size_t)(batch * L.m_pad * L.n_pad * L.es);
   const size_t as = (size_t)(batch * L.m_pad * L.m_pad * L.es);
-  L.off_x = take(xs);
-  L.off_xt0 = take(xs);
-  L.off_xt1 = take(xs);
+  L.off_x0 = take(xs);
+  L.off_x1 = take(xs);
   L.off_a = take(as);
   L.off_b = take(as);
   L.off_part = take((size_t)(batch * L.parts * 4));
@@ -199,11 +201,14 @@ int muon_orth_result(int dtype, int64_t batch, int64_t rows, int64_t cols, int s
     return MUON_ERR_ARG;
   }
   OrthLayout L = muon_orth_layout(dtype, batch, rows, cols);
+  // The iterate after `steps` GEMMs is in X[steps % 2]; a tall matrix's result is its
+  // transpose, which the last GEMM (or, for steps == 0, the scaling pass) writes into
+  // X[steps % 2] (X1 for steps == 0) with pitch m_pad.
   if (L.tall) {
-    *offset_bytes = (int64_t)((steps % 2) ? L.off_xt1 : L.off_xt0);
+    *offset_bytes = (int64_t)((steps == 0 || steps % 2) ? L.off_x1 : L.off_x0);
     *row_pitch = L.m_pad;
   } else {
-    *offset_bytes = (int64_t)L.off_x;
+    *offset_bytes = (int64_t)((steps % 2) ? L.off_x1 : L.off_x0);
     *row_pitch = L.n_pad;
   }
   *matrix_stride = L.m_pad * L.n_pad;
@@ -249,12 +254,15 @@ int muon_prepass(int ntensors, void* const* grads, void* const* bufs, int g_dtyp
   const int ges = g_dtype == MUON_DT_F32 ? 4 : 2, bes = buf_dtype == MUON_DT_F32 ? 4 : 2;
   const double per_elem = ges + (bufs ? 2.0 * bes : 0.0) + L.es + (write_back_grad ? ges : 0);
   Timed timed(MUON_K_PREPASS, per_elem * (double)ntensors * nb * rows * cols, s);
+  // X0 holds the wide iterate: the stored layout itself, or its transpose (tall)
+  char* x0 = (char*)ws + L.off_x0;
   for (int t0 = 0; t0 < ntensors; t0 += MUON_MAX_TENSORS) {
     const int cnt = std::min(MUON_MAX_TENSORS, ntensors - t0);
     int rc = muon_launch_prepass(cnt, grads + t0, bufs ? bufs + t0 : nullptr, g_dtype,
                                  buf_dtype, nb, rows, cols, cols, rows * cols, momentum,
-                                 nesterov, maximize, write_back_grad, 1, L, ws, ws_dtype,
-                                 (int64_t)t0 * nb, s);
+                                 nesterov, maximize, write_back_grad, L.tall ? 0 : 1,
+                                 L.tall ? nullptr : x0, L.n_pad, L.tall ? x0 : nullptr, L, ws,
+                                 ws_dtype, (int64_t)t0 * nb, s);
     if (rc != MUON_OK) return rc;
   }
   return MUON_OK;
@@ -284,24 +292,26 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
   }
   if (rc != MUON_OK) return rc;
   const float* scale = (const float*)(w + L.off_scale);
-  char* X = w + L.off_x;
-  char* XT[2] = {w + L.off_xt0, w + L.off_xt1};
+  char* X[2] = {w + L.off_x0, w + L.off_x1};
   char* A = w + L.off_a;
   char* B = w + L.off_b;
   const int64_t mp = L.m_pad, np = L.n_pad;
   if (steps == 0) {
     Timed t(MUON_K_OTHER, 0.0, s);
-    return muon_launch_scale(L, L.tall ? XT[0] : X, ws_dtype, batch, scale, s);
+    if (L.tall) return muon_launch_scale_transpose(L, X[0], X[1], ws_dtype, batch, scale, s);
+    return muon_launch_scale(L, X[0], ws_dtype, batch, scale, s);
   }
   const double bm = (double)batch, md = (double)L.m, nd = (double)L.n;
   for (int it = 0; it < steps; ++it) {
     const float a = (float)coeffs[3 * it], b = (float)coeffs[3 * it + 1],
                 c = (float)coeffs[3 * it + 2];
     const bool first = it == 0, last = it == steps - 1;
+    char* Xc = X[it & 1];
+    char* Xn = X[(it + 1) & 1];
     // A = X X^T (the first iteration folds the Frobenius prescale s in as s^2)
     {
     Timed t(MUON_K_SYRK_XX, bm * md * (md + 1) * nd, s);
-    rc = muon_launch_gemm(ws_dtype, MODE_SYRK, false, batch, mp, mp, np, X, np, mp * np, X, np,
+    rc = muon_launch_gemm(ws_dtype, MODE_SYRK, false, batch, mp, mp, np, Xc, np, mp * np, Xc, np,
                           mp * np, nullptr, 0, 0, A, mp, mp * mp, nullptr, 0, 0, L.m, L.m, 1.0f,
                           0.0f, scale, first ? 2 : 0, s);
     }
@@ -314,15 +324,15 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
                           nullptr, 0, s);
     }
     if (rc != MUON_OK) return rc;
-    // X' = a*X + B X, as B(i, k) . X^T(j, k); X is updated in place (its elements are
-    // only touched by the epilogue of their own tile), X^T ping-pongs.
-    void* out = (last && L.tall) ? nullptr : (void*)X;
-    void* out_t = (last && !L.tall) ? nullptr : (void*)XT[(it + 1) & 1];
+    // X' = a*X + B X into the other buffer (every tile reads whole columns of X); the
+    // last iteration of a tall matrix stores X'^T, its stored layout
+    void* out = (last && L.tall) ? nullptr : (void*)Xn;
+    void* out_t = (last && L.tall) ? (void*)Xn : nullptr;
     {
     Timed t(MUON_K_GEMM_BX, bm * 2.0 * md * md * nd, s);
-    rc = muon_launch_gemm(ws_dtype, MODE_GEMM, false, batch, mp, np, mp, B, mp, mp * mp,
-                          XT[it & 1], mp, np * mp, X, np, mp * np, out, np, mp * np, out_t, mp,
-                          np * mp, L.m, L.n, 1.0f, a, scale, first ? 1 : 0, s);
+    rc = muon_launch_gemm(ws_dtype, MODE_GEMM, false, batch, mp, np, mp, B, mp, mp * mp, Xc, np,
+                          mp * np, Xc, np, mp * np, out, np, mp * np, out_t, mp, np * mp, L.m,
+                          L.n, 1.0f, a, scale, first ? 1 : 0, s);
     }
     if (rc != MUON_OK) return rc;
   }
@@ -418,7 +428,9 @@ int muon_lp_prepass(int ntensors, void* const* grads, int g_dtype, void* const* 
   OrthLayout L = muon_orth_layout(ws_dtype, ws_batch, rows, cols);
   hipStream_t s = (hipStream_t)stream;
   char* w = (char*)ws;
-  char* direct = w + (L.tall ? L.off_xt0 : L.off_x);
+  // the stored-layout X goes to X0 (wide) or, for a tall matrix, to X1 (n_pad x m_pad)
+  // from where the second pass below transposes it into X0
+  char* direct = w + (L.tall ? L.off_x1 : L.off_x0);
   const int64_t d_pitch = L.tall ? L.m_pad : L.n_pad;
   const int64_t mst = L.m_pad * L.n_pad;
   {
@@ -435,16 +447,18 @@ int muon_lp_prepass(int ntensors, void* const* grads, int g_dtype, void* const* 
   }
   }
   Timed timed_t(MUON_K_OTHER, 0.0, s);
-  // Second layout and norm partials from the stored-layout X just written: a plain
-  // (no momentum) prepass that reads the valid region of the workspace itself and
-  // rewrites only its padding.
+  // Norm partials (and, tall, the transpose into X0) from the stored-layout X just
+  // written: a plain (no momentum) prepass reading the valid region of the workspace;
+  // for a wide matrix it rewrites only the padding of X0 in place.
   const int64_t nmat = (int64_t)ntensors * nb;
+  char* x0 = w + L.off_x0;
   for (int64_t m0 = 0; m0 < nmat; m0 += MUON_MAX_TENSORS) {
     const int cnt = (int)std::min<int64_t>(MUON_MAX_TENSORS, nmat - m0);
     void* srcs[MUON_MAX_TENSORS];
     for (int i = 0; i < cnt; ++i) srcs[i] = direct + (m0 + i) * mst * L.es;
     rc = muon_launch_prepass(cnt, srcs, nullptr, MUON_DT_BF16, MUON_DT_BF16, 1, rows, cols,
-                             d_pitch, mst, 0.0f, 0, 0, 0, 2, L, ws, ws_dtype, m0, s);
+                             d_pitch, mst, 0.0f, 0, 0, 0, L.tall ? 0 : 2, L.tall ? nullptr : x0,
+                             L.n_pad, L.tall ? x0 : nullptr, L, ws, ws_dtype, m0, s);
     if (rc != MUON_OK) return rc;
   }
   return MUON_OK;

@@ -190,6 +190,8 @@ void muon_set_error(const char* fmt, ...);
   } while (0)
 
 // Workspace layout shared by the prepass, iteration and postpass entry points.
+// X0/X1: the wide iterate (m_pad x n_pad, row-major), ping-ponged by the GEMM; the
+// result of a tall matrix is written transposed (n_pad x m_pad) into one of them.
 struct OrthLayout {
   int64_t rows, cols;  // stored (param) matrix shape
   int64_t m, n;        // m = min, n = max: the iteration runs on the wide m x n matrix
@@ -198,7 +200,7 @@ struct OrthLayout {
   int es;              // element size of the iteration dtype
   int64_t batch;       // capacity in matrices
   int64_t parts;       // norm partials per matrix
-  size_t off_x, off_xt0, off_xt1, off_a, off_b, off_part, off_scale, total;
+  size_t off_x0, off_x1, off_a, off_b, off_part, off_scale, total;
 };
 
 OrthLayout muon_orth_layout(int dtype, int64_t batch, int64_t rows, int64_t cols);

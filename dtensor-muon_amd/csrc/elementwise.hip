@@ -117,11 +117,14 @@ __global__ __launch_bounds__(256) void prepass_kernel(PrepassArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) xv[e] = 0.0f;
       }
+      if (a.trans) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) tile[rl][cl + e] = xv[e];
+        for (int e = 0; e < 8; ++e) tile[rl][cl + e] = xv[e];
+      }
       if (a.write_direct == 1 || (a.write_direct == 2 && !valid))
         Vec8<WDT>::store(a.direct, (int64_t)mat * a.d_mstride + r * a.d_pitch + c, xv);
     }
+    if (a.trans) {
     __syncthreads();
 #pragma unroll
     for (int rp = 0; rp < TILE / RPP; ++rp) {
@@ -130,6 +133,7 @@ __global__ __launch_bounds__(256) void prepass_kernel(PrepassArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) tv[e] = tile[cl + e][cc];
       Vec8<WDT>::store(a.trans, (int64_t)mat * a.t_mstride + (c0 + cc) * a.t_pitch + r0 + cl, tv);
+    }
     }
   } else {
 #pragma unroll
@@ -151,7 +155,7 @@ __global__ __launch_bounds__(256) void prepass_kernel(PrepassArgs a) {
         ss += x * x;
       }
       xv[e] = x;
-      tile[rl][cl + e] = x;
+      if (a.trans) tile[rl][cl + e] = x;
     }
     if (a.write_direct) {
       const int64_t o = (int64_t)mat * a.d_mstride + r * a.d_pitch + c0 + cl;
@@ -160,6 +164,7 @@ __global__ __launch_bounds__(256) void prepass_kernel(PrepassArgs a) {
         if (a.write_direct == 1 || !valid[e]) Elem<WDT>::store(a.direct, o + e, xv[e]);
     }
   }
+  if (a.trans) {
   __syncthreads();
   // Transposed layout: row (c0 + cc) of the transpose holds column cc of the tile.
 #pragma unroll
@@ -168,6 +173,7 @@ __global__ __launch_bounds__(256) void prepass_kernel(PrepassArgs a) {
     const int64_t o = (int64_t)mat * a.t_mstride + (c0 + cc) * a.t_pitch + r0 + cl;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) Elem<WDT>::store(a.trans, o + e, tile[cl + e][cc]);
+  }
   }
   }
   ss = warp_sum(ss);
@@ -230,6 +236,29 @@ __global__ __launch_bounds__(256) void scale_kernel(void* x, int64_t mstride,
        i += (int64_t)gridDim.x * 256) {
     const int64_t idx = b * mstride + i;
     Elem<WDT>::store(x, idx, Elem<WDT>::load(x, idx) * s);
+  }
+}
+
+// xt[b] = transpose(x[b]) * scale[b] over the padded extents (steps == 0 path of a tall
+// matrix, whose stored layout is the transpose of the wide iterate x).
+template <int WDT>
+__global__ __launch_bounds__(256) void scale_transpose_kernel(const void* x, void* xt,
+                                                              int64_t m_pad, int64_t n_pad,
+                                                              const float* scale) {
+  __shared__ float tile[TILE][TILE + 1];
+  const int64_t b = blockIdx.y;
+  const int64_t tiles_c = n_pad / TILE;
+  const int64_t r0 = (blockIdx.x / tiles_c) * TILE, c0 = (blockIdx.x % tiles_c) * TILE;
+  const int64_t base = b * m_pad * n_pad;
+  const float s = scale[b];
+  for (int i = threadIdx.x; i < TILE * TILE; i += 256) {
+    const int r = i / TILE, c = i % TILE;
+    tile[r][c] = Elem<WDT>::load(x, base + (r0 + r) * n_pad + c0 + c) * s;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < TILE * TILE; i += 256) {
+    const int r = i / TILE, c = i % TILE;  // row r of the transposed tile = column r
+    Elem<WDT>::store(xt, base + (c0 + r) * m_pad + r0 + c, tile[c][r]);
   }
 }
 
@@ -402,8 +431,9 @@ int launch_extract_o(int odt, const void* src, int64_t pitch, int64_t mstride, v
 int muon_launch_prepass(int ntensors, void* const* grads, void* const* bufs, int gdt, int bdt,
                         int64_t nb, int64_t rows, int64_t cols, int64_t s_pitch,
                         int64_t s_mstride, float momentum, int nesterov, int maximize,
-                        int write_grad, int write_direct, const OrthLayout& L, void* ws,
-                        int wdt, int64_t mat0, hipStream_t s) {
+                        int write_grad, int write_direct, void* direct, int64_t d_pitch,
+                        void* trans, const OrthLayout& L, void* ws, int wdt, int64_t mat0,
+                        hipStream_t s) {
   PrepassArgs a;
   for (int i = 0; i < ntensors; ++i) {
     a.grads[i] = grads[i];
@@ -418,11 +448,10 @@ int muon_launch_prepass(int ntensors, void* const* grads, void* const* bufs, int
   const int64_t rows_pad = L.tall ? L.n_pad : L.m_pad;
   const int64_t cols_pad = L.tall ? L.m_pad : L.n_pad;
   const int64_t mst = L.m_pad * L.n_pad;
-  char* direct = w + (L.tall ? L.off_xt0 : L.off_x);
-  char* trans = w + (L.tall ? L.off_x : L.off_xt0);
-  a.direct = direct + mat0 * mst * L.es;
-  a.trans = trans + mat0 * mst * L.es;
-  a.d_pitch = cols_pad;
+  a.direct = direct ? (char*)direct + mat0 * mst * L.es : nullptr;
+  a.trans = trans ? (char*)trans + mat0 * mst * L.es : nullptr;
+  if (write_direct && !direct) write_direct = 0;
+  a.d_pitch = d_pitch;
   a.t_pitch = rows_pad;
   a.d_mstride = mst;
   a.t_mstride = mst;
@@ -506,6 +535,19 @@ int muon_launch_finalize(const OrthLayout& L, void* ws, int64_t batch, float pre
                      (const float*)(w + L.off_part), L.parts, (float*)(w + L.off_scale),
                      prescale, eps);
   MUON_CHECK_LAUNCH("finalize_scale");
+  return MUON_OK;
+}
+
+int muon_launch_scale_transpose(const OrthLayout& L, const void* x, void* xt, int wdt,
+                                int64_t batch, const float* scale, hipStream_t s) {
+  dim3 grid((unsigned)((L.m_pad / TILE) * (L.n_pad / TILE)), (unsigned)batch);
+  if (wdt == MUON_DT_BF16)
+    hipLaunchKernelGGL((scale_transpose_kernel<MUON_DT_BF16>), grid, dim3(256), 0, s, x, xt,
+                       L.m_pad, L.n_pad, scale);
+  else
+    hipLaunchKernelGGL((scale_transpose_kernel<MUON_DT_F32>), grid, dim3(256), 0, s, x, xt,
+                       L.m_pad, L.n_pad, scale);
+  MUON_CHECK_LAUNCH("scale_transpose");
   return MUON_OK;
 }
 

@@ -1,16 +1,16 @@
-// Batched "NT" matrix products on CDNA4 MFMA for the Newton-Schulz / Polar Express
-// iteration:  C[b](i, j) = alpha * sum_k A[b](i, k) * B[b](j, k) + beta * Cin[b](i, j)
-// Both operands are K-contiguous rows, which is the native MFMA operand layout.
+// Batched matrix products on CDNA4 MFMA for the Newton-Schulz / Polar Express
+// iteration.
 //
-//  * SYRK mode  (A == B, upper-triangle tiles only, mirrored store): the Gram
+//  * SYRK mode ("NT": C(i, j) = alpha * sum_k A(i, k) A(j, k) + beta * Cin(i, j), both
+//    operands K-contiguous rows, upper-triangle tiles only, mirrored store): the Gram
 //    products X X^T and A A (A symmetric) of pe_loop_triton / ns_loop_triton
 //    (polar_express.py:98-104, newton_schulz.py:105-112; Triton gram_nd,
 //    gram.py:21-106). The polynomial combination B = b*A + c*A^2 rides in the
 //    epilogue (beta*Cin with Cin = A).
-//  * GEMM mode: X' = a*X + B X (polar_express.py:109-110) with B symmetric, computed
-//    as sum_k B(i, k) X^T(j, k); the epilogue writes X' row-major and, optionally,
-//    its transpose, which the next iteration's GEMM consumes as its K-contiguous
-//    operand.
+//  * GEMM mode ("NN": C(i, j) = alpha * sum_k B(i, k) X(k, j) + beta * X(i, j)):
+//    X' = a*X + B X (polar_express.py:109-110) with X in its own row-major layout
+//    as the second operand; the epilogue writes X' row-major (into the other of two
+//    ping-pong buffers) or, for the last iteration of a tall matrix, transposed.
 //
 // Operands live in workspaces whose extents are padded to the tile size and whose
 // padding is rewritten as zeros by every producer, so the K loop and the stores
@@ -61,7 +61,7 @@ MUON_DEVICE void map_tile(const GemmArgs& g, int mode, int& bidx, int& tm, int& 
     tm = r;
     tn = r + t;
   } else {
-    const int GM = 4;
+    const int GM = 8;  // 8 tile rows per group: measured best for the GEMM stores (X^T rows stay adjacent)
     int TN = g.tiles_n, TM = g.tiles_m;
     int group = t / (GM * TN);
     int first = group * GM;
@@ -316,8 +316,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_bf16_kernel(GemmArgs g
 
 // ----------------------------------------------------------------------------------
 // fp32: 128 x 128 x 16 tile, 4 wavefronts in 2 x 2, each 64 x 64 (2 x 2 MFMA
-// 32x32x2 f32 blocks). Used for the fp32 iteration mode and fp32 gram_.
-constexpr int F_BM = 128, F_BN = 128, F_BK = 16, F_LDSP = F_BK + 4;
+// 32x32x2 f32 blocks). Used for the fp32 iteration mode and fp32 gram_. In GEMM (NN)
+// mode the b panel is staged as rows k of X (pitch F_XP); the MFMA takes one value
+// per lane, so no transpose is needed.
+constexpr int F_BM = 128, F_BN = 128, F_BK = 16, F_LDSP = F_BK + 4, F_XP = F_BN + 4;
+static_assert(F_BK * F_XP <= F_BN * F_LDSP, "fp32 X panel fits the b buffer");
 
 template <int MODE, bool MASKED>
 __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
@@ -341,7 +344,10 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
       const int r = c >> 2, cc = (c & 3) * 4;
       if (!MASKED) {
         ra[q] = *(const float4*)(A + (arow0 + r) * g.lda + k0 + cc);
-        rb[q] = *(const float4*)(B + (brow0 + r) * g.ldb + k0 + cc);
+        if (MODE == MODE_GEMM)
+          rb[q] = *(const float4*)(B + (k0 + (c >> 5)) * g.ldb + brow0 + (c & 31) * 4);
+        else
+          rb[q] = *(const float4*)(B + (brow0 + r) * g.ldb + k0 + cc);
       } else {
         float ta[4], tb[4];
 #pragma unroll
@@ -362,7 +368,10 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
       const int c = q * 256 + tid;
       const int r = c >> 2, cc = (c & 3) * 4;
       *(float4*)(&As[buf][r * F_LDSP + cc]) = ra[q];
-      *(float4*)(&Bs[buf][r * F_LDSP + cc]) = rb[q];
+      if (MODE == MODE_GEMM)
+        *(float4*)(&Bs[buf][(c >> 5) * F_XP + (c & 31) * 4]) = rb[q];
+      else
+        *(float4*)(&Bs[buf][r * F_LDSP + cc]) = rb[q];
     }
   };
 
@@ -388,7 +397,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
 #pragma unroll
       for (int f = 0; f < 2; ++f) {
         af[f] = As[cur][(wm * 64 + f * 32 + frow) * F_LDSP + ks * 2 + fk];
-        bfr[f] = Bs[cur][(wn * 64 + f * 32 + frow) * F_LDSP + ks * 2 + fk];
+        bfr[f] = MODE == MODE_GEMM ? Bs[cur][(ks * 2 + fk) * F_XP + wn * 64 + f * 32 + frow]
+                                   : Bs[cur][(wn * 64 + f * 32 + frow) * F_LDSP + ks * 2 + fk];
       }
 #pragma unroll
       for (int fm = 0; fm < 2; ++fm)
@@ -699,8 +709,289 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
   }
 }
 
+// ----------------------------------------------------------------------------------
+// bf16 X' = alpha * (B X + ratio * X) with X read in its own row-major layout.
+//
+// The a operand (B, rows i, k contiguous) is handled as in gemm_bf16_v2_kernel. The
+// b operand is X itself, whose rows are k: each K-tile stages a 64 x 256 panel
+// X[k][j] (rows of 512 B, 16-byte chunk c of row k stored at chunk c ^ ((k & 3) << 2))
+// and the MFMA fragments, which need 8 consecutive k of one column j per lane, come
+// from ds_read_b64_tr_b16: within a group of 16 lanes, lane r points at 4 consecutive
+// elements of row kb + r/4, columns jb + 4 (r % 4) .. +3, and lane i receives column
+// jb + i of rows kb .. kb+3. Two such reads (kb, kb + 4) fill one fragment. The
+// swizzle puts the four rows of one read in four different 64-byte bank groups.
+//
+// The MFMA takes the X fragment as its first operand, so an accumulator holds X'
+// transposed: lane l has row i = l % 32 and 4 consecutive columns j of a 32 x 32
+// block. Stores of X' are then 8-byte row pieces straight from registers, and the
+// beta term X(i, j .. j+3) is 8 contiguous bytes of row k = i of the X panel.
+// A transposed copy (the last iteration of a tall matrix) goes through LDS.
+// No X^T is kept in memory; X ping-pongs between two buffers because every tile
+// reads whole columns of X.
+constexpr int NN_XROWB = 512;                        // X panel row: 256 bf16
+constexpr int NN_ATILEB = 256 * V2_ROWB;             // B panel: 256 rows x 64 k
+constexpr int NN_XTILEB = V2_BK * NN_XROWB;          // X panel: 64 k x 256 j
+constexpr int NN_STAGEB = NN_ATILEB + NN_XTILEB;
+constexpr int NN_SMEM = (2 * NN_STAGEB > 256 * V2_EP_PITCH * 2) ? 2 * NN_STAGEB
+                                                                 : 256 * V2_EP_PITCH * 2;
+
+typedef __attribute__((ext_vector_type(4))) short i16x4;
+
+#define MUON_MFMA_NN(C, X, B) "v_mfma_f32_32x32x16_bf16 %[" #C "], %[" #X "], %[" #B "], %[" #C "]\n\t"
+// One k-substep of the NN product for a 64 x 128 wave tile: 8 MFMAs on the current
+// fragments (cb: B rows, cx: X columns), interleaved with the reads of the next:
+// nb0/nb1 (b128 at ba, ba + 4 KB) and the two halves of each X fragment (tr reads at
+// xa[f] + XO and xa[f] + XO + 2 KB).
+template <int XO>
+MUON_DEVICE void nn_substep(f32x16 (&acc)[2][4], const bf16x8_mfma (&cb)[2],
+                            const bf16x8_mfma (&cx)[4], bf16x8_mfma (&nb)[2], i16x4 (&nxl)[4],
+                            i16x4 (&nxh)[4], uint32_t ba, const uint32_t (&xa)[4]) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %[l0], %[x0] offset:%[o0]\n\t"
+      MUON_MFMA_NN(c00, cx0, cb0)
+      "ds_read_b64_tr_b16 %[h0], %[x0] offset:%[o1]\n\t"
+      MUON_MFMA_NN(c01, cx1, cb0)
+      "ds_read_b64_tr_b16 %[l1], %[x1] offset:%[o0]\n\t"
+      MUON_MFMA_NN(c02, cx2, cb0)
+      "ds_read_b64_tr_b16 %[h1], %[x1] offset:%[o1]\n\t"
+      MUON_MFMA_NN(c03, cx3, cb0)
+      "ds_read_b64_tr_b16 %[l2], %[x2] offset:%[o0]\n\t"
+      MUON_MFMA_NN(c10, cx0, cb1)
+      "ds_read_b64_tr_b16 %[h2], %[x2] offset:%[o1]\n\t"
+      "ds_read_b64_tr_b16 %[l3], %[x3] offset:%[o0]\n\t"
+      MUON_MFMA_NN(c11, cx1, cb1)
+      "ds_read_b64_tr_b16 %[h3], %[x3] offset:%[o1]\n\t"
+      "ds_read_b128 %[nb0], %[ba]\n\t"
+      MUON_MFMA_NN(c12, cx2, cb1)
+      "ds_read_b128 %[nb1], %[ba] offset:4096\n\t"
+      MUON_MFMA_NN(c13, cx3, cb1)
+      "s_waitcnt lgkmcnt(0)"
+      : [c00] "+v"(acc[0][0]), [c01] "+v"(acc[0][1]), [c02] "+v"(acc[0][2]),
+        [c03] "+v"(acc[0][3]), [c10] "+v"(acc[1][0]), [c11] "+v"(acc[1][1]),
+        [c12] "+v"(acc[1][2]), [c13] "+v"(acc[1][3]), [nb0] "=&v"(nb[0]), [nb1] "=&v"(nb[1]),
+        [l0] "=&v"(nxl[0]), [h0] "=&v"(nxh[0]), [l1] "=&v"(nxl[1]), [h1] "=&v"(nxh[1]),
+        [l2] "=&v"(nxl[2]), [h2] "=&v"(nxh[2]), [l3] "=&v"(nxl[3]), [h3] "=&v"(nxh[3])
+      : [cb0] "v"(cb[0]), [cb1] "v"(cb[1]), [cx0] "v"(cx[0]), [cx1] "v"(cx[1]),
+        [cx2] "v"(cx[2]), [cx3] "v"(cx[3]), [ba] "v"(ba), [x0] "v"(xa[0]), [x1] "v"(xa[1]),
+        [x2] "v"(xa[2]), [x3] "v"(xa[3]), [o0] "i"(XO), [o1] "i"(XO + 4 * NN_XROWB));
+}
+#undef MUON_MFMA_NN
+
+template <int XO>
+MUON_DEVICE void nn_frag_load(bf16x8_mfma (&nb)[2], i16x4 (&nxl)[4], i16x4 (&nxh)[4], uint32_t ba,
+                              const uint32_t (&xa)[4]) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %[l0], %[x0] offset:%[o0]\n\t"
+      "ds_read_b64_tr_b16 %[h0], %[x0] offset:%[o1]\n\t"
+      "ds_read_b64_tr_b16 %[l1], %[x1] offset:%[o0]\n\t"
+      "ds_read_b64_tr_b16 %[h1], %[x1] offset:%[o1]\n\t"
+      "ds_read_b64_tr_b16 %[l2], %[x2] offset:%[o0]\n\t"
+      "ds_read_b64_tr_b16 %[h2], %[x2] offset:%[o1]\n\t"
+      "ds_read_b64_tr_b16 %[l3], %[x3] offset:%[o0]\n\t"
+      "ds_read_b64_tr_b16 %[h3], %[x3] offset:%[o1]\n\t"
+      "ds_read_b128 %[nb0], %[ba]\n\t"
+      "ds_read_b128 %[nb1], %[ba] offset:4096\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : [nb0] "=&v"(nb[0]), [nb1] "=&v"(nb[1]), [l0] "=&v"(nxl[0]), [h0] "=&v"(nxh[0]),
+        [l1] "=&v"(nxl[1]), [h1] "=&v"(nxh[1]), [l2] "=&v"(nxl[2]), [h2] "=&v"(nxh[2]),
+        [l3] "=&v"(nxl[3]), [h3] "=&v"(nxh[3])
+      : [ba] "v"(ba), [x0] "v"(xa[0]), [x1] "v"(xa[1]), [x2] "v"(xa[2]), [x3] "v"(xa[3]),
+        [o0] "i"(XO), [o1] "i"(XO + 4 * NN_XROWB));
+}
+
+MUON_DEVICE void nn_join(bf16x8_mfma (&cx)[4], const i16x4 (&lo)[4], const i16x4 (&hi)[4]) {
+#pragma unroll
+  for (int f = 0; f < 4; ++f) {
+    const i16x4 l = lo[f], h = hi[f];
+    const __attribute__((ext_vector_type(8))) short v =
+        __builtin_shufflevector(l, h, 0, 1, 2, 3, 4, 5, 6, 7);
+    cx[f] = __builtin_bit_cast(bf16x8_mfma, v);
+  }
+}
+
+__global__ __launch_bounds__(512, 1) void gemm_bf16_nn_kernel(GemmArgs g) {
+  constexpr int NW = 8, WGN = 2, WM = 64, WN = 128, FM = 2, FN = 4;
+  constexpr int SPW = (NN_ATILEB / 1024) / NW;  // 1 KB load slabs per wave per operand
+  extern __shared__ __align__(16) uint8_t smem[];
+
+  int bidx, tm, tn;
+  map_tile(g, MODE_GEMM, bidx, tm, tn);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+  const bf16_t* A = (const bf16_t*)g.a + (int64_t)bidx * g.sa;
+  const bf16_t* X = (const bf16_t*)g.b + (int64_t)bidx * g.sb;
+  const int64_t arow0 = (int64_t)tm * 256, bcol0 = (int64_t)tn * 256;
+  const int lda_b = (int)(g.lda * 2), ldx_b = (int)(g.ldb * 2);
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(A + arow0 * g.lda), 0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(X + bcol0), 0, 0x7fffffff, 0x00020000);
+  // a slabs as in gemm_bf16_v2_kernel; X slab q*NW + wave = panel rows
+  // 2 (q*NW + wave) + {0, 1}: lane -> row lane/32, chunk position lane%32, which holds
+  // logical chunk (lane%32) ^ ((row & 3) << 2)
+  const int ra_in = wave * 8 + (lane >> 3);
+  const int voa = ra_in * lda_b + (((lane & 7) ^ (ra_in & 7)) << 4);
+  const int rx_in = wave * 2 + (lane >> 5);
+  const int vox = rx_in * ldx_b + (((lane & 31) ^ ((rx_in & 3) << 2)) << 4);
+  auto issue = [&](int kt, int st) {
+    uint8_t* sa = smem + st * NN_STAGEB;
+    uint8_t* sx = sa + NN_ATILEB;
+#pragma unroll
+    for (int q = 0; q < SPW; ++q) {
+      const int slab = q * NW + wave;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(sa + slab * 1024), 16, voa,
+                                               q * NW * 8 * lda_b + kt * V2_ROWB, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsx, (lds_ptr_t)(sx + slab * 1024), 16, vox,
+                                               (q * NW * 2 + kt * V2_BK) * ldx_b, 0, 0);
+    }
+  };
+
+  // B fragment reads (rows i, k contiguous) as in gemm_bf16_v2_kernel
+  const int fr = lane & 31, fh = lane >> 5;
+  int foff[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) foff[ks] = fr * V2_ROWB + (((ks * 2 + fh) ^ (fr & 7)) << 4);
+  const int abase = wm * WM * V2_ROWB;
+  // X fragment tr reads: group g = lane/16, r = lane%16 points at panel row
+  // 8 (g/2) + r/4 (+ 16 ks, + 4 for the high half), column jw + 32 f + 16 (g%2) + 4 (r%4)
+  const int tg = lane >> 4, tr = lane & 15, ts = tr >> 2;
+  uint32_t xoff[4];
+#pragma unroll
+  for (int f = 0; f < 4; ++f) {
+    const int chunk = wn * 16 + ((f ^ ts) << 2) + (tg & 1) * 2 + ((tr & 3) >> 1);
+    xoff[f] = NN_ATILEB + (8 * (tg >> 1) + ts) * NN_XROWB + chunk * 16 + (tr & 1) * 8;
+  }
+
+  float alpha = g.alpha, beta = g.beta;
+  if (g.scale_mode == 1) {
+    const float s = g.scale[bidx];
+    alpha *= s;
+    beta *= s;
+  }
+  const float ratio = beta != 0.0f ? beta / alpha : 0.0f;
+  const int kdiag = ratio != 0.0f ? (int)((arow0 + wm * WM) / V2_BK) : -1;
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int KT = (int)(g.K / V2_BK);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  auto baddr = [&](int st, int ks) -> uint32_t { return lds0 + st * NN_STAGEB + abase + foff[ks]; };
+  uint32_t xa[4];
+  auto set_xa = [&](int st) {
+#pragma unroll
+    for (int f = 0; f < 4; ++f) xa[f] = lds0 + st * NN_STAGEB + xoff[f];
+  };
+  bf16x8_mfma b0[FM], b1[FM], x0[FN], x1[FN];
+  i16x4 xl[FN], xh[FN];
+  issue(0, 0);
+  wait_vmcnt0();
+  lds_barrier();
+  if (KT > 1) issue(1, 1);
+  set_xa(0);
+  nn_frag_load<0>(b0, xl, xh, baddr(0, 0), xa);
+  nn_join(x0, xl, xh);
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cs = kt & 1;
+    set_xa(cs);
+    nn_substep<1 * 16 * NN_XROWB>(acc, b0, x0, b1, xl, xh, baddr(cs, 1), xa);
+    nn_join(x1, xl, xh);
+    nn_substep<2 * 16 * NN_XROWB>(acc, b1, x1, b0, xl, xh, baddr(cs, 2), xa);
+    nn_join(x0, xl, xh);
+    nn_substep<3 * 16 * NN_XROWB>(acc, b0, x0, b1, xl, xh, baddr(cs, 3), xa);
+    nn_join(x1, xl, xh);
+    if (kt == kdiag) {
+      // X(i, j..j+3) for accumulator (fm, fn, rg): panel row k = fm*32 + lane%32,
+      // columns jw + 32 fn + 8 rg + 4 (lane/32)
+      mfma_to_valu_wait();
+      const uint8_t* sx = smem + cs * NN_STAGEB + NN_ATILEB;
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+          for (int rg = 0; rg < 4; ++rg) {
+            const int kl = fm * 32 + fr;
+            const int jl = wn * WN + fn * 32 + rg * 8 + fh * 4;
+            const uint2 w = *(const uint2*)(sx + kl * NN_XROWB +
+                                            (((jl >> 3) ^ ((kl & 3) << 2)) << 4) + (jl & 7) * 2);
+            acc[fm][fn][rg * 4 + 0] += ratio * bf16_to_f32((bf16_t)(w.x & 0xffffu));
+            acc[fm][fn][rg * 4 + 1] += ratio * bf16_to_f32((bf16_t)(w.x >> 16));
+            acc[fm][fn][rg * 4 + 2] += ratio * bf16_to_f32((bf16_t)(w.y & 0xffffu));
+            acc[fm][fn][rg * 4 + 3] += ratio * bf16_to_f32((bf16_t)(w.y >> 16));
+          }
+      valu_to_mfma_wait();
+    }
+    wait_vmcnt0();
+    lds_barrier();
+    if (kt + 2 < KT) issue(kt + 2, cs);
+    set_xa(cs ^ 1);
+    nn_substep<0>(acc, b1, x1, b0, xl, xh, baddr(cs ^ 1, 0), xa);
+    nn_join(x0, xl, xh);
+  }
+  mfma_to_valu_wait();
+
+  // ---- epilogue: accumulator (fm, fn, rg) holds X'(i, j .. j+3) ----
+  bf16_t* out = g.out ? (bf16_t*)g.out + (int64_t)bidx * g.so : nullptr;
+  auto packed = [&](int fm, int fn, int rg, int64_t i, int64_t j) -> uint2 {
+    float v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      v[q] = (i < g.Mv && j + q < g.Nv) ? alpha * acc[fm][fn][rg * 4 + q] : 0.0f;
+    uint2 w;
+    w.x = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+    w.y = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+    return w;
+  };
+  if (out) {
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const int64_t i = arow0 + wm * WM + fm * 32 + fr;
+          const int64_t j = bcol0 + wn * WN + fn * 32 + rg * 8 + fh * 4;
+          *(uint2*)(out + i * g.ldo + j) = packed(fm, fn, rg, i, j);
+        }
+  }
+  if (g.out_t) {
+    // transposed copy through a row-major LDS tile T[i][j]
+    bf16_t* out_t = (bf16_t*)g.out_t + (int64_t)bidx * g.st;
+    bf16_t* T = (bf16_t*)smem;
+    lds_barrier();
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const int il = wm * WM + fm * 32 + fr;
+          const int jl = wn * WN + fn * 32 + rg * 8 + fh * 4;
+          *(uint2*)(T + il * V2_EP_PITCH + jl) = packed(fm, fn, rg, arow0 + il, bcol0 + jl);
+        }
+    lds_barrier();
+#pragma unroll 4
+    for (int it = 0; it < 16; ++it) {
+      const int id = it * 512 + tid;
+      const int jl = id >> 5, c = (id & 31) * 8;
+      uint16_t e[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) e[q] = T[(c + q) * V2_EP_PITCH + jl];
+      uint4 w;
+      __builtin_memcpy(&w, e, 16);
+      *(uint4*)(out_t + (bcol0 + jl) * g.ldt + arow0 + c) = w;
+    }
+  }
+}
+
 // Wave grid of the register-staged bf16 kernel (gemm_bf16_kernel), which serves the
-// masked gram_ path and products whose beta term has no alpha to fold into: 4 x 2
+// masked gram_ path and SYRKs whose beta term has no alpha to fold into: 4 x 2
 // wavefronts, each 64 x 128, two waves per SIMD.
 #ifndef MUON_BF16_WGM
 #define MUON_BF16_WGM 4
@@ -717,21 +1008,19 @@ int reserve_bf16_lds() {
   static int status = -1;
   static std::once_flag once;
   std::call_once(once, [] {
-    const void* ks[4] = {(const void*)gemm_bf16_kernel<MODE_GEMM, false, BF_WGM, BF_WGN>,
-                         (const void*)gemm_bf16_kernel<MODE_GEMM, true, BF_WGM, BF_WGN>,
-                         (const void*)gemm_bf16_kernel<MODE_SYRK, false, BF_WGM, BF_WGN>,
+    const void* ks[2] = {(const void*)gemm_bf16_kernel<MODE_SYRK, false, BF_WGM, BF_WGN>,
                          (const void*)gemm_bf16_kernel<MODE_SYRK, true, BF_WGM, BF_WGN>};
-    const void* ks2[2] = {(const void*)gemm_bf16_v2_kernel<MODE_GEMM>,
-                          (const void*)gemm_bf16_v2_kernel<MODE_SYRK>};
     status = 0;
     for (const void* k : ks)
       if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, BF_SMEM) !=
           hipSuccess)
         status = -1;
-    for (const void* k : ks2)
-      if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, V2_SMEM) !=
-          hipSuccess)
-        status = -1;
+    if (hipFuncSetAttribute((const void*)gemm_bf16_v2_kernel<MODE_SYRK>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, V2_SMEM) != hipSuccess)
+      status = -1;
+    if (hipFuncSetAttribute((const void*)gemm_bf16_nn_kernel,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, NN_SMEM) != hipSuccess)
+      status = -1;
   });
   return status;
 }
@@ -739,10 +1028,11 @@ int reserve_bf16_lds() {
 }  // namespace
 
 // Launch one batched product. `dtype` selects bf16 (256-tiles) or fp32 (128-tiles).
-// M/N are the (padded) row extents of the a/b operands; they must be multiples of
-// the tile unless `masked`. The unmasked bf16 path (gemm_bf16_v2_kernel) takes the
-// beta term from the b operand: with beta != 0 the caller guarantees
-// cin(i, j) == b(j, i) (true of every product of the iteration).
+// M/N are the (padded) output extents; they must be multiples of the tile unless
+// `masked`. SYRK: a and b are the same K-contiguous rows. GEMM (NN): b is the
+// K x N row-major operand (row pitch ldb) and the beta term reads cin = b's first
+// M rows (cin(i, j) = b(i, j), true of X' = a X + B X); the bf16 kernels take it from
+// the staged operand panels. Masked (arbitrary-extent) launches exist for SYRK only.
 int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M, int64_t N,
                      int64_t K, const void* a, int64_t lda, int64_t sa, const void* b,
                      int64_t ldb, int64_t sb, const void* cin, int64_t ldc, int64_t sc,
@@ -786,6 +1076,17 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
                    (long long)N, (long long)K);
     return MUON_ERR_SHAPE;
   }
+  if (masked && mode != MODE_SYRK) {
+    muon_set_error("gemm: masked launches are SYRK only");
+    return MUON_ERR_ARG;
+  }
+  // the bf16 kernels address one matrix's operands with 32-bit byte offsets
+  const int64_t es = dtype == MUON_DT_BF16 ? 2 : 4;
+  if (std::max(M * lda, (mode == MODE_SYRK ? M : K) * ldb) * es >= (int64_t)0x7fffffff) {
+    muon_set_error("gemm: operand of %lld x %lld elements exceeds the 2 GiB per-matrix limit",
+                   (long long)std::max(M, K), (long long)std::max(lda, ldb));
+    return MUON_ERR_SHAPE;
+  }
   if (mode == MODE_SYRK)
     g.tiles_per_batch = g.tiles_m * (g.tiles_m + 1) / 2;
   else
@@ -807,15 +1108,16 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
     hipLaunchKernelGGL((gemm_bf16_kernel<MODE_, MASK_, BF_WGM, BF_WGN>), grid, dim3(BF_NT), \
                        BF_SMEM, stream, g);                                                \
   } while (0)
-    if (!masked && (alpha != 0.0f || beta == 0.0f)) {
-      if (mode == MODE_SYRK)
-        hipLaunchKernelGGL(gemm_bf16_v2_kernel<MODE_SYRK>, grid, dim3(512), V2_SMEM, stream, g);
-      else
-        hipLaunchKernelGGL(gemm_bf16_v2_kernel<MODE_GEMM>, grid, dim3(512), V2_SMEM, stream, g);
-    } else if (mode == MODE_SYRK) {
-      if (masked) LAUNCH_BF(MODE_SYRK, true); else LAUNCH_BF(MODE_SYRK, false);
+    if (mode == MODE_GEMM) {
+      if (alpha == 0.0f) {
+        muon_set_error("gemm: alpha must be nonzero");
+        return MUON_ERR_ARG;
+      }
+      hipLaunchKernelGGL(gemm_bf16_nn_kernel, grid, dim3(512), NN_SMEM, stream, g);
+    } else if (!masked && (alpha != 0.0f || beta == 0.0f)) {
+      hipLaunchKernelGGL(gemm_bf16_v2_kernel<MODE_SYRK>, grid, dim3(512), V2_SMEM, stream, g);
     } else {
-      if (masked) LAUNCH_BF(MODE_GEMM, true); else LAUNCH_BF(MODE_GEMM, false);
+      if (masked) LAUNCH_BF(MODE_SYRK, true); else LAUNCH_BF(MODE_SYRK, false);
     }
 #undef LAUNCH_BF
   } else if (dtype == MUON_DT_F32) {
@@ -825,10 +1127,7 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
       else
         hipLaunchKernelGGL((gemm_f32_kernel<MODE_SYRK, false>), grid, block, 0, stream, g);
     } else {
-      if (masked)
-        hipLaunchKernelGGL((gemm_f32_kernel<MODE_GEMM, true>), grid, block, 0, stream, g);
-      else
-        hipLaunchKernelGGL((gemm_f32_kernel<MODE_GEMM, false>), grid, block, 0, stream, g);
+      hipLaunchKernelGGL((gemm_f32_kernel<MODE_GEMM, false>), grid, block, 0, stream, g);
     }
   } else {
     muon_set_error("gemm: unsupported dtype %d", dtype);

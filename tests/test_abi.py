@@ -42,7 +42,8 @@ def test_workspace_size_formula():
     x = 2 * 256 * 512 * 2
     a = 2 * 256 * 256 * 2
     parts = 2 * (256 // 64) * (512 // 64) * 4
-    assert nbytes == 3 * x + 2 * a + parts + 256
+    # two ping-pong copies of the wide iterate, A, B, norm partials, per-matrix scale
+    assert nbytes == 2 * x + 2 * a + parts + 256
     assert lib.muon_orth_workspace_bytes(_lib.DT_BF16, 1, 300, 130) < nbytes
     assert lib.muon_orth_workspace_bytes(7, 1, 4, 4) == -1
     assert lib.muon_orth_workspace_bytes(_lib.DT_F32, 1, 0, 4) == -1
@@ -51,12 +52,21 @@ def test_workspace_size_formula():
 def test_result_location_follows_orientation():
     lib = _lib.load()
     off, pitch, mst = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    x1 = 4 * 256 * 512 * 2  # byte offset of the second iterate buffer
+    # wide: X[steps % 2] in the wide layout
     assert lib.muon_orth_result(_lib.DT_BF16, 4, 100, 300, 5, off, pitch, mst) == 0
-    assert off.value == 0 and pitch.value == 512 and mst.value == 256 * 512
+    assert off.value == x1 and pitch.value == 512 and mst.value == 256 * 512
+    assert lib.muon_orth_result(_lib.DT_BF16, 4, 100, 300, 4, off, pitch, mst) == 0
+    assert off.value == 0 and pitch.value == 512
+    assert lib.muon_orth_result(_lib.DT_BF16, 4, 100, 300, 0, off, pitch, mst) == 0
+    assert off.value == 0
+    # tall: the transposed result, pitch m_pad, in X[steps % 2] (X1 for steps == 0)
     assert lib.muon_orth_result(_lib.DT_BF16, 4, 300, 100, 5, off, pitch, mst) == 0
-    tall_odd = off.value
+    assert off.value == x1 and pitch.value == 256
     assert lib.muon_orth_result(_lib.DT_BF16, 4, 300, 100, 4, off, pitch, mst) == 0
-    assert pitch.value == 256 and off.value != tall_odd
+    assert off.value == 0 and pitch.value == 256
+    assert lib.muon_orth_result(_lib.DT_BF16, 4, 300, 100, 0, off, pitch, mst) == 0
+    assert off.value == x1
 
 
 @pytest.mark.parametrize(
