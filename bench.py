@@ -124,6 +124,21 @@ def cpu_baseline(config: str = "llama", min_seconds: float = 10.0) -> dict:
     }
 
 
+def _measured_traffic(kernel: str, config: str, lp):
+    """HBM bytes per dispatch of `kernel` from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by a 1 GiB copy), for the workload it was
+    measured on; None elsewhere."""
+    if config != "llama" or lp:
+        return None, None
+    path = os.path.join(ROOT, "profiles", "muon_step_llama3_8b_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        return data["kernels"][kernel]["traffic_bytes"], os.path.relpath(path, ROOT)
+    except (OSError, KeyError, ValueError):
+        return None, None
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -134,6 +149,8 @@ def main() -> None:
     ap.add_argument("--block-size", type=int, default=None)
     ap.add_argument("--strategy", default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 1 GiB device-to-device copy 5 times (PMC calibration)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -149,6 +166,16 @@ def main() -> None:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate_copy:
+        # A plain copy of known size: FETCH_SIZE / WRITE_SIZE of these dispatches give
+        # the counters' scale against exactly 1 GiB read and 1 GiB written.
+        src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": src.numel() * 2, "dispatches": 5}))
+        return
     shapes = _shapes(args.config)
     strategy = args.strategy or ("newton_schulz" if args.config == "moe" else "polar_express")
     print(f"[bench] config={args.config} tensors={len(shapes)} strategy={strategy} "
@@ -220,14 +247,16 @@ def main() -> None:
     gms, gn, gwork = kern["gemm_bx"]
     avg_ms = gms / max(gn, 1)
     achieved = (gwork / max(gn, 1)) / (avg_ms * 1e-3) / 1e12
+    traffic, traffic_src = _measured_traffic("gemm_bf16_nn_kernel", args.config, args.lp)
     roofline = {
         "bound": "mfma",
-        "kernel": "gemm_bf16_kernel<MODE_GEMM> (X' = a X + B X)",
+        "kernel": "gemm_bf16_nn_kernel (X' = a X + B X)",
         "achieved": round(achieved, 1),
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-        "traffic": None,
+        "traffic": traffic,
+        "traffic_source": traffic_src,
         "avg_launch_ms": round(avg_ms, 4),
         "flop_per_launch": gwork / max(gn, 1),
     }

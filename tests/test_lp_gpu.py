@@ -64,9 +64,10 @@ def test_qmap_matches_oracle():
 
 @pytest.mark.parametrize("fmt,cls", FORMATS)
 @pytest.mark.parametrize("nesterov,maximize", [(True, False), (False, False), (True, True)])
-def test_lp_prepass_codes_bit_exact_and_step(fmt, cls, nesterov, maximize):
+@pytest.mark.parametrize("shape", [(128, 96), (96, 128)])  # tall and wide workspace paths
+def test_lp_prepass_codes_bit_exact_and_step(fmt, cls, nesterov, maximize, shape):
     opt_cls = {"8bit": Muon8bit, "4bit": Muon4bit, "fp8": MuonFp8}[fmt]
-    shape, block = (128, 96), 256
+    block = 256
     gen = torch.Generator().manual_seed(1)
     p0 = torch.randn(shape, generator=gen)
     p = nn.Parameter(p0.clone().to(DEV))
