@@ -741,9 +741,9 @@ typedef __attribute__((ext_vector_type(4))) short i16x4;
 // One k-substep of the NN product for a 64 x 128 wave tile: 8 MFMAs on the current
 // fragments (cb: B rows, cx: X columns), two reads of the next fragments ahead of each
 // of the first five MFMAs (measured a few percent faster than one per MFMA):
-// nb0/nb1 (b128 at ba, ba + 4 KB) and the two halves of each X fragment (tr reads at
+// nb0/nb1 (b128 at ba, ba + BO) and the two halves of each X fragment (tr reads at
 // xa[f] + XO and xa[f] + XO + 2 KB).
-template <int XO>
+template <int XO, int BO = 32 * V2_ROWB>
 MUON_DEVICE void nn_substep(f32x16 (&acc)[2][4], const bf16x8_mfma (&cb)[2],
                             const bf16x8_mfma (&cx)[4], bf16x8_mfma (&nb)[2], i16x4 (&nxl)[4],
                             i16x4 (&nxh)[4], uint32_t ba, const uint32_t (&xa)[4]) {
@@ -761,7 +761,7 @@ MUON_DEVICE void nn_substep(f32x16 (&acc)[2][4], const bf16x8_mfma (&cb)[2],
       "ds_read_b64_tr_b16 %[h3], %[x3] offset:%[o1]\n\t"
       MUON_MFMA_NN(c03, cx3, cb0)
       "ds_read_b128 %[nb0], %[ba]\n\t"
-      "ds_read_b128 %[nb1], %[ba] offset:4096\n\t"
+      "ds_read_b128 %[nb1], %[ba] offset:%[bo]\n\t"
       MUON_MFMA_NN(c10, cx0, cb1)
       MUON_MFMA_NN(c11, cx1, cb1)
       MUON_MFMA_NN(c12, cx2, cb1)
@@ -774,11 +774,11 @@ MUON_DEVICE void nn_substep(f32x16 (&acc)[2][4], const bf16x8_mfma (&cb)[2],
         [l2] "=&v"(nxl[2]), [h2] "=&v"(nxh[2]), [l3] "=&v"(nxl[3]), [h3] "=&v"(nxh[3])
       : [cb0] "v"(cb[0]), [cb1] "v"(cb[1]), [cx0] "v"(cx[0]), [cx1] "v"(cx[1]),
         [cx2] "v"(cx[2]), [cx3] "v"(cx[3]), [ba] "v"(ba), [x0] "v"(xa[0]), [x1] "v"(xa[1]),
-        [x2] "v"(xa[2]), [x3] "v"(xa[3]), [o0] "i"(XO), [o1] "i"(XO + 4 * NN_XROWB));
+        [x2] "v"(xa[2]), [x3] "v"(xa[3]), [o0] "i"(XO), [o1] "i"(XO + 4 * NN_XROWB), [bo] "i"(BO));
 }
 #undef MUON_MFMA_NN
 
-template <int XO>
+template <int XO, int BO = 32 * V2_ROWB>
 MUON_DEVICE void nn_frag_load(bf16x8_mfma (&nb)[2], i16x4 (&nxl)[4], i16x4 (&nxh)[4], uint32_t ba,
                               const uint32_t (&xa)[4]) {
   asm volatile(
@@ -791,13 +791,13 @@ MUON_DEVICE void nn_frag_load(bf16x8_mfma (&nb)[2], i16x4 (&nxl)[4], i16x4 (&nxh
       "ds_read_b64_tr_b16 %[l3], %[x3] offset:%[o0]\n\t"
       "ds_read_b64_tr_b16 %[h3], %[x3] offset:%[o1]\n\t"
       "ds_read_b128 %[nb0], %[ba]\n\t"
-      "ds_read_b128 %[nb1], %[ba] offset:4096\n\t"
+      "ds_read_b128 %[nb1], %[ba] offset:%[bo]\n\t"
       "s_waitcnt lgkmcnt(0)"
       : [nb0] "=&v"(nb[0]), [nb1] "=&v"(nb[1]), [l0] "=&v"(nxl[0]), [h0] "=&v"(nxh[0]),
         [l1] "=&v"(nxl[1]), [h1] "=&v"(nxh[1]), [l2] "=&v"(nxl[2]), [h2] "=&v"(nxh[2]),
         [l3] "=&v"(nxl[3]), [h3] "=&v"(nxh[3])
       : [ba] "v"(ba), [x0] "v"(xa[0]), [x1] "v"(xa[1]), [x2] "v"(xa[2]), [x3] "v"(xa[3]),
-        [o0] "i"(XO), [o1] "i"(XO + 4 * NN_XROWB));
+        [o0] "i"(XO), [o1] "i"(XO + 4 * NN_XROWB), [bo] "i"(BO));
 }
 
 MUON_DEVICE void nn_join(bf16x8_mfma (&cx)[4], const i16x4 (&lo)[4], const i16x4 (&hi)[4]) {
