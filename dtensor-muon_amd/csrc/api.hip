@@ -38,6 +38,11 @@ int muon_launch_postpass(int ntensors, void* const* params, const float* adj, in
 int muon_launch_extract(const void* src, int wdt, int64_t pitch, int64_t mstride, void* dst,
                         int odt, int64_t rows, int64_t cols, int64_t batch, hipStream_t s);
 int muon_check_lp_format(int qformat, int64_t numel, int64_t block);
+int muon_launch_lp_prepass_tiled(int ntensors, void* const* grads, int gdt, void* const* codes,
+                                 void* const* scales, const float* qmap, int qf, int64_t block,
+                                 int64_t nb, int64_t rows, int64_t cols, float momentum,
+                                 int nesterov, int maximize, const OrthLayout& L, void* ws,
+                                 int64_t mat0, hipStream_t s);
 int muon_launch_lp_prepass(int ntensors, void* const* grads, int gdt, void* const* codes,
                            void* const* scales, const float* qmap, int qf, int64_t block,
                            int64_t nb, int64_t rows, int64_t cols, float momentum,
@@ -428,8 +433,25 @@ int muon_lp_prepass(int ntensors, void* const* grads, int g_dtype, void* const* 
   OrthLayout L = muon_orth_layout(ws_dtype, ws_batch, rows, cols);
   hipStream_t s = (hipStream_t)stream;
   char* w = (char*)ws;
-  // the stored-layout X goes to X0 (wide) or, for a tall matrix, to X1 (n_pad x m_pad)
-  // from where the second pass below transposes it into X0
+  {
+    // one pass writing X0 and the norm partials directly, when the shape allows it
+    const double ges = g_dtype == MUON_DT_F32 ? 4.0 : 2.0;
+    const double code_b = qformat == MUON_Q_4BIT ? 0.5 : 1.0;
+    const double per_elem = ges + 2.0 * code_b + 8.0 / (double)block + 2.0;
+    Timed timed(MUON_K_LP_PREPASS, per_elem * (double)ntensors * nb * rows * cols, s);
+    rc = MUON_OK;
+    for (int t0 = 0; t0 < ntensors && rc == MUON_OK; t0 += MUON_MAX_TENSORS) {
+      const int cnt = std::min(MUON_MAX_TENSORS, ntensors - t0);
+      rc = muon_launch_lp_prepass_tiled(cnt, grads + t0, g_dtype, codes + t0, scales + t0, qmap,
+                                        qformat, block, nb, rows, cols, momentum, nesterov,
+                                        maximize, L, ws, (int64_t)t0 * nb, s);
+      if (rc != MUON_OK && t0 > 0) return rc;  // shape checks are the same for every chunk
+    }
+    if (rc == MUON_OK) return MUON_OK;
+    if (rc != MUON_ERR_SHAPE) return rc;
+  }
+  // general path: the stored-layout X goes to X0 (wide) or, for a tall matrix, to X1
+  // (n_pad x m_pad) from where the second pass below transposes it into X0
   char* direct = w + (L.tall ? L.off_x1 : L.off_x0);
   const int64_t d_pitch = L.tall ? L.m_pad : L.n_pad;
   const int64_t mst = L.m_pad * L.n_pad;

@@ -126,3 +126,107 @@ def test_base_muon_lp_matches_muon():
     # MuonLP's plain buffers are in the param's dtype (fp32 here): identical arithmetic
     assert torch.equal(a, b)
     assert math.isfinite(a.sum().item())
+
+
+
+def _rel(a, b):
+    return float((a.float() - b.float()).norm() / b.float().norm().clamp_min(1e-30))
+
+
+TILED = [("8bit", OptimState8bit, 256), ("4bit", OptimState4bit, 128), ("fp8", OptimStateFp8, 256),
+         ("8bit", OptimState8bit, 64)]
+TILED_SHAPES = [(512, 256), (256, 768), (300, 256), (2, 256, 512), (4, 96, 512)]
+
+
+@pytest.mark.parametrize("fmt,cls,block", TILED)
+@pytest.mark.parametrize("shape", TILED_SHAPES)
+@pytest.mark.parametrize("gdtype", [torch.float32, torch.bfloat16])
+def test_lp_tiled_prepass_outputs_exact(fmt, cls, block, shape, gdtype):
+    """Shapes whose column count is a multiple of 256 take the one-pass tiled prepass,
+    which writes X straight into the iteration's wide buffer X0 (transposed through LDS
+    for tall matrices, zero padding included) and the norm partials. Called through
+    the C ABI: codes and scales bit-exact against the quantizer oracle, X0 equal to
+    bf16(g') in the wide layout, the partials summing to sum(x^2)."""
+    from muonium_amd import _lib
+
+    lib = _lib.load()
+    dev = torch.device(DEV)
+    _lib.ensure_device(dev)
+    nb = 1
+    for d in shape[:-2]:
+        nb *= d
+    rows, cols = shape[-2:]
+    gen = torch.Generator().manual_seed(5)
+    g = (torch.randn(shape, generator=gen) * torch.exp(torch.randn(*shape[:-1], 1, generator=gen)))
+    g = g.to(gdtype)
+    st = _state(cls, shape, block)
+    codes = np.zeros(st.codes.numel(), np.uint8)
+    scales = np.zeros(st.scale.numel(), np.float32)
+    nbytes = lib.muon_orth_workspace_bytes(_lib.DT_BF16, nb, rows, cols)
+    ws = torch.full((nbytes,), 0x7F, dtype=torch.uint8, device=dev)  # garbage: padding must be rewritten
+    gd = g.to(dev)
+    for step in range(2):
+        rc = lib.muon_lp_prepass(1, _lib.ptr_array([gd]), _lib.dtype_code(gdtype), _lib.ptr_array([st.codes]),
+                                 _lib.ptr_array([st.scale]),
+                                 st.qmap.data_ptr() if st.qmap is not None else None, st.qformat, block,
+                                 nb, rows, cols, 0.9, 1, 0, ws.data_ptr(), _lib.DT_BF16, nb,
+                                 _lib.stream(dev))
+        assert rc == 0, _lib.last_error()
+        torch.cuda.synchronize()
+        codes, scales, gq = quant_ref.lp_momentum_step(
+            codes, scales, g.float().numpy(), block=block, fmt=fmt, qmap=_qmap(fmt), momentum=0.9,
+            nesterov=True, maximize=False,
+        )
+        assert np.array_equal(st.codes.cpu().numpy(), codes), f"codes differ at step {step}"
+        assert np.array_equal(st.scale.cpu().numpy().view(np.uint32), scales.view(np.uint32))
+    m, n = min(rows, cols), max(rows, cols)
+    mp, npad = -(-m // 256) * 256, -(-n // 256) * 256
+    X0 = ws[: nb * mp * npad * 2].view(torch.bfloat16).view(nb, mp, npad).float().cpu()
+    exp = torch.zeros(nb, mp, npad)
+    x = torch.from_numpy(gq).view(nb, rows, cols).bfloat16().float()
+    exp[:, :m, :n] = x.transpose(1, 2) if rows > cols else x
+    assert torch.equal(X0, exp)
+    rup = lambda v: -(-v // 256) * 256
+    off = 2 * rup(nb * mp * npad * 2) + 2 * rup(nb * mp * mp * 2)
+    parts = (mp // 64) * (npad // 64)
+    P = ws[off: off + nb * parts * 4].view(torch.float32).view(nb, parts).double().cpu()
+    want = (x.double() ** 2).sum(dim=(1, 2))
+    torch.testing.assert_close(P.sum(dim=1), want, rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("fmt,cls,block", TILED[:3])
+@pytest.mark.parametrize("shape", [(512, 256), (256, 768)])
+def test_lp_tiled_step_matches_oracle(fmt, cls, block, shape):
+    """The full MuonLP step on a tiled shape: codes bit-exact; the update within the
+    bf16 bar (1e-2 rel-Frobenius) of the fused-bf16 oracle iteration of the same g'.
+    wd = 0 here: the cautious mask (U * p > 0) flips discontinuously on bf16-level
+    differences in U, so the wd term is covered by the bit-exact small-shape test."""
+    opt_cls = {"8bit": Muon8bit, "4bit": Muon4bit, "fp8": MuonFp8}[fmt]
+    gen = torch.Generator().manual_seed(3)
+    p0 = torch.randn(shape, generator=gen)
+    p = nn.Parameter(p0.clone().to(DEV))
+    opt = opt_cls([p], lr=0.05, wd=0.0, momentum=0.9, nesterov=True, block_size=block)
+    codes = scales = None
+    ref_p = p0.clone()
+    coeffs, prescale = muon_ref.strategy_coeffs("polar_express", 5)
+    for step in range(2):
+        g = torch.randn(shape, generator=gen)
+        p.grad = g.clone().to(DEV)
+        opt.step()
+        st = opt.state[p]["momentum_buffer"]
+        assert isinstance(st, cls)
+        if codes is None:
+            codes = np.zeros(st.codes.numel(), np.uint8)
+            scales = np.zeros(st.scale.numel(), np.float32)
+        codes, scales, gq = quant_ref.lp_momentum_step(
+            codes, scales, g.numpy(), block=block, fmt=fmt, qmap=_qmap(fmt), momentum=0.9,
+            nesterov=True, maximize=False,
+        )
+        assert np.array_equal(st.codes.cpu().numpy(), codes), f"codes differ at step {step}"
+        U = muon_ref.polar_iteration_bf16(torch.from_numpy(gq).view(shape), coeffs,
+                                          prescale=prescale, eps=1e-7)
+        adj = muon_ref.lr_ratio(shape) * 0.05
+        got = p.detach().cpu()
+        r = _rel(got - ref_p, -adj * U.float())
+        assert r < 1e-2, f"step {step}: {r:.3e}"
+        ref_p = got.clone()
