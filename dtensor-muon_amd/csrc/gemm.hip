@@ -15,7 +15,9 @@
 // Operands live in workspaces whose extents are padded to the tile size and whose
 // padding is rewritten as zeros by every producer, so the K loop and the stores
 // need no masking (only the standalone gram_ path uses the masked variant).
+#include <atomic>
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 
@@ -38,6 +40,7 @@ struct GemmArgs {
   const float* scale;          // per-batch prescale s (nullable)
   int scale_mode;              // 1: alpha *= s, beta *= s;  2: alpha *= s * s
   int tiles_m, tiles_n, tiles_per_batch;
+  int tiles_total;             // tiles_per_batch * batch
   int store_out, store_out_t;
 };
 
@@ -991,6 +994,395 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_nn_kernel(GemmArgs g) {
   }
 }
 
+// ----------------------------------------------------------------------------------
+// Persistent bf16 X' = alpha * (B X + ratio * X): 4 wavefronts (2 x 2), each owning a
+// 128 x 128 block of the 256 x 256 tile, accumulators in AGPRs (256 per lane).
+//
+// Against gemm_bf16_nn_kernel (8 waves of 64 x 128) a wave reads 8 KB of fragments
+// from LDS per 16 MFMAs instead of 6 KB per 8, and with one wave per SIMD the DMA of the
+// next K-tile is issued from inside the MFMA stream (one buffer_load ... lds per MFMA,
+// M0 stepping through the destination slabs) so its issue never stalls the matrix
+// pipe. The grid is one workgroup per CU; each walks a list of tiles with the operand
+// pipeline running across tile boundaries: the last two K-tiles of a tile prefetch
+// the first two of the next, so a tile's epilogue (stores straight from the
+// accumulators) overlaps the next tile's loads, and its stores drain while the next
+// tile computes.
+//
+// Tiles are dealt to the 8 XCDs as contiguous ranges (workgroup b runs on XCD b % 8):
+// the workgroups of one XCD share its L2 across neighbouring tiles (GM = 8 tile rows
+// per column group, as map_tile). The beta term reads the staged X panel during the
+// two K-tiles whose k range covers the wave's output rows, holds the values in 128
+// VGPRs (bf16 pairs) and adds them in the epilogue.
+constexpr int N4_SMEM = 2 * NN_STAGEB;
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+typedef __attribute__((ext_vector_type(2))) float f2x;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf2x;  // v_cvt_pk_bf16_f32 (RNE)
+
+// buffer descriptor words (raw, stride 0, 2^31 - 1 bytes; num_records 0 for `none`)
+MUON_DEVICE u32x4 n4_rsrc(const void* base, bool none) {
+  const uint64_t a = (uint64_t)base;
+  return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, none ? 0u : 0x7fffffffu, 0x00020000u};
+}
+
+#define MF(C, X, B) "v_mfma_f32_32x32x16_bf16 %[" #C "], %[" #X "], %[" #B "], %[" #C "]\n\t"
+#define TRL(D, XA, O) "ds_read_b64_tr_b16 %[" #D "], %[" #XA "] offset:%[" #O "]\n\t"
+#define N4_ACC_OUT                                                                          \
+  [c00] "+a"(acc[0][0]), [c01] "+a"(acc[0][1]), [c02] "+a"(acc[0][2]), [c03] "+a"(acc[0][3]), \
+  [c10] "+a"(acc[1][0]), [c11] "+a"(acc[1][1]), [c12] "+a"(acc[1][2]), [c13] "+a"(acc[1][3]), \
+  [c20] "+a"(acc[2][0]), [c21] "+a"(acc[2][1]), [c22] "+a"(acc[2][2]), [c23] "+a"(acc[2][3]), \
+  [c30] "+a"(acc[3][0]), [c31] "+a"(acc[3][1]), [c32] "+a"(acc[3][2]), [c33] "+a"(acc[3][3]), \
+  [nb0] "=&v"(nb[0]), [nb1] "=&v"(nb[1]), [nb2] "=&v"(nb[2]), [nb3] "=&v"(nb[3]),              \
+  [l0] "=&v"(nxl[0]), [h0] "=&v"(nxh[0]), [l1] "=&v"(nxl[1]), [h1] "=&v"(nxh[1]),              \
+  [l2] "=&v"(nxl[2]), [h2] "=&v"(nxh[2]), [l3] "=&v"(nxl[3]), [h3] "=&v"(nxh[3])
+#define N4_FRAG_IN                                                                          \
+  [cb0] "v"(cb[0]), [cb1] "v"(cb[1]), [cb2] "v"(cb[2]), [cb3] "v"(cb[3]), [cx0] "v"(cx[0]),    \
+  [cx1] "v"(cx[1]), [cx2] "v"(cx[2]), [cx3] "v"(cx[3]), [ba] "v"(ba), [x0] "v"(xa[0]),         \
+  [x1] "v"(xa[1]), [x2] "v"(xa[2]), [x3] "v"(xa[3]), [o0] "i"(XO), [o1] "i"(XO + 4 * NN_XROWB)
+
+// One k-substep of the 128 x 128 wave tile: 16 MFMAs (accumulator (fm, fn) takes X
+// fragment fn as srcA and B fragment fm as srcB) interleaved with the 12 LDS reads of
+// the next substep's fragments (X: two tr reads per fragment at xa[f] + XO and + 2 KB;
+// B: b128 at ba + 4 KB * fm), complete when the block ends.
+template <int XO>
+MUON_DEVICE void nn4_substep(f32x16 (&acc)[4][4], const bf16x8_mfma (&cb)[4],
+                             const bf16x8_mfma (&cx)[4], bf16x8_mfma (&nb)[4], i16x4 (&nxl)[4],
+                             i16x4 (&nxh)[4], uint32_t ba, const uint32_t (&xa)[4]) {
+  asm volatile(
+      TRL(l0, x0, o0) MF(c00, cx0, cb0)
+      TRL(h0, x0, o1) MF(c01, cx1, cb0)
+      TRL(l1, x1, o0) MF(c02, cx2, cb0)
+      TRL(h1, x1, o1) MF(c03, cx3, cb0)
+      TRL(l2, x2, o0) MF(c10, cx0, cb1)
+      TRL(h2, x2, o1) MF(c11, cx1, cb1)
+      TRL(l3, x3, o0) MF(c12, cx2, cb1)
+      TRL(h3, x3, o1) MF(c13, cx3, cb1)
+      "ds_read_b128 %[nb0], %[ba]\n\t" MF(c20, cx0, cb2)
+      "ds_read_b128 %[nb1], %[ba] offset:4096\n\t" MF(c21, cx1, cb2)
+      "ds_read_b128 %[nb2], %[ba] offset:8192\n\t" MF(c22, cx2, cb2)
+      "ds_read_b128 %[nb3], %[ba] offset:12288\n\t" MF(c23, cx3, cb2)
+      MF(c30, cx0, cb3) MF(c31, cx1, cb3) MF(c32, cx2, cb3) MF(c33, cx3, cb3)
+      "s_waitcnt lgkmcnt(0)"
+      : N4_ACC_OUT
+      : N4_FRAG_IN);
+}
+
+// nn4_substep plus the DMA of one K-tile into one stage: this wave's 8 slabs of the B
+// panel (rows 32 q + 8 wave .. +7, LDS slab 4 q + wave) and 8 of the X panel (rows
+// 8 q + 2 wave, +1), one buffer_load ... lds after each MFMA. M0 holds the LDS
+// destination; each M0 write is separated from its load by an MFMA (the one wait
+// state the hardware needs). ta/tx step the scalar byte offset by one slab group.
+#define DA "buffer_load_dwordx4 %[voa], %[rsa], %[ta] offen lds\n\t"
+#define DX "buffer_load_dwordx4 %[vox], %[rsx], %[tx] offen lds\n\t"
+#define NA "s_add_u32 m0, m0, 0x1000\n\ts_add_u32 %[ta], %[ta], %[sta]\n\t"
+#define NX "s_add_u32 m0, m0, 0x1000\n\ts_add_u32 %[tx], %[tx], %[stx]\n\t"
+template <int XO>
+MUON_DEVICE void nn4_substep_dma(f32x16 (&acc)[4][4], const bf16x8_mfma (&cb)[4],
+                                 const bf16x8_mfma (&cx)[4], bf16x8_mfma (&nb)[4],
+                                 i16x4 (&nxl)[4], i16x4 (&nxh)[4], uint32_t ba,
+                                 const uint32_t (&xa)[4], int voa, int vox, u32x4 rsa,
+                                 u32x4 rsx, int soa, int sox, int sta, int stx, uint32_t m0a,
+                                 uint32_t m0x) {
+  int ta, tx;
+  asm volatile(
+      "s_mov_b32 m0, %[m0a]\n\ts_mov_b32 %[ta], %[soa]\n\t"
+      TRL(l0, x0, o0) MF(c00, cx0, cb0) DA
+      NA TRL(h0, x0, o1) MF(c01, cx1, cb0) DA
+      NA TRL(l1, x1, o0) MF(c02, cx2, cb0) DA
+      NA TRL(h1, x1, o1) MF(c03, cx3, cb0) DA
+      NA TRL(l2, x2, o0) MF(c10, cx0, cb1) DA
+      NA TRL(h2, x2, o1) MF(c11, cx1, cb1) DA
+      NA TRL(l3, x3, o0) MF(c12, cx2, cb1) DA
+      NA TRL(h3, x3, o1) MF(c13, cx3, cb1) DA
+      "s_mov_b32 m0, %[m0x]\n\ts_mov_b32 %[tx], %[sox]\n\t"
+      "ds_read_b128 %[nb0], %[ba]\n\t" MF(c20, cx0, cb2) DX
+      NX "ds_read_b128 %[nb1], %[ba] offset:4096\n\t" MF(c21, cx1, cb2) DX
+      NX "ds_read_b128 %[nb2], %[ba] offset:8192\n\t" MF(c22, cx2, cb2) DX
+      NX "ds_read_b128 %[nb3], %[ba] offset:12288\n\t" MF(c23, cx3, cb2) DX
+      NX MF(c30, cx0, cb3) DX
+      NX MF(c31, cx1, cb3) DX
+      NX MF(c32, cx2, cb3) DX
+      NX MF(c33, cx3, cb3) DX
+      "s_waitcnt lgkmcnt(0)"
+      : N4_ACC_OUT, [ta] "=&s"(ta), [tx] "=&s"(tx)
+      : N4_FRAG_IN, [voa] "v"(voa), [vox] "v"(vox), [rsa] "s"(rsa), [rsx] "s"(rsx),
+        [soa] "s"(soa), [sox] "s"(sox), [sta] "s"(sta), [stx] "s"(stx), [m0a] "s"(m0a),
+        [m0x] "s"(m0x)
+      : "m0", "scc", "memory");
+}
+
+// The DMA of one K-tile without MFMAs (pipeline start).
+MUON_DEVICE void nn4_dma(int voa, int vox, u32x4 rsa, u32x4 rsx, int soa, int sox, int sta,
+                         int stx, uint32_t m0a, uint32_t m0x) {
+  int ta, tx;
+  asm volatile(
+      "s_mov_b32 m0, %[m0a]\n\ts_mov_b32 %[ta], %[soa]\n\ts_nop 0\n\t"
+      DA NA "s_nop 0\n\t" DA NA "s_nop 0\n\t" DA NA "s_nop 0\n\t" DA
+      NA "s_nop 0\n\t" DA NA "s_nop 0\n\t" DA NA "s_nop 0\n\t" DA NA "s_nop 0\n\t" DA
+      "s_mov_b32 m0, %[m0x]\n\ts_mov_b32 %[tx], %[sox]\n\ts_nop 0\n\t"
+      DX NX "s_nop 0\n\t" DX NX "s_nop 0\n\t" DX NX "s_nop 0\n\t" DX
+      NX "s_nop 0\n\t" DX NX "s_nop 0\n\t" DX NX "s_nop 0\n\t" DX NX "s_nop 0\n\t" DX
+      : [ta] "=&s"(ta), [tx] "=&s"(tx)
+      : [voa] "v"(voa), [vox] "v"(vox), [rsa] "s"(rsa), [rsx] "s"(rsx), [soa] "s"(soa),
+        [sox] "s"(sox), [sta] "s"(sta), [stx] "s"(stx), [m0a] "s"(m0a), [m0x] "s"(m0x)
+      : "m0", "scc", "memory");
+}
+#undef DA
+#undef DX
+#undef NA
+#undef NX
+
+template <int XO>
+MUON_DEVICE void nn4_frag_load(bf16x8_mfma (&nb)[4], i16x4 (&nxl)[4], i16x4 (&nxh)[4], uint32_t ba,
+                               const uint32_t (&xa)[4]) {
+  asm volatile(
+      TRL(l0, x0, o0) TRL(h0, x0, o1) TRL(l1, x1, o0) TRL(h1, x1, o1)
+      TRL(l2, x2, o0) TRL(h2, x2, o1) TRL(l3, x3, o0) TRL(h3, x3, o1)
+      "ds_read_b128 %[nb0], %[ba]\n\t"
+      "ds_read_b128 %[nb1], %[ba] offset:4096\n\t"
+      "ds_read_b128 %[nb2], %[ba] offset:8192\n\t"
+      "ds_read_b128 %[nb3], %[ba] offset:12288\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : [nb0] "=&v"(nb[0]), [nb1] "=&v"(nb[1]), [nb2] "=&v"(nb[2]), [nb3] "=&v"(nb[3]),
+        [l0] "=&v"(nxl[0]), [h0] "=&v"(nxh[0]), [l1] "=&v"(nxl[1]), [h1] "=&v"(nxh[1]),
+        [l2] "=&v"(nxl[2]), [h2] "=&v"(nxh[2]), [l3] "=&v"(nxl[3]), [h3] "=&v"(nxh[3])
+      : [ba] "v"(ba), [x0] "v"(xa[0]), [x1] "v"(xa[1]), [x2] "v"(xa[2]), [x3] "v"(xa[3]),
+        [o0] "i"(XO), [o1] "i"(XO + 4 * NN_XROWB));
+}
+#undef MF
+#undef TRL
+#undef N4_ACC_OUT
+#undef N4_FRAG_IN
+
+// X(i, j .. j+3) for the accumulators of rows H0, H0 + 1 (panel row k = h*32 + lane%32,
+// columns 128 wn + 32 fn + 8 rg + 4 (lane/32)) from the staged X panel at sx, as bf16
+// pairs. The LDS base is laundered so the lane addresses are formed here and not kept
+// live across the main loop.
+template <int H0>
+MUON_DEVICE void nn4_beta_rows(u32x2 (&xb)[4][4][4], uint32_t sx, int wn, int fr, int fh) {
+  asm volatile("" : "+v"(sx));
+  const uint32_t base = sx + fr * NN_XROWB + wn * 256 + fh * 8;
+#pragma unroll
+  for (int fn = 0; fn < 4; ++fn) {
+    // logical 16-byte chunk 16 wn + 4 fn + rg sits at position ^ ((k & 3) << 2)
+    const uint32_t b2 = base + (((fn ^ (fr & 3)) << 2) << 4);
+    asm volatile(
+        "ds_read_b64 %0, %8 offset:0\n\t"
+        "ds_read_b64 %1, %8 offset:16\n\t"
+        "ds_read_b64 %2, %8 offset:32\n\t"
+        "ds_read_b64 %3, %8 offset:48\n\t"
+        "ds_read_b64 %4, %8 offset:%9\n\t"
+        "ds_read_b64 %5, %8 offset:%10\n\t"
+        "ds_read_b64 %6, %8 offset:%11\n\t"
+        "ds_read_b64 %7, %8 offset:%12\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(xb[H0][fn][0]), "=&v"(xb[H0][fn][1]), "=&v"(xb[H0][fn][2]),
+          "=&v"(xb[H0][fn][3]), "=&v"(xb[H0 + 1][fn][0]), "=&v"(xb[H0 + 1][fn][1]),
+          "=&v"(xb[H0 + 1][fn][2]), "=&v"(xb[H0 + 1][fn][3])
+        : "v"(b2), "i"(32 * NN_XROWB), "i"(32 * NN_XROWB + 16), "i"(32 * NN_XROWB + 32),
+          "i"(32 * NN_XROWB + 48));
+  }
+}
+
+// Tile t of the launch -> (matrix, row origin, column origin); GM tile rows per column
+// group, as map_tile.
+MUON_DEVICE void nn4_tile(const GemmArgs& g, int t, int& bidx, int64_t& arow0, int64_t& bcol0) {
+  bidx = t / g.tiles_per_batch;
+  const int r = t - bidx * g.tiles_per_batch;
+  const int GM = 8, TN = g.tiles_n, TM = g.tiles_m;
+  const int group = r / (GM * TN);
+  const int first = group * GM;
+  const int gsz = min(TM - first, GM);
+  const int local = r - group * (GM * TN);
+  arow0 = (int64_t)(first + local % gsz) * 256;
+  bcol0 = (int64_t)(local / gsz) * 256;
+}
+
+__global__ __launch_bounds__(256, 1) void gemm_bf16_nn4_kernel(GemmArgs g) {
+  constexpr int FM = 4, FN = 4, WM = 128, WN = 128;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // this workgroup's tiles: XCD x owns tiles [tbase, tbase + tcount); its gx
+  // workgroups take every gx-th one starting at their index l within the XCD
+  const int G = gridDim.x, T = g.tiles_total;
+  const int x = blockIdx.x & 7, l = blockIdx.x >> 3;
+  const int gx = (G >> 3) + (x < (G & 7) ? 1 : 0);
+  const int tcount = (T >> 3) + (x < (T & 7) ? 1 : 0);
+  const int tbase = x * (T >> 3) + min(x, T & 7);
+  int li = l;
+  if (li >= tcount) return;
+
+  const int lda_b = (int)(g.lda * 2), ldx_b = (int)(g.ldb * 2);
+  // DMA lanes: B panel row 8 wave + lane/8 (+ 32 q), logical chunk (lane%8) ^ (row & 7);
+  // X panel row 2 wave + lane/32 (+ 8 q), chunk (lane%32) ^ ((row & 3) << 2)
+  const int ra_in = wave * 8 + (lane >> 3);
+  const int voa = ra_in * lda_b + (((lane & 7) ^ (ra_in & 7)) << 4);
+  const int rx_in = wave * 2 + (lane >> 5);
+  const int vox = rx_in * ldx_b + (((lane & 31) ^ ((rx_in & 3) << 2)) << 4);
+  const int sta = 32 * lda_b, stx = 8 * ldx_b;
+  const bf16_t* const A0 = (const bf16_t*)g.a;
+  const bf16_t* const X0 = (const bf16_t*)g.b;
+
+  // B fragment rows (k contiguous) and X fragment tr-read offsets, as gemm_bf16_nn_kernel
+  const int fr = lane & 31, fh = lane >> 5;
+  int foff[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) foff[ks] = fr * V2_ROWB + (((ks * 2 + fh) ^ (fr & 7)) << 4);
+  const int abase = wm * WM * V2_ROWB;
+  const int tg = lane >> 4, trr = lane & 15, ts = trr >> 2;
+  uint32_t xoff[4];
+#pragma unroll
+  for (int f = 0; f < 4; ++f) {
+    const int chunk = wn * 16 + ((f ^ ts) << 2) + (tg & 1) * 2 + ((trr & 3) >> 1);
+    xoff[f] = NN_ATILEB + (8 * (tg >> 1) + ts) * NN_XROWB + chunk * 16 + (trr & 1) * 8;
+  }
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  auto baddr = [&](int st, int ks) -> uint32_t { return lds0 + st * NN_STAGEB + abase + foff[ks]; };
+  uint32_t xa[4];
+  auto set_xa = [&](int st) {
+#pragma unroll
+    for (int f = 0; f < 4; ++f) xa[f] = lds0 + st * NN_STAGEB + xoff[f];
+  };
+  const uint32_t m0w = lds0 + wave * 1024;
+  const int KT = (int)(g.K / V2_BK);  // a multiple of 4 (K is padded to 256)
+
+  // current tile and its descriptors; the next tile's (num_records 0 if none)
+  int bidx;
+  int64_t arow0, bcol0;
+  nn4_tile(g, tbase + li, bidx, arow0, bcol0);
+  u32x4 rsa = n4_rsrc(A0 + (int64_t)bidx * g.sa + arow0 * g.lda, false);
+  u32x4 rsx = n4_rsrc(X0 + (int64_t)bidx * g.sb + bcol0, false);
+
+  bf16x8_mfma b0[FM], b1[FM], x0[FN], x1[FN];
+  i16x4 xl[FN], xh[FN];
+  nn4_dma(voa, vox, rsa, rsx, 0, 0, sta, stx, m0w, m0w + NN_ATILEB);
+  wait_vmcnt0();
+  lds_barrier();
+  nn4_dma(voa, vox, rsa, rsx, V2_ROWB, V2_BK * ldx_b, sta, stx, m0w + NN_STAGEB,
+          m0w + NN_STAGEB + NN_ATILEB);
+  set_xa(0);
+  nn4_frag_load<0>(b0, xl, xh, baddr(0, 0), xa);
+  nn_join(x0, xl, xh);
+
+  f32x16 acc[FM][FN];
+  for (;;) {
+    const int lnext = li + gx;
+    const bool has_next = lnext < tcount;
+    int nbidx = 0;
+    int64_t narow0 = 0, nbcol0 = 0;
+    if (has_next) nn4_tile(g, tbase + lnext, nbidx, narow0, nbcol0);
+    const u32x4 rsa_n = n4_rsrc(A0 + (int64_t)nbidx * g.sa + narow0 * g.lda, !has_next);
+    const u32x4 rsx_n = n4_rsrc(X0 + (int64_t)nbidx * g.sb + nbcol0, !has_next);
+
+    float alpha = g.alpha, beta = g.beta;
+    if (g.scale_mode == 1) {
+      const float sc = g.scale[bidx];
+      alpha *= sc;
+      beta *= sc;
+    }
+    const float ratio = beta != 0.0f ? beta / alpha : 0.0f;
+    // the wave's 128 output rows are the k rows of K-tiles kd0 and kd0 + 1
+    const int kd0 = ratio != 0.0f ? (int)((arow0 + wm * WM) / V2_BK) : -8;
+
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    u32x2 xb[FM][FN][4];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xb[i][j][r] = u32x2{0u, 0u};
+
+    int kt = 0;
+    do {
+      const int cs = kt & 1;
+      set_xa(cs);
+      nn4_substep<1 * 16 * NN_XROWB>(acc, b0, x0, b1, xl, xh, baddr(cs, 1), xa);
+      nn_join(x1, xl, xh);
+      nn4_substep<2 * 16 * NN_XROWB>(acc, b1, x1, b0, xl, xh, baddr(cs, 2), xa);
+      nn_join(x0, xl, xh);
+      nn4_substep<3 * 16 * NN_XROWB>(acc, b0, x0, b1, xl, xh, baddr(cs, 3), xa);
+      nn_join(x1, xl, xh);
+      if (kt == kd0) nn4_beta_rows<0>(xb, lds0 + cs * NN_STAGEB + NN_ATILEB, wn, fr, fh);
+      if (kt == kd0 + 1) nn4_beta_rows<2>(xb, lds0 + cs * NN_STAGEB + NN_ATILEB, wn, fr, fh);
+      wait_vmcnt0();
+      lds_barrier();
+      // K-tile kt + 2 of this tile, or K-tile kt + 2 - KT of the next, into stage cs
+      const bool cur = kt + 2 < KT;
+      const int kn = cur ? kt + 2 : kt + 2 - KT;
+      set_xa(cs ^ 1);
+      const uint32_t m0a = m0w + cs * NN_STAGEB;
+      nn4_substep_dma<0>(acc, b1, x1, b0, xl, xh, baddr(cs ^ 1, 0), xa, voa, vox,
+                         cur ? rsa : rsa_n, cur ? rsx : rsx_n, kn * V2_ROWB, kn * V2_BK * ldx_b,
+                         sta, stx, m0a, m0a + NN_ATILEB);
+      nn_join(x0, xl, xh);
+    } while (++kt < KT);
+    mfma_to_valu_wait();
+
+    // epilogue: accumulator (fm, fn) element 4 rg + q is X'(i, j + q) with
+    // i = 128 wm + 32 fm + lane%32, j = 128 wn + 32 fn + 8 rg + 4 (lane/32)
+    bf16_t* outw = (bf16_t*)g.out + (int64_t)bidx * g.so + (arow0 + wm * WM) * g.ldo + bcol0 + wn * WN;
+    const __amdgpu_buffer_rsrc_t rso =
+        __builtin_amdgcn_make_buffer_rsrc((void*)outw, 0, 0x7fffffff, 0x00020000);
+    const int ldo_b = (int)(g.ldo * 2);
+    const int vo = fr * ldo_b + fh * 8;
+    // valid extents from this lane's first row / column (zeros are stored beyond);
+    // most tiles lie inside both and take the unmasked path
+    const bool full = arow0 + 256 <= g.Mv && bcol0 + 256 <= g.Nv;
+    const int rem_i = (int)g.Mv - (int)(arow0 + wm * WM + fr);
+    const int rem_j = (int)g.Nv - (int)(bcol0 + wn * WN + fh * 4);
+    auto emit = [&](auto masked) {
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          // one accumulator at a time out of the AGPRs
+          f32x16 av;
+          asm volatile("" : "=v"(av) : "0"(acc[fm][fn]));
+#pragma unroll
+          for (int rg = 0; rg < 4; ++rg) {
+            const u32x2 xw = xb[fm][fn][rg];
+            f2x v01 = {alpha * (av[rg * 4 + 0] + ratio * __uint_as_float(xw.x << 16)),
+                       alpha * (av[rg * 4 + 1] + ratio * __uint_as_float(xw.x & 0xffff0000u))};
+            f2x v23 = {alpha * (av[rg * 4 + 2] + ratio * __uint_as_float(xw.y << 16)),
+                       alpha * (av[rg * 4 + 3] + ratio * __uint_as_float(xw.y & 0xffff0000u))};
+            if (decltype(masked)::value) {
+              const int jq = fn * 32 + rg * 8;
+              const bool vi = fm * 32 < rem_i;
+              v01.x = vi && jq + 0 < rem_j ? v01.x : 0.0f;
+              v01.y = vi && jq + 1 < rem_j ? v01.y : 0.0f;
+              v23.x = vi && jq + 2 < rem_j ? v23.x : 0.0f;
+              v23.y = vi && jq + 3 < rem_j ? v23.y : 0.0f;
+            }
+            const u32x2 w = {__builtin_bit_cast(uint32_t, __builtin_convertvector(v01, bf2x)),
+                             __builtin_bit_cast(uint32_t, __builtin_convertvector(v23, bf2x))};
+            __builtin_amdgcn_raw_buffer_store_b64(w, rso, vo + (fn * 32 + rg * 8) * 2,
+                                                  fm * 32 * ldo_b, 0);
+          }
+        }
+    };
+    if (full)
+      emit(std::false_type{});
+    else
+      emit(std::true_type{});
+    if (!has_next) break;
+    li = lnext;
+    bidx = nbidx;
+    arow0 = narow0;
+    bcol0 = nbcol0;
+    rsa = rsa_n;
+    rsx = rsx_n;
+  }
+}
+
 // Wave grid of the register-staged bf16 kernel (gemm_bf16_kernel), which serves the
 // masked gram_ path and SYRKs whose beta term has no alpha to fold into: 4 x 2
 // wavefronts, each 64 x 128, two waves per SIMD.
@@ -1022,8 +1414,27 @@ int reserve_bf16_lds() {
     if (hipFuncSetAttribute((const void*)gemm_bf16_nn_kernel,
                             hipFuncAttributeMaxDynamicSharedMemorySize, NN_SMEM) != hipSuccess)
       status = -1;
+    if (hipFuncSetAttribute((const void*)gemm_bf16_nn4_kernel,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, N4_SMEM) != hipSuccess)
+      status = -1;
   });
   return status;
+}
+
+// Compute units of the current device (the persistent kernel's grid), cached per device.
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
 }
 
 }  // namespace
@@ -1094,6 +1505,7 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
     g.tiles_per_batch = g.tiles_m * g.tiles_n;
   const int64_t blocks = (int64_t)g.tiles_per_batch * batch;
   if (blocks == 0) return MUON_OK;
+  g.tiles_total = (int)std::min<int64_t>(blocks, 0x7fffffffLL);
   if (blocks > 0x7fffffffLL) {
     muon_set_error("gemm: grid too large (%lld workgroups)", (long long)blocks);
     return MUON_ERR_SHAPE;
@@ -1114,7 +1526,14 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
         muon_set_error("gemm: alpha must be nonzero");
         return MUON_ERR_ARG;
       }
-      hipLaunchKernelGGL(gemm_bf16_nn_kernel, grid, dim3(512), NN_SMEM, stream, g);
+      if (out_t == nullptr && K % 256 == 0) {
+        // persistent: one workgroup per CU walks the tile list
+        const int cus = device_cus();
+        const int wgs = (int)std::min<int64_t>(blocks, cus);
+        hipLaunchKernelGGL(gemm_bf16_nn4_kernel, dim3((unsigned)wgs), dim3(256), N4_SMEM, stream, g);
+      } else {
+        hipLaunchKernelGGL(gemm_bf16_nn_kernel, grid, dim3(512), NN_SMEM, stream, g);
+      }
     } else if (!masked && (alpha != 0.0f || beta == 0.0f)) {
       hipLaunchKernelGGL(gemm_bf16_v2_kernel<MODE_SYRK>, grid, dim3(512), V2_SMEM, stream, g);
     } else {
