@@ -425,8 +425,13 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
 // staging, no ds_write), double-buffered: the loads of tile k+1 are issued right
 // after the barrier that opens tile k and land while tile k's MFMAs run. Each load
 // instruction fills 1 KB of LDS (64 lanes x 16 B), i.e. 8 rows of 128 B; the lane ->
-// global-address map stores 16-byte chunk c of row r at chunk position c ^ (r & 7),
-// which makes the MFMA fragment reads (rows r..r+7 at one chunk) bank-conflict free.
+// global-address map stores 16-byte chunk c of row r at chunk position c ^ kswz(r).
+// The LDS has 64 four-byte banks (256 B per cycle) and serves a 16-byte read 16 lanes
+// at a time; a fragment read puts 16 consecutive rows (at one logical chunk) in those
+// 16 lanes. With a 128-byte row pitch even rows start at bank 0 and odd rows at bank
+// 32, so the swizzle must give the 8 even (and the 8 odd) rows of a 16-row group 8
+// distinct chunk positions: kswz(r) = (r >> 1) & 7. (c ^ (r & 7) repeats every 8 rows
+// and costs a 2-way conflict on every fragment read.)
 // The barrier is an LDS-only wait plus s_barrier: a full __syncthreads would also
 // wait for the in-flight prefetch.
 //
@@ -464,6 +469,10 @@ constexpr int V2_SMEM = (2 * V2_STAGEB > 256 * V2_EP_PITCH * 2) ? 2 * V2_STAGEB
                                                                    : 256 * V2_EP_PITCH * 2;
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Chunk swizzle of a K-contiguous operand panel row (rows of 128 B in LDS); a row offset
+// by a multiple of 16 keeps its swizzle.
+MUON_DEVICE int kswz(int row) { return (row >> 1) & 7; }
 
 MUON_DEVICE void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
@@ -542,9 +551,9 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
   const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(B + brow0 * g.ldb), 0, 0x7fffffff, 0x00020000);
   // load slab q*NW + wave = rows (q*NW + wave)*8 .. +7; lane -> row lane/8, chunk
-  // position lane%8, which holds logical chunk (lane%8) ^ (row & 7)
+  // position lane%8, which holds logical chunk (lane%8) ^ kswz(row)
   const int r_in = wave * 8 + (lane >> 3);
-  const int lch = (lane & 7) ^ (r_in & 7);
+  const int lch = (lane & 7) ^ kswz(r_in);
   const int voa = r_in * lda_b + lch * 16;
   const int vob = r_in * ldb_b + lch * 16;
   auto issue = [&](int kt, int st) {
@@ -565,7 +574,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
   const int fr = lane & 31, fh = lane >> 5;
   int foff[4];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) foff[ks] = fr * V2_ROWB + (((ks * 2 + fh) ^ (fr & 7)) << 4);
+  for (int ks = 0; ks < 4; ++ks) foff[ks] = fr * V2_ROWB + (((ks * 2 + fh) ^ kswz(fr)) << 4);
   const int abase = wm * WM * V2_ROWB, bbase = V2_TILEB + wn * WN * V2_ROWB;
 
   float alpha = g.alpha, beta = g.beta;
@@ -619,7 +628,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
             const int jl = fn * 32 + fr;  // row within this wave's b rows
             const int kl = fm * 32 + rg * 8 + fh * 4;
             const uint2 w = *(const uint2*)(sb + jl * V2_ROWB +
-                                            ((((kl >> 3) ^ (jl & 7))) << 4) + (kl & 7) * 2);
+                                            (((kl >> 3) ^ kswz(jl)) << 4) + (kl & 7) * 2);
             acc[fm][fn][rg * 4 + 0] += ratio * bf16_to_f32((bf16_t)(w.x & 0xffffu));
             acc[fm][fn][rg * 4 + 1] += ratio * bf16_to_f32((bf16_t)(w.x >> 16));
             acc[fm][fn][rg * 4 + 2] += ratio * bf16_to_f32((bf16_t)(w.y & 0xffffu));
@@ -834,7 +843,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_nn_kernel(GemmArgs g) {
   // 2 (q*NW + wave) + {0, 1}: lane -> row lane/32, chunk position lane%32, which holds
   // logical chunk (lane%32) ^ ((row & 3) << 2)
   const int ra_in = wave * 8 + (lane >> 3);
-  const int voa = ra_in * lda_b + (((lane & 7) ^ (ra_in & 7)) << 4);
+  const int voa = ra_in * lda_b + (((lane & 7) ^ kswz(ra_in)) << 4);
   const int rx_in = wave * 2 + (lane >> 5);
   const int vox = rx_in * ldx_b + (((lane & 31) ^ ((rx_in & 3) << 2)) << 4);
   auto issue = [&](int kt, int st) {
@@ -854,7 +863,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_nn_kernel(GemmArgs g) {
   const int fr = lane & 31, fh = lane >> 5;
   int foff[4];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) foff[ks] = fr * V2_ROWB + (((ks * 2 + fh) ^ (fr & 7)) << 4);
+  for (int ks = 0; ks < 4; ++ks) foff[ks] = fr * V2_ROWB + (((ks * 2 + fh) ^ kswz(fr)) << 4);
   const int abase = wm * WM * V2_ROWB;
   // X fragment tr reads: group g = lane/16, r = lane%16 points at panel row
   // 8 (g/2) + r/4 (+ 16 ks, + 4 for the high half), column jw + 32 f + 16 (g%2) + 4 (r%4)
@@ -1216,10 +1225,10 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn4_kernel(GemmArgs g) {
   if (li >= tcount) return;
 
   const int lda_b = (int)(g.lda * 2), ldx_b = (int)(g.ldb * 2);
-  // DMA lanes: B panel row 8 wave + lane/8 (+ 32 q), logical chunk (lane%8) ^ (row & 7);
+  // DMA lanes: B panel row 8 wave + lane/8 (+ 32 q), logical chunk (lane%8) ^ kswz(row);
   // X panel row 2 wave + lane/32 (+ 8 q), chunk (lane%32) ^ ((row & 3) << 2)
   const int ra_in = wave * 8 + (lane >> 3);
-  const int voa = ra_in * lda_b + (((lane & 7) ^ (ra_in & 7)) << 4);
+  const int voa = ra_in * lda_b + (((lane & 7) ^ kswz(ra_in)) << 4);
   const int rx_in = wave * 2 + (lane >> 5);
   const int vox = rx_in * ldx_b + (((lane & 31) ^ ((rx_in & 3) << 2)) << 4);
   const int sta = 32 * lda_b, stx = 8 * ldx_b;
@@ -1230,7 +1239,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn4_kernel(GemmArgs g) {
   const int fr = lane & 31, fh = lane >> 5;
   int foff[4];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) foff[ks] = fr * V2_ROWB + (((ks * 2 + fh) ^ (fr & 7)) << 4);
+  for (int ks = 0; ks < 4; ++ks) foff[ks] = fr * V2_ROWB + (((ks * 2 + fh) ^ kswz(fr)) << 4);
   const int abase = wm * WM * V2_ROWB;
   const int tg = lane >> 4, trr = lane & 15, ts = trr >> 2;
   uint32_t xoff[4];
