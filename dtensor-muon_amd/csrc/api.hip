@@ -30,13 +30,13 @@ int muon_launch_momentum(int ntensors, void* const* grads, void* const* bufs, in
                          int write_grad, hipStream_t s);
 int muon_launch_scale(const OrthLayout& L, void* x, int wdt, int64_t batch, const float* scale,
                       hipStream_t s);
-int muon_launch_scale_transpose(const OrthLayout& L, const void* x, void* xt, int wdt,
-                                int64_t batch, const float* scale, hipStream_t s);
 int muon_launch_postpass(int ntensors, void* const* params, const float* adj, int pdt,
-                         const void* u, int udt, int64_t u_pitch, int64_t u_mstride, int64_t nb,
-                         int64_t rows, int64_t cols, float wd, int cautious, hipStream_t s);
-int muon_launch_extract(const void* src, int wdt, int64_t pitch, int64_t mstride, void* dst,
-                        int odt, int64_t rows, int64_t cols, int64_t batch, hipStream_t s);
+                         const void* u, int udt, int64_t u_pitch, int64_t u_mstride, int u_trans,
+                         int64_t nb, int64_t rows, int64_t cols, float wd, int cautious,
+                         hipStream_t s);
+int muon_launch_extract(const void* src, int wdt, int64_t pitch, int64_t mstride, int trans,
+                        void* dst, int odt, int64_t rows, int64_t cols, int64_t batch,
+                        hipStream_t s);
 int muon_check_lp_format(int qformat, int64_t numel, int64_t block);
 int muon_launch_lp_prepass_tiled(int ntensors, void* const* grads, int gdt, void* const* codes,
                                  void* const* scales, const float* qmap, int qf, int64_t block,
@@ -155,7 +155,7 @@ static bool io_dtype_ok(int dt) {
 
 extern "C" {
 
-int muon_amd_abi_version(void) { return 1; }
+int muon_amd_abi_version(void) { return 2; }
 
 const char* muon_amd_last_error(void) { return g_err; }
 
@@ -200,23 +200,19 @@ int64_t muon_orth_workspace_bytes(int dtype, int64_t batch, int64_t rows, int64_
 }
 
 int muon_orth_result(int dtype, int64_t batch, int64_t rows, int64_t cols, int steps,
-                     int64_t* offset_bytes, int64_t* row_pitch, int64_t* matrix_stride) {
+                     int64_t* offset_bytes, int64_t* row_pitch, int64_t* matrix_stride,
+                     int* transposed) {
   if (!iter_dtype_ok(dtype) || rows <= 0 || cols <= 0 || steps < 0) {
     muon_set_error("orth_result: bad arguments");
     return MUON_ERR_ARG;
   }
   OrthLayout L = muon_orth_layout(dtype, batch, rows, cols);
-  // The iterate after `steps` GEMMs is in X[steps % 2]; a tall matrix's result is its
-  // transpose, which the last GEMM (or, for steps == 0, the scaling pass) writes into
-  // X[steps % 2] (X1 for steps == 0) with pitch m_pad.
-  if (L.tall) {
-    *offset_bytes = (int64_t)((steps == 0 || steps % 2) ? L.off_x1 : L.off_x0);
-    *row_pitch = L.m_pad;
-  } else {
-    *offset_bytes = (int64_t)((steps % 2) ? L.off_x1 : L.off_x0);
-    *row_pitch = L.n_pad;
-  }
+  // The iterate after `steps` GEMMs (or the scaled input for steps == 0) is in
+  // X[steps % 2], in the wide orientation; a tall matrix's result is its transpose.
+  *offset_bytes = (int64_t)((steps % 2) ? L.off_x1 : L.off_x0);
+  *row_pitch = L.n_pad;
   *matrix_stride = L.m_pad * L.n_pad;
+  *transposed = L.tall;
   return MUON_OK;
 }
 
@@ -303,14 +299,13 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
   const int64_t mp = L.m_pad, np = L.n_pad;
   if (steps == 0) {
     Timed t(MUON_K_OTHER, 0.0, s);
-    if (L.tall) return muon_launch_scale_transpose(L, X[0], X[1], ws_dtype, batch, scale, s);
     return muon_launch_scale(L, X[0], ws_dtype, batch, scale, s);
   }
   const double bm = (double)batch, md = (double)L.m, nd = (double)L.n;
   for (int it = 0; it < steps; ++it) {
     const float a = (float)coeffs[3 * it], b = (float)coeffs[3 * it + 1],
                 c = (float)coeffs[3 * it + 2];
-    const bool first = it == 0, last = it == steps - 1;
+    const bool first = it == 0;
     char* Xc = X[it & 1];
     char* Xn = X[(it + 1) & 1];
     // A = X X^T (the first iteration folds the Frobenius prescale s in as s^2)
@@ -330,14 +325,12 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
     }
     if (rc != MUON_OK) return rc;
     // X' = a*X + B X into the other buffer (every tile reads whole columns of X); the
-    // last iteration of a tall matrix stores X'^T, its stored layout
-    void* out = (last && L.tall) ? nullptr : (void*)Xn;
-    void* out_t = (last && L.tall) ? (void*)Xn : nullptr;
+    // result stays in the wide orientation (readers of a tall result transpose on load)
     {
     Timed t(MUON_K_GEMM_BX, bm * 2.0 * md * md * nd, s);
     rc = muon_launch_gemm(ws_dtype, MODE_GEMM, false, batch, mp, np, mp, B, mp, mp * mp, Xc, np,
-                          mp * np, Xc, np, mp * np, out, np, mp * np, out_t, mp, np * mp, L.m,
-                          L.n, 1.0f, a, scale, first ? 1 : 0, s);
+                          mp * np, Xc, np, mp * np, Xn, np, mp * np, nullptr, 0, 0, L.m, L.n,
+                          1.0f, a, scale, first ? 1 : 0, s);
     }
     if (rc != MUON_OK) return rc;
   }
@@ -357,10 +350,11 @@ int muon_orth_extract(const void* ws, int ws_dtype, int64_t ws_batch, int64_t ba
   }
   if (batch == 0) return MUON_OK;
   int64_t off, pitch, mst;
-  int rc = muon_orth_result(ws_dtype, ws_batch, rows, cols, steps, &off, &pitch, &mst);
+  int trans;
+  int rc = muon_orth_result(ws_dtype, ws_batch, rows, cols, steps, &off, &pitch, &mst, &trans);
   if (rc != MUON_OK) return rc;
-  return muon_launch_extract((const char*)ws + off, ws_dtype, pitch, mst, out, out_dtype, rows,
-                             cols, batch, (hipStream_t)stream);
+  return muon_launch_extract((const char*)ws + off, ws_dtype, pitch, mst, trans, out, out_dtype,
+                             rows, cols, batch, (hipStream_t)stream);
 }
 
 int muon_postpass(int ntensors, void* const* params, int p_dtype, const void* u, int u_dtype,
@@ -376,7 +370,7 @@ int muon_postpass(int ntensors, void* const* params, int p_dtype, const void* u,
     return MUON_ERR_SHAPE;
   }
   const char* ubase;
-  int udt;
+  int udt, trans = 0;
   int64_t pitch, mst;
   if (u) {
     if (!io_dtype_ok(u_dtype)) {
@@ -393,7 +387,7 @@ int muon_postpass(int ntensors, void* const* params, int p_dtype, const void* u,
       return MUON_ERR_ARG;
     }
     int64_t off;
-    int rc = muon_orth_result(ws_dtype, ws_batch, rows, cols, steps, &off, &pitch, &mst);
+    int rc = muon_orth_result(ws_dtype, ws_batch, rows, cols, steps, &off, &pitch, &mst, &trans);
     if (rc != MUON_OK) return rc;
     ubase = (const char*)ws + off;
     udt = ws_dtype;
@@ -405,8 +399,8 @@ int muon_postpass(int ntensors, void* const* params, int p_dtype, const void* u,
   for (int t0 = 0; t0 < ntensors; t0 += MUON_MAX_TENSORS) {
     const int cnt = std::min(MUON_MAX_TENSORS, ntensors - t0);
     int rc = muon_launch_postpass(cnt, params + t0, adjusted_lrs + t0, p_dtype,
-                                  ubase + (int64_t)t0 * nb * mst * es, udt, pitch, mst, nb, rows,
-                                  cols, wd, cautious, s);
+                                  ubase + (int64_t)t0 * nb * mst * es, udt, pitch, mst, trans, nb,
+                                  rows, cols, wd, cautious, s);
     if (rc != MUON_OK) return rc;
   }
   return MUON_OK;

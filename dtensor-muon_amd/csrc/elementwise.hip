@@ -239,33 +239,10 @@ __global__ __launch_bounds__(256) void scale_kernel(void* x, int64_t mstride,
   }
 }
 
-// xt[b] = transpose(x[b]) * scale[b] over the padded extents (steps == 0 path of a tall
-// matrix, whose stored layout is the transpose of the wide iterate x).
-template <int WDT>
-__global__ __launch_bounds__(256) void scale_transpose_kernel(const void* x, void* xt,
-                                                              int64_t m_pad, int64_t n_pad,
-                                                              const float* scale) {
-  __shared__ float tile[TILE][TILE + 1];
-  const int64_t b = blockIdx.y;
-  const int64_t tiles_c = n_pad / TILE;
-  const int64_t r0 = (blockIdx.x / tiles_c) * TILE, c0 = (blockIdx.x % tiles_c) * TILE;
-  const int64_t base = b * m_pad * n_pad;
-  const float s = scale[b];
-  for (int i = threadIdx.x; i < TILE * TILE; i += 256) {
-    const int r = i / TILE, c = i % TILE;
-    tile[r][c] = Elem<WDT>::load(x, base + (r0 + r) * n_pad + c0 + c) * s;
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < TILE * TILE; i += 256) {
-    const int r = i / TILE, c = i % TILE;  // row r of the transposed tile = column r
-    Elem<WDT>::store(xt, base + (c0 + r) * m_pad + r0 + c, tile[c][r]);
-  }
-}
-
 struct PostArgs {
   void* params[MUON_MAX_TENSORS];
   float adj[MUON_MAX_TENSORS];
-  const void* u;        // matrix 0 of this launch
+  const void* u;        // matrix 0 of this launch; (TRANS) U(r, c) at u[c * u_pitch + r]
   int64_t u_pitch, u_mstride;
   int64_t nb, rows, cols;
   int tiles_c;
@@ -294,7 +271,11 @@ MUON_DEVICE float apply_elem(float p, float u, float wd, int cautious, float adj
   return p - step;
 }
 
-template <int PDT, int UDT, int VEC>
+// TRANS: U is the wide-orientation iterate of a tall matrix, U(r, c) = u[c][r] (the
+// workspace after the iteration); the 64 x 64 block u[c0 .. c0+63][r0 .. r0+63] is read
+// with coalesced 16-byte loads and transposed through LDS. Its extents are padded to the
+// 256-element tile, so the block is in bounds.
+template <int PDT, int UDT, int VEC, bool TRANS>
 __global__ __launch_bounds__(256) void postpass_kernel(PostArgs a) {
 #pragma clang fp contract(off)
   const int mat = blockIdx.y;
@@ -308,6 +289,19 @@ __global__ __launch_bounds__(256) void postpass_kernel(PostArgs a) {
   constexpr int TPR = TILE / VEC;
   constexpr int RPP = 256 / TPR;
   const int cl = (tid % TPR) * VEC;
+  __shared__ float ut[TRANS ? TILE : 1][TILE + 1];  // ut[r - r0][c - c0]
+  if constexpr (TRANS) {
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int id = it * 256 + tid;
+      const int cc = id >> 3, rr = (id & 7) * 8;
+      float v[8];
+      Vec8<UDT>::load(a.u, (int64_t)mat * a.u_mstride + (c0 + cc) * a.u_pitch + r0 + rr, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ut[rr + e][cc] = v[e];
+    }
+    __syncthreads();
+  }
 #pragma unroll
   for (int rp = 0; rp < TILE / RPP; ++rp) {
     const int64_t r = r0 + rp * RPP + tid / TPR;
@@ -319,7 +313,12 @@ __global__ __launch_bounds__(256) void postpass_kernel(PostArgs a) {
       const int64_t ui = (int64_t)mat * a.u_mstride + r * a.u_pitch + c;
       float p[8], u[8], o[8];
       Vec8<PDT>::load(pp, pi, p);
-      Vec8<UDT>::load(a.u, ui, u);
+      if constexpr (TRANS) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) u[e] = ut[r - r0][cl + e];
+      } else {
+        Vec8<UDT>::load(a.u, ui, u);
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = apply_elem<PDT, UDT>(p[e], u[e], a.wd, a.cautious, adj);
       Vec8<PDT>::store(pp, pi, o);
@@ -331,7 +330,7 @@ __global__ __launch_bounds__(256) void postpass_kernel(PostArgs a) {
         const int64_t pi = mb * a.rows * a.cols + r * a.cols + c;
         const int64_t ui = (int64_t)mat * a.u_mstride + r * a.u_pitch + c;
         const float p = Elem<PDT>::load(pp, pi);
-        const float u = Elem<UDT>::load(a.u, ui);
+        const float u = TRANS ? ut[r - r0][cl + e] : Elem<UDT>::load(a.u, ui);
         Elem<PDT>::store(pp, pi, apply_elem<PDT, UDT>(p, u, a.wd, a.cautious, adj));
       }
     }
@@ -349,6 +348,27 @@ __global__ __launch_bounds__(256) void extract_kernel(const void* src, int64_t p
        i += (int64_t)gridDim.x * 256) {
     const int64_t r = i / cols, c = i % cols;
     Elem<ODT>::store(dst, b * n + i, Elem<WDT>::load(src, b * mstride + r * pitch + c));
+  }
+}
+
+// As extract_kernel for a tall matrix whose result is held transposed (element (r, c) at
+// src[c * pitch + r], extents padded to 64): one 64 x 64 block per workgroup through LDS.
+template <int WDT, int ODT>
+__global__ __launch_bounds__(256) void extract_t_kernel(const void* src, int64_t pitch,
+                                                        int64_t mstride, void* dst, int64_t rows,
+                                                        int64_t cols, int tiles_c) {
+  __shared__ float tile[TILE][TILE + 1];  // tile[c - c0][r - r0]
+  const int64_t b = blockIdx.y;
+  const int64_t r0 = (int64_t)(blockIdx.x / tiles_c) * TILE, c0 = (int64_t)(blockIdx.x % tiles_c) * TILE;
+  for (int i = threadIdx.x; i < TILE * TILE; i += 256) {
+    const int cc = i / TILE, rr = i % TILE;
+    tile[cc][rr] = Elem<WDT>::load(src, b * mstride + (c0 + cc) * pitch + r0 + rr);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < TILE * TILE; i += 256) {
+    const int rr = i / TILE, cc = i % TILE;
+    const int64_t r = r0 + rr, c = c0 + cc;
+    if (r < rows && c < cols) Elem<ODT>::store(dst, (b * rows + r) * cols + c, tile[cc][rr]);
   }
 }
 
@@ -382,27 +402,57 @@ int launch_prepass_b(int bdt, int wdt, const PrepassArgs& a, dim3 grid, bool vec
   return MUON_ERR_DTYPE;
 }
 
-template <int PDT, int UDT>
+template <int PDT, int UDT, bool TRANS>
 void launch_post_t(const PostArgs& a, dim3 grid, bool vec8, hipStream_t s) {
   if (vec8)
-    hipLaunchKernelGGL((postpass_kernel<PDT, UDT, 8>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((postpass_kernel<PDT, UDT, 8, TRANS>), grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((postpass_kernel<PDT, UDT, 1>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((postpass_kernel<PDT, UDT, 1, TRANS>), grid, dim3(256), 0, s, a);
 }
 
+// A transposed U comes from the workspace only (bf16 or fp32).
 template <int PDT>
-int launch_post_u(int udt, const PostArgs& a, dim3 grid, bool vec8, hipStream_t s) {
+int launch_post_u(int udt, bool trans, const PostArgs& a, dim3 grid, bool vec8, hipStream_t s) {
   switch (udt) {
-    case MUON_DT_F32: launch_post_t<PDT, MUON_DT_F32>(a, grid, vec8, s); return MUON_OK;
-    case MUON_DT_BF16: launch_post_t<PDT, MUON_DT_BF16>(a, grid, vec8, s); return MUON_OK;
-    case MUON_DT_F16: launch_post_t<PDT, MUON_DT_F16>(a, grid, vec8, s); return MUON_OK;
+    case MUON_DT_F32:
+      if (trans)
+        launch_post_t<PDT, MUON_DT_F32, true>(a, grid, vec8, s);
+      else
+        launch_post_t<PDT, MUON_DT_F32, false>(a, grid, vec8, s);
+      return MUON_OK;
+    case MUON_DT_BF16:
+      if (trans)
+        launch_post_t<PDT, MUON_DT_BF16, true>(a, grid, vec8, s);
+      else
+        launch_post_t<PDT, MUON_DT_BF16, false>(a, grid, vec8, s);
+      return MUON_OK;
+    case MUON_DT_F16:
+      if (trans) return MUON_ERR_DTYPE;
+      launch_post_t<PDT, MUON_DT_F16, false>(a, grid, vec8, s);
+      return MUON_OK;
   }
   return MUON_ERR_DTYPE;
 }
 
+template <int WDT, int ODT>
+void launch_extract_t(const void* src, int64_t pitch, int64_t mstride, void* dst, int64_t rows,
+                      int64_t cols, int64_t batch, hipStream_t s) {
+  const int64_t tr = (rows + TILE - 1) / TILE, tc = (cols + TILE - 1) / TILE;
+  hipLaunchKernelGGL((extract_t_kernel<WDT, ODT>), dim3((unsigned)(tr * tc), (unsigned)batch),
+                     dim3(256), 0, s, src, pitch, mstride, dst, rows, cols, (int)tc);
+}
+
 template <int WDT>
-int launch_extract_o(int odt, const void* src, int64_t pitch, int64_t mstride, void* dst,
-                     int64_t rows, int64_t cols, int64_t batch, hipStream_t s) {
+int launch_extract_o(int odt, const void* src, int64_t pitch, int64_t mstride, int trans,
+                     void* dst, int64_t rows, int64_t cols, int64_t batch, hipStream_t s) {
+  if (trans) {
+    switch (odt) {
+      case MUON_DT_F32: launch_extract_t<WDT, MUON_DT_F32>(src, pitch, mstride, dst, rows, cols, batch, s); return MUON_OK;
+      case MUON_DT_BF16: launch_extract_t<WDT, MUON_DT_BF16>(src, pitch, mstride, dst, rows, cols, batch, s); return MUON_OK;
+      case MUON_DT_F16: launch_extract_t<WDT, MUON_DT_F16>(src, pitch, mstride, dst, rows, cols, batch, s); return MUON_OK;
+    }
+    return MUON_ERR_DTYPE;
+  }
   const int64_t n = rows * cols;
   dim3 grid((unsigned)std::min<int64_t>((n + 255) / 256, 4096), (unsigned)batch);
   switch (odt) {
@@ -538,19 +588,6 @@ int muon_launch_finalize(const OrthLayout& L, void* ws, int64_t batch, float pre
   return MUON_OK;
 }
 
-int muon_launch_scale_transpose(const OrthLayout& L, const void* x, void* xt, int wdt,
-                                int64_t batch, const float* scale, hipStream_t s) {
-  dim3 grid((unsigned)((L.m_pad / TILE) * (L.n_pad / TILE)), (unsigned)batch);
-  if (wdt == MUON_DT_BF16)
-    hipLaunchKernelGGL((scale_transpose_kernel<MUON_DT_BF16>), grid, dim3(256), 0, s, x, xt,
-                       L.m_pad, L.n_pad, scale);
-  else
-    hipLaunchKernelGGL((scale_transpose_kernel<MUON_DT_F32>), grid, dim3(256), 0, s, x, xt,
-                       L.m_pad, L.n_pad, scale);
-  MUON_CHECK_LAUNCH("scale_transpose");
-  return MUON_OK;
-}
-
 int muon_launch_scale(const OrthLayout& L, void* x, int wdt, int64_t batch, const float* scale,
                       hipStream_t s) {
   const int64_t mst = L.m_pad * L.n_pad;
@@ -564,8 +601,9 @@ int muon_launch_scale(const OrthLayout& L, void* x, int wdt, int64_t batch, cons
 }
 
 int muon_launch_postpass(int ntensors, void* const* params, const float* adj, int pdt,
-                         const void* u, int udt, int64_t u_pitch, int64_t u_mstride, int64_t nb,
-                         int64_t rows, int64_t cols, float wd, int cautious, hipStream_t s) {
+                         const void* u, int udt, int64_t u_pitch, int64_t u_mstride, int u_trans,
+                         int64_t nb, int64_t rows, int64_t cols, float wd, int cautious,
+                         hipStream_t s) {
   PostArgs a;
   for (int i = 0; i < ntensors; ++i) {
     a.params[i] = params[i];
@@ -581,6 +619,11 @@ int muon_launch_postpass(int ntensors, void* const* params, const float* adj, in
   a.cautious = cautious;
   const int64_t tiles_r = (rows + TILE - 1) / TILE, tiles_c = (cols + TILE - 1) / TILE;
   a.tiles_c = (int)tiles_c;
+  // the transposed read needs 64-padded extents and 16-byte rows (the workspace layout)
+  if (u_trans && ((u_pitch % TILE) || (u_mstride % 8) || ((uintptr_t)u & 15))) {
+    muon_set_error("postpass: transposed update must come from the workspace");
+    return MUON_ERR_ALIGN;
+  }
   bool vec8 = (cols % 8) == 0 && (u_pitch % 8) == 0 && (u_mstride % 8) == 0 &&
               !((uintptr_t)u & 15);
   for (int i = 0; i < ntensors; ++i)
@@ -588,9 +631,9 @@ int muon_launch_postpass(int ntensors, void* const* params, const float* adj, in
   dim3 grid((unsigned)(tiles_r * tiles_c), (unsigned)(ntensors * nb));
   int rc;
   switch (pdt) {
-    case MUON_DT_F32: rc = launch_post_u<MUON_DT_F32>(udt, a, grid, vec8, s); break;
-    case MUON_DT_BF16: rc = launch_post_u<MUON_DT_BF16>(udt, a, grid, vec8, s); break;
-    case MUON_DT_F16: rc = launch_post_u<MUON_DT_F16>(udt, a, grid, vec8, s); break;
+    case MUON_DT_F32: rc = launch_post_u<MUON_DT_F32>(udt, u_trans, a, grid, vec8, s); break;
+    case MUON_DT_BF16: rc = launch_post_u<MUON_DT_BF16>(udt, u_trans, a, grid, vec8, s); break;
+    case MUON_DT_F16: rc = launch_post_u<MUON_DT_F16>(udt, u_trans, a, grid, vec8, s); break;
     default: rc = MUON_ERR_DTYPE;
   }
   if (rc != MUON_OK) {
@@ -601,13 +644,14 @@ int muon_launch_postpass(int ntensors, void* const* params, const float* adj, in
   return MUON_OK;
 }
 
-int muon_launch_extract(const void* src, int wdt, int64_t pitch, int64_t mstride, void* dst,
-                        int odt, int64_t rows, int64_t cols, int64_t batch, hipStream_t s) {
+int muon_launch_extract(const void* src, int wdt, int64_t pitch, int64_t mstride, int trans,
+                        void* dst, int odt, int64_t rows, int64_t cols, int64_t batch,
+                        hipStream_t s) {
   int rc;
   if (wdt == MUON_DT_BF16)
-    rc = launch_extract_o<MUON_DT_BF16>(odt, src, pitch, mstride, dst, rows, cols, batch, s);
+    rc = launch_extract_o<MUON_DT_BF16>(odt, src, pitch, mstride, trans, dst, rows, cols, batch, s);
   else
-    rc = launch_extract_o<MUON_DT_F32>(odt, src, pitch, mstride, dst, rows, cols, batch, s);
+    rc = launch_extract_o<MUON_DT_F32>(odt, src, pitch, mstride, trans, dst, rows, cols, batch, s);
   if (rc != MUON_OK) {
     muon_set_error("extract: unsupported dtype %d", odt);
     return rc;

@@ -724,7 +724,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
 // ----------------------------------------------------------------------------------
 // bf16 X' = alpha * (B X + ratio * X) with X read in its own row-major layout.
 //
-// The a operand (B, rows i, k contiguous) is handled as in gemm_bf16_v2_kernel. The
+// The a operand (B, rows i, k contiguous) is staged as in gemm_bf16_v2_kernel. The
 // b operand is X itself, whose rows are k: each K-tile stages a 64 x 256 panel
 // X[k][j] (rows of 512 B, 16-byte chunk c of row k stored at chunk c ^ ((k & 3) << 2))
 // and the MFMA fragments, which need 8 consecutive k of one column j per lane, come
@@ -737,80 +737,14 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
 // transposed: lane l has row i = l % 32 and 4 consecutive columns j of a 32 x 32
 // block. Stores of X' are then 8-byte row pieces straight from registers, and the
 // beta term X(i, j .. j+3) is 8 contiguous bytes of row k = i of the X panel.
-// A transposed copy (the last iteration of a tall matrix) goes through LDS.
 // No X^T is kept in memory; X ping-pongs between two buffers because every tile
 // reads whole columns of X.
 constexpr int NN_XROWB = 512;                        // X panel row: 256 bf16
 constexpr int NN_ATILEB = 256 * V2_ROWB;             // B panel: 256 rows x 64 k
 constexpr int NN_XTILEB = V2_BK * NN_XROWB;          // X panel: 64 k x 256 j
 constexpr int NN_STAGEB = NN_ATILEB + NN_XTILEB;
-constexpr int NN_SMEM = (2 * NN_STAGEB > 256 * V2_EP_PITCH * 2) ? 2 * NN_STAGEB
-                                                                 : 256 * V2_EP_PITCH * 2;
 
 typedef __attribute__((ext_vector_type(4))) short i16x4;
-
-#define MUON_MFMA_NN(C, X, B) "v_mfma_f32_32x32x16_bf16 %[" #C "], %[" #X "], %[" #B "], %[" #C "]\n\t"
-// One k-substep of the NN product for a 64 x 128 wave tile: 8 MFMAs on the current
-// fragments (cb: B rows, cx: X columns), two reads of the next fragments ahead of each
-// of the first five MFMAs (measured a few percent faster than one per MFMA):
-// nb0/nb1 (b128 at ba, ba + BO) and the two halves of each X fragment (tr reads at
-// xa[f] + XO and xa[f] + XO + 2 KB).
-template <int XO, int BO = 32 * V2_ROWB>
-MUON_DEVICE void nn_substep(f32x16 (&acc)[2][4], const bf16x8_mfma (&cb)[2],
-                            const bf16x8_mfma (&cx)[4], bf16x8_mfma (&nb)[2], i16x4 (&nxl)[4],
-                            i16x4 (&nxh)[4], uint32_t ba, const uint32_t (&xa)[4]) {
-  asm volatile(
-      "ds_read_b64_tr_b16 %[l0], %[x0] offset:%[o0]\n\t"
-      "ds_read_b64_tr_b16 %[h0], %[x0] offset:%[o1]\n\t"
-      MUON_MFMA_NN(c00, cx0, cb0)
-      "ds_read_b64_tr_b16 %[l1], %[x1] offset:%[o0]\n\t"
-      "ds_read_b64_tr_b16 %[h1], %[x1] offset:%[o1]\n\t"
-      MUON_MFMA_NN(c01, cx1, cb0)
-      "ds_read_b64_tr_b16 %[l2], %[x2] offset:%[o0]\n\t"
-      "ds_read_b64_tr_b16 %[h2], %[x2] offset:%[o1]\n\t"
-      MUON_MFMA_NN(c02, cx2, cb0)
-      "ds_read_b64_tr_b16 %[l3], %[x3] offset:%[o0]\n\t"
-      "ds_read_b64_tr_b16 %[h3], %[x3] offset:%[o1]\n\t"
-      MUON_MFMA_NN(c03, cx3, cb0)
-      "ds_read_b128 %[nb0], %[ba]\n\t"
-      "ds_read_b128 %[nb1], %[ba] offset:%[bo]\n\t"
-      MUON_MFMA_NN(c10, cx0, cb1)
-      MUON_MFMA_NN(c11, cx1, cb1)
-      MUON_MFMA_NN(c12, cx2, cb1)
-      MUON_MFMA_NN(c13, cx3, cb1)
-      "s_waitcnt lgkmcnt(0)"
-      : [c00] "+v"(acc[0][0]), [c01] "+v"(acc[0][1]), [c02] "+v"(acc[0][2]),
-        [c03] "+v"(acc[0][3]), [c10] "+v"(acc[1][0]), [c11] "+v"(acc[1][1]),
-        [c12] "+v"(acc[1][2]), [c13] "+v"(acc[1][3]), [nb0] "=&v"(nb[0]), [nb1] "=&v"(nb[1]),
-        [l0] "=&v"(nxl[0]), [h0] "=&v"(nxh[0]), [l1] "=&v"(nxl[1]), [h1] "=&v"(nxh[1]),
-        [l2] "=&v"(nxl[2]), [h2] "=&v"(nxh[2]), [l3] "=&v"(nxl[3]), [h3] "=&v"(nxh[3])
-      : [cb0] "v"(cb[0]), [cb1] "v"(cb[1]), [cx0] "v"(cx[0]), [cx1] "v"(cx[1]),
-        [cx2] "v"(cx[2]), [cx3] "v"(cx[3]), [ba] "v"(ba), [x0] "v"(xa[0]), [x1] "v"(xa[1]),
-        [x2] "v"(xa[2]), [x3] "v"(xa[3]), [o0] "i"(XO), [o1] "i"(XO + 4 * NN_XROWB), [bo] "i"(BO));
-}
-#undef MUON_MFMA_NN
-
-template <int XO, int BO = 32 * V2_ROWB>
-MUON_DEVICE void nn_frag_load(bf16x8_mfma (&nb)[2], i16x4 (&nxl)[4], i16x4 (&nxh)[4], uint32_t ba,
-                              const uint32_t (&xa)[4]) {
-  asm volatile(
-      "ds_read_b64_tr_b16 %[l0], %[x0] offset:%[o0]\n\t"
-      "ds_read_b64_tr_b16 %[h0], %[x0] offset:%[o1]\n\t"
-      "ds_read_b64_tr_b16 %[l1], %[x1] offset:%[o0]\n\t"
-      "ds_read_b64_tr_b16 %[h1], %[x1] offset:%[o1]\n\t"
-      "ds_read_b64_tr_b16 %[l2], %[x2] offset:%[o0]\n\t"
-      "ds_read_b64_tr_b16 %[h2], %[x2] offset:%[o1]\n\t"
-      "ds_read_b64_tr_b16 %[l3], %[x3] offset:%[o0]\n\t"
-      "ds_read_b64_tr_b16 %[h3], %[x3] offset:%[o1]\n\t"
-      "ds_read_b128 %[nb0], %[ba]\n\t"
-      "ds_read_b128 %[nb1], %[ba] offset:%[bo]\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : [nb0] "=&v"(nb[0]), [nb1] "=&v"(nb[1]), [l0] "=&v"(nxl[0]), [h0] "=&v"(nxh[0]),
-        [l1] "=&v"(nxl[1]), [h1] "=&v"(nxh[1]), [l2] "=&v"(nxl[2]), [h2] "=&v"(nxh[2]),
-        [l3] "=&v"(nxl[3]), [h3] "=&v"(nxh[3])
-      : [ba] "v"(ba), [x0] "v"(xa[0]), [x1] "v"(xa[1]), [x2] "v"(xa[2]), [x3] "v"(xa[3]),
-        [o0] "i"(XO), [o1] "i"(XO + 4 * NN_XROWB), [bo] "i"(BO));
-}
 
 MUON_DEVICE void nn_join(bf16x8_mfma (&cx)[4], const i16x4 (&lo)[4], const i16x4 (&hi)[4]) {
 #pragma unroll
@@ -822,193 +756,12 @@ MUON_DEVICE void nn_join(bf16x8_mfma (&cx)[4], const i16x4 (&lo)[4], const i16x4
   }
 }
 
-__global__ __launch_bounds__(512, 1) void gemm_bf16_nn_kernel(GemmArgs g) {
-  constexpr int NW = 8, WGN = 2, WM = 64, WN = 128, FM = 2, FN = 4;
-  constexpr int SPW = (NN_ATILEB / 1024) / NW;  // 1 KB load slabs per wave per operand
-  extern __shared__ __align__(16) uint8_t smem[];
-
-  int bidx, tm, tn;
-  map_tile(g, MODE_GEMM, bidx, tm, tn);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WGN, wn = wave % WGN;
-  const bf16_t* A = (const bf16_t*)g.a + (int64_t)bidx * g.sa;
-  const bf16_t* X = (const bf16_t*)g.b + (int64_t)bidx * g.sb;
-  const int64_t arow0 = (int64_t)tm * 256, bcol0 = (int64_t)tn * 256;
-  const int lda_b = (int)(g.lda * 2), ldx_b = (int)(g.ldb * 2);
-  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(A + arow0 * g.lda), 0, 0x7fffffff, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(X + bcol0), 0, 0x7fffffff, 0x00020000);
-  // a slabs as in gemm_bf16_v2_kernel; X slab q*NW + wave = panel rows
-  // 2 (q*NW + wave) + {0, 1}: lane -> row lane/32, chunk position lane%32, which holds
-  // logical chunk (lane%32) ^ ((row & 3) << 2)
-  const int ra_in = wave * 8 + (lane >> 3);
-  const int voa = ra_in * lda_b + (((lane & 7) ^ kswz(ra_in)) << 4);
-  const int rx_in = wave * 2 + (lane >> 5);
-  const int vox = rx_in * ldx_b + (((lane & 31) ^ ((rx_in & 3) << 2)) << 4);
-  auto issue = [&](int kt, int st) {
-    uint8_t* sa = smem + st * NN_STAGEB;
-    uint8_t* sx = sa + NN_ATILEB;
-#pragma unroll
-    for (int q = 0; q < SPW; ++q) {
-      const int slab = q * NW + wave;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(sa + slab * 1024), 16, voa,
-                                               q * NW * 8 * lda_b + kt * V2_ROWB, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsx, (lds_ptr_t)(sx + slab * 1024), 16, vox,
-                                               (q * NW * 2 + kt * V2_BK) * ldx_b, 0, 0);
-    }
-  };
-
-  // B fragment reads (rows i, k contiguous) as in gemm_bf16_v2_kernel
-  const int fr = lane & 31, fh = lane >> 5;
-  int foff[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) foff[ks] = fr * V2_ROWB + (((ks * 2 + fh) ^ kswz(fr)) << 4);
-  const int abase = wm * WM * V2_ROWB;
-  // X fragment tr reads: group g = lane/16, r = lane%16 points at panel row
-  // 8 (g/2) + r/4 (+ 16 ks, + 4 for the high half), column jw + 32 f + 16 (g%2) + 4 (r%4)
-  const int tg = lane >> 4, tr = lane & 15, ts = tr >> 2;
-  uint32_t xoff[4];
-#pragma unroll
-  for (int f = 0; f < 4; ++f) {
-    const int chunk = wn * 16 + ((f ^ ts) << 2) + (tg & 1) * 2 + ((tr & 3) >> 1);
-    xoff[f] = NN_ATILEB + (8 * (tg >> 1) + ts) * NN_XROWB + chunk * 16 + (tr & 1) * 8;
-  }
-
-  float alpha = g.alpha, beta = g.beta;
-  if (g.scale_mode == 1) {
-    const float s = g.scale[bidx];
-    alpha *= s;
-    beta *= s;
-  }
-  const float ratio = beta != 0.0f ? beta / alpha : 0.0f;
-  const int kdiag = ratio != 0.0f ? (int)((arow0 + wm * WM) / V2_BK) : -1;
-
-  f32x16 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  const int KT = (int)(g.K / V2_BK);
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
-  auto baddr = [&](int st, int ks) -> uint32_t { return lds0 + st * NN_STAGEB + abase + foff[ks]; };
-  uint32_t xa[4];
-  auto set_xa = [&](int st) {
-#pragma unroll
-    for (int f = 0; f < 4; ++f) xa[f] = lds0 + st * NN_STAGEB + xoff[f];
-  };
-  bf16x8_mfma b0[FM], b1[FM], x0[FN], x1[FN];
-  i16x4 xl[FN], xh[FN];
-  issue(0, 0);
-  wait_vmcnt0();
-  lds_barrier();
-  if (KT > 1) issue(1, 1);
-  set_xa(0);
-  nn_frag_load<0>(b0, xl, xh, baddr(0, 0), xa);
-  nn_join(x0, xl, xh);
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cs = kt & 1;
-    set_xa(cs);
-    nn_substep<1 * 16 * NN_XROWB>(acc, b0, x0, b1, xl, xh, baddr(cs, 1), xa);
-    nn_join(x1, xl, xh);
-    nn_substep<2 * 16 * NN_XROWB>(acc, b1, x1, b0, xl, xh, baddr(cs, 2), xa);
-    nn_join(x0, xl, xh);
-    nn_substep<3 * 16 * NN_XROWB>(acc, b0, x0, b1, xl, xh, baddr(cs, 3), xa);
-    nn_join(x1, xl, xh);
-    if (kt == kdiag) {
-      // X(i, j..j+3) for accumulator (fm, fn, rg): panel row k = fm*32 + lane%32,
-      // columns jw + 32 fn + 8 rg + 4 (lane/32)
-      mfma_to_valu_wait();
-      const uint8_t* sx = smem + cs * NN_STAGEB + NN_ATILEB;
-#pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-          for (int rg = 0; rg < 4; ++rg) {
-            const int kl = fm * 32 + fr;
-            const int jl = wn * WN + fn * 32 + rg * 8 + fh * 4;
-            const uint2 w = *(const uint2*)(sx + kl * NN_XROWB +
-                                            (((jl >> 3) ^ ((kl & 3) << 2)) << 4) + (jl & 7) * 2);
-            acc[fm][fn][rg * 4 + 0] += ratio * bf16_to_f32((bf16_t)(w.x & 0xffffu));
-            acc[fm][fn][rg * 4 + 1] += ratio * bf16_to_f32((bf16_t)(w.x >> 16));
-            acc[fm][fn][rg * 4 + 2] += ratio * bf16_to_f32((bf16_t)(w.y & 0xffffu));
-            acc[fm][fn][rg * 4 + 3] += ratio * bf16_to_f32((bf16_t)(w.y >> 16));
-          }
-      valu_to_mfma_wait();
-    }
-    wait_vmcnt0();
-    lds_barrier();
-    if (kt + 2 < KT) issue(kt + 2, cs);
-    set_xa(cs ^ 1);
-    nn_substep<0>(acc, b1, x1, b0, xl, xh, baddr(cs ^ 1, 0), xa);
-    nn_join(x0, xl, xh);
-  }
-  mfma_to_valu_wait();
-
-  // ---- epilogue: accumulator (fm, fn, rg) holds X'(i, j .. j+3) ----
-  bf16_t* out = g.out ? (bf16_t*)g.out + (int64_t)bidx * g.so : nullptr;
-  auto packed = [&](int fm, int fn, int rg, int64_t i, int64_t j) -> uint2 {
-    float v[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      v[q] = (i < g.Mv && j + q < g.Nv) ? alpha * acc[fm][fn][rg * 4 + q] : 0.0f;
-    uint2 w;
-    w.x = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
-    w.y = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
-    return w;
-  };
-  if (out) {
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-        for (int rg = 0; rg < 4; ++rg) {
-          const int64_t i = arow0 + wm * WM + fm * 32 + fr;
-          const int64_t j = bcol0 + wn * WN + fn * 32 + rg * 8 + fh * 4;
-          *(uint2*)(out + i * g.ldo + j) = packed(fm, fn, rg, i, j);
-        }
-  }
-  if (g.out_t) {
-    // transposed copy through a row-major LDS tile T[i][j]
-    bf16_t* out_t = (bf16_t*)g.out_t + (int64_t)bidx * g.st;
-    bf16_t* T = (bf16_t*)smem;
-    lds_barrier();
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-        for (int rg = 0; rg < 4; ++rg) {
-          const int il = wm * WM + fm * 32 + fr;
-          const int jl = wn * WN + fn * 32 + rg * 8 + fh * 4;
-          *(uint2*)(T + il * V2_EP_PITCH + jl) = packed(fm, fn, rg, arow0 + il, bcol0 + jl);
-        }
-    lds_barrier();
-#pragma unroll 4
-    for (int it = 0; it < 16; ++it) {
-      const int id = it * 512 + tid;
-      const int jl = id >> 5, c = (id & 31) * 8;
-      uint16_t e[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) e[q] = T[(c + q) * V2_EP_PITCH + jl];
-      uint4 w;
-      __builtin_memcpy(&w, e, 16);
-      *(uint4*)(out_t + (bcol0 + jl) * g.ldt + arow0 + c) = w;
-    }
-  }
-}
-
 // ----------------------------------------------------------------------------------
 // Persistent bf16 X' = alpha * (B X + ratio * X): 4 wavefronts (2 x 2), each owning a
 // 128 x 128 block of the 256 x 256 tile, accumulators in AGPRs (256 per lane).
 //
-// Against gemm_bf16_nn_kernel (8 waves of 64 x 128) a wave reads 8 KB of fragments
-// from LDS per 16 MFMAs instead of 6 KB per 8, and with one wave per SIMD the DMA of the
+// Against 8 waves of 64 x 128 (measured 2-8% slower on the same box) a wave reads 8 KB of
+// fragments from LDS per 16 MFMAs instead of 6 KB per 8, and with one wave per SIMD the DMA of the
 // next K-tile is issued from inside the MFMA stream (one buffer_load ... lds per MFMA,
 // M0 stepping through the destination slabs) so its issue never stalls the matrix
 // pipe. The grid is one workgroup per CU; each walks a list of tiles with the operand
@@ -1235,7 +988,9 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn4_kernel(GemmArgs g) {
   const bf16_t* const A0 = (const bf16_t*)g.a;
   const bf16_t* const X0 = (const bf16_t*)g.b;
 
-  // B fragment rows (k contiguous) and X fragment tr-read offsets, as gemm_bf16_nn_kernel
+  // B fragment rows (k contiguous, as gemm_bf16_v2_kernel) and X fragment tr-read offsets:
+  // group g = lane/16, r = lane%16 points at panel row 8 (g/2) + r/4 (+ 16 ks, + 4 for
+  // the high half), column 128 wn + 32 f + 16 (g%2) + 4 (r%4)
   const int fr = lane & 31, fh = lane >> 5;
   int foff[4];
 #pragma unroll
@@ -1420,9 +1175,6 @@ int reserve_bf16_lds() {
     if (hipFuncSetAttribute((const void*)gemm_bf16_v2_kernel<MODE_SYRK>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, V2_SMEM) != hipSuccess)
       status = -1;
-    if (hipFuncSetAttribute((const void*)gemm_bf16_nn_kernel,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, NN_SMEM) != hipSuccess)
-      status = -1;
     if (hipFuncSetAttribute((const void*)gemm_bf16_nn4_kernel,
                             hipFuncAttributeMaxDynamicSharedMemorySize, N4_SMEM) != hipSuccess)
       status = -1;
@@ -1535,14 +1287,13 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
         muon_set_error("gemm: alpha must be nonzero");
         return MUON_ERR_ARG;
       }
-      if (out_t == nullptr && K % 256 == 0) {
-        // persistent: one workgroup per CU walks the tile list
-        const int cus = device_cus();
-        const int wgs = (int)std::min<int64_t>(blocks, cus);
-        hipLaunchKernelGGL(gemm_bf16_nn4_kernel, dim3((unsigned)wgs), dim3(256), N4_SMEM, stream, g);
-      } else {
-        hipLaunchKernelGGL(gemm_bf16_nn_kernel, grid, dim3(512), NN_SMEM, stream, g);
+      if (out_t != nullptr || K % 256 != 0) {
+        muon_set_error("gemm: bf16 NN products take K a multiple of 256 and no transposed output");
+        return MUON_ERR_ARG;
       }
+      // persistent: one workgroup per CU walks the tile list
+      const int wgs = (int)std::min<int64_t>(blocks, device_cus());
+      hipLaunchKernelGGL(gemm_bf16_nn4_kernel, dim3((unsigned)wgs), dim3(256), N4_SMEM, stream, g);
     } else if (!masked && (alpha != 0.0f || beta == 0.0f)) {
       hipLaunchKernelGGL(gemm_bf16_v2_kernel<MODE_SYRK>, grid, dim3(512), V2_SMEM, stream, g);
     } else {

@@ -36,7 +36,7 @@ _SIGNATURES = {
     "muon_orth_result": (
         _c_int,
         [_c_int, _c_i64, _c_i64, _c_i64, _c_int, ctypes.POINTER(_c_i64),
-         ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64)],
+         ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), ctypes.POINTER(_c_int)],
     ),
     "muon_prepass": (
         _c_int,

@@ -76,11 +76,13 @@ int muon_gram(const void* x, void* y, int dtype, int64_t batch, int64_t M, int64
 /* ---- Orthogonalization workspace ---------------------------------------------- */
 int64_t muon_orth_workspace_bytes(int dtype, int64_t batch, int64_t rows, int64_t cols);
 
-/* Location of the orthogonalized result U (stored layout rows x cols) inside the
- * workspace after muon_orth_run(..., steps, ...): byte offset of matrix 0, row
- * pitch and matrix stride in elements. */
+/* Location of the orthogonalized result U (rows x cols) inside the workspace after
+ * muon_orth_run(..., steps, ...): byte offset of matrix 0, row pitch and matrix stride
+ * in elements of the wide iterate (m x n). *transposed is 1 for a tall matrix
+ * (rows > cols), whose U(r, c) is then at row c, column r of that iterate. */
 int muon_orth_result(int dtype, int64_t batch, int64_t rows, int64_t cols, int steps,
-                     int64_t* offset_bytes, int64_t* row_pitch, int64_t* matrix_stride);
+                     int64_t* offset_bytes, int64_t* row_pitch, int64_t* matrix_stride,
+                     int* transposed);
 
 /* ---- Pre-pass: momentum / Nesterov -> bf16 X (both layouts) + norm partials ------
  * For tensor t < ntensors (each nb matrices of rows x cols, elementwise):

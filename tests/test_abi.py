@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_text():
     lib = _lib.load()
-    assert lib.muon_amd_abi_version() == 1
+    assert lib.muon_amd_abi_version() == 2
     assert isinstance(_lib.last_error(), str)
 
 
@@ -52,21 +52,17 @@ def test_workspace_size_formula():
 def test_result_location_follows_orientation():
     lib = _lib.load()
     off, pitch, mst = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    trans = ctypes.c_int()
     x1 = 4 * 256 * 512 * 2  # byte offset of the second iterate buffer
-    # wide: X[steps % 2] in the wide layout
-    assert lib.muon_orth_result(_lib.DT_BF16, 4, 100, 300, 5, off, pitch, mst) == 0
-    assert off.value == x1 and pitch.value == 512 and mst.value == 256 * 512
-    assert lib.muon_orth_result(_lib.DT_BF16, 4, 100, 300, 4, off, pitch, mst) == 0
-    assert off.value == 0 and pitch.value == 512
-    assert lib.muon_orth_result(_lib.DT_BF16, 4, 100, 300, 0, off, pitch, mst) == 0
-    assert off.value == 0
-    # tall: the transposed result, pitch m_pad, in X[steps % 2] (X1 for steps == 0)
-    assert lib.muon_orth_result(_lib.DT_BF16, 4, 300, 100, 5, off, pitch, mst) == 0
-    assert off.value == x1 and pitch.value == 256
-    assert lib.muon_orth_result(_lib.DT_BF16, 4, 300, 100, 4, off, pitch, mst) == 0
-    assert off.value == 0 and pitch.value == 256
-    assert lib.muon_orth_result(_lib.DT_BF16, 4, 300, 100, 0, off, pitch, mst) == 0
-    assert off.value == x1
+    # the result is X[steps % 2] in the wide layout (pitch n_pad) for both orientations;
+    # a tall matrix's result is flagged as transposed
+    for rows, cols, t in ((100, 300, 0), (300, 100, 1)):
+        assert lib.muon_orth_result(_lib.DT_BF16, 4, rows, cols, 5, off, pitch, mst, trans) == 0
+        assert (off.value, pitch.value, mst.value, trans.value) == (x1, 512, 256 * 512, t)
+        assert lib.muon_orth_result(_lib.DT_BF16, 4, rows, cols, 4, off, pitch, mst, trans) == 0
+        assert (off.value, pitch.value, trans.value) == (0, 512, t)
+        assert lib.muon_orth_result(_lib.DT_BF16, 4, rows, cols, 0, off, pitch, mst, trans) == 0
+        assert (off.value, trans.value) == (0, t)
 
 
 @pytest.mark.parametrize(
