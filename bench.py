@@ -247,10 +247,10 @@ def main() -> None:
     gms, gn, gwork = kern["gemm_bx"]
     avg_ms = gms / max(gn, 1)
     achieved = (gwork / max(gn, 1)) / (avg_ms * 1e-3) / 1e12
-    traffic, traffic_src = _measured_traffic("gemm_bf16_nn_kernel", args.config, args.lp)
+    traffic, traffic_src = _measured_traffic("gemm_bf16_nn4_kernel", args.config, args.lp)
     roofline = {
         "bound": "mfma",
-        "kernel": "gemm_bf16_nn_kernel (X' = a X + B X)",
+        "kernel": "gemm_bf16_nn4_kernel (X' = a X + B X)",
         "achieved": round(achieved, 1),
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",

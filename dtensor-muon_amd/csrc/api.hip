@@ -144,6 +144,7 @@ OrthLayout muon_orth_layout(int dtype, int64_t batch, int64_t rows, int64_t cols
   L.off_b = take(as);
   L.off_part = take((size_t)(batch * L.parts * 4));
   L.off_scale = take((size_t)(batch * 4));
+  L.off_qtab = take((size_t)MUON_QTAB_BYTES);
   L.total = off;
   return L;
 }

@@ -126,40 +126,34 @@ struct Vec8<MUON_DT_F16> {
 // fp32 -> float8_e4m3fn (bias 7, no infinities, 0x7f/0xff are NaN, max 448).
 // Written from the format definition: exact round-to-nearest-even onto the e4m3fn
 // grid; a magnitude that rounds above 448 becomes NaN (matching torch's cast).
+// Branch-free (both the subnormal and the normal rounding are formed, one selected).
 MUON_DEVICE uint8_t f32_to_e4m3fn(float f) {
-  uint32_t u = __float_as_uint(f);
-  uint8_t sign = (uint8_t)((u >> 24) & 0x80u);
-  uint32_t a = u & 0x7fffffffu;
-  if (a > 0x7f800000u) return (uint8_t)(sign | 0x7f);  // NaN
-  // Values >= 464 (the midpoint between 448 and the next, unrepresentable, grid
-  // point 480) round above the largest finite value. 464 itself ties to even (448).
-  if (a > 0x43e80000u) return (uint8_t)(sign | 0x7f);  // > 464 -> NaN (inf too)
-  if (a < 0x3c800000u) {
-    // |f| < 2^-6: subnormal range of e4m3 (step 2^-9). Round |f| * 2^9 to an integer
-    // with ties-to-even; exact in fp32 because the scaling is a power of two.
-    float s = __uint_as_float(a) * 512.0f;
-    float r = __builtin_rintf(s);  // current rounding mode = nearest-even
-    return (uint8_t)(sign | (uint8_t)r);  // r in [0, 8]; 8 == smallest normal 0x08
-  }
-  // Normal range: keep 3 mantissa bits, round to nearest even on the dropped 20 bits.
-  uint32_t exp = (a >> 23) - 127 + 7;  // e4m3 biased exponent, >= 1 here
-  uint32_t mant = a & 0x7fffffu;
-  uint32_t q = (exp << 3) | (mant >> 20);
-  uint32_t rem = mant & 0xfffffu;
-  if (rem > 0x80000u || (rem == 0x80000u && (q & 1u))) q += 1;
-  return (uint8_t)(sign | (uint8_t)q);  // q <= 0x7e guaranteed by the 464 bound
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  // |f| < 2^-6: subnormal range of e4m3 (step 2^-9). |f| * 2^9 rounded to an integer with
+  // ties-to-even is exact in fp32 (power-of-two scaling); 8 is the smallest normal 0x08.
+  const uint32_t sub = (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.0f);
+  // normal range: keep 3 mantissa bits, round to nearest even on the dropped 20 bits
+  uint32_t q = ((((a >> 23) - 120u) << 3) | ((a >> 20) & 7u)) & 0xffu;
+  const uint32_t rem = a & 0xfffffu;
+  q += (rem > 0x80000u || (rem == 0x80000u && (q & 1u))) ? 1u : 0u;
+  uint32_t r = a < 0x3c800000u ? sub : q;
+  // values >= 464 (the midpoint between 448 and the next, unrepresentable, grid point
+  // 480) round above the largest finite value; 464 itself ties to even (448). NaN and
+  // infinity land here too.
+  r = a > 0x43e80000u ? 0x7fu : r;
+  return (uint8_t)(sign | r);
 }
 
 MUON_DEVICE float e4m3fn_to_f32(uint8_t v) {
-  uint32_t sign = ((uint32_t)v & 0x80u) << 24;
-  uint32_t e = (v >> 3) & 0xfu;
-  uint32_t m = v & 0x7u;
-  if (e == 0xf && m == 0x7) return __uint_as_float(sign | 0x7fc00000u);
-  if (e == 0) {
-    float r = (float)m * 0.001953125f;  // m * 2^-9
-    return sign ? -r : r;
-  }
-  return __uint_as_float(sign | ((e - 7 + 127) << 23) | (m << 20));
+  const uint32_t sign = ((uint32_t)v & 0x80u) << 24;
+  const uint32_t e = (v >> 3) & 0xfu;
+  const uint32_t m = v & 0x7u;
+  const float sub = (float)m * 0.001953125f;  // m * 2^-9, exact
+  uint32_t bits = e == 0 ? __float_as_uint(sub) : (((e + 120u) << 23) | (m << 20));
+  bits = (e == 0xf && m == 0x7) ? 0x7fc00000u : bits;
+  return __uint_as_float(sign | bits);
 }
 
 MUON_DEVICE float warp_sum(float v) {
@@ -200,7 +194,15 @@ struct OrthLayout {
   int es;              // element size of the iteration dtype
   int64_t batch;       // capacity in matrices
   int64_t parts;       // norm partials per matrix
-  size_t off_x0, off_x1, off_a, off_b, off_part, off_scale, total;
+  size_t off_x0, off_x1, off_a, off_b, off_part, off_scale, off_qtab, total;
 };
+
+// Code-search tables of the 8/4-bit quantized state (lp.hip): one byte per bucket of the
+// order-preserving key of an fp32 value (key >> 18), then 256 + MUON_QTHR_PAD uint32
+// thresholds.
+constexpr int MUON_QTAB_SHIFT = 18;
+constexpr int MUON_QTAB_SIZE = 1 << (32 - MUON_QTAB_SHIFT);
+constexpr int MUON_QTHR_PAD = 4;
+constexpr int MUON_QTAB_BYTES = MUON_QTAB_SIZE + (256 + MUON_QTHR_PAD) * 4;
 
 OrthLayout muon_orth_layout(int dtype, int64_t batch, int64_t rows, int64_t cols);

@@ -5,13 +5,18 @@
 // (optim_lp.py:118-133): scale = max(|x|) over the block clipped at 1e-12 (divided by
 // 448 for fp8), y = x / scale, and for the map formats the code is found by a
 // fixed-depth binary search over the sorted map followed by a round-half-up step
-// between the two neighbouring entries. One wavefront owns one block; the block is
-// read twice (absmax, then quantize) with the second read served from cache.
+// between the two neighbouring entries. The general kernel: one wavefront owns one
+// block, read twice (absmax, then quantize) with the second read served from cache; the
+// tiled kernel (below) keeps each block in registers and finds 8-bit codes through a
+// bucket table that gives the same result as the search.
 #include <algorithm>
 
 #include "common.h"
 
 namespace {
+
+typedef __attribute__((ext_vector_type(2))) float f2x;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf2x;  // v_cvt_pk_bf16_f32 (RNE)
 
 struct LpArgs {
   void* grads[MUON_MAX_TENSORS];
@@ -26,17 +31,23 @@ struct LpArgs {
   int nesterov, maximize;
 };
 
+// Largest i with q[i] <= y over a sorted 256-entry map (0 if none, or y NaN).
+MUON_DEVICE int quant_search8(float y, const float* q) {
+  int c = (y >= q[128]) ? 128 : 0;
+  c += (y >= q[c + 64]) ? 64 : 0;
+  c += (y >= q[c + 32]) ? 32 : 0;
+  c += (y >= q[c + 16]) ? 16 : 0;
+  c += (y >= q[c + 8]) ? 8 : 0;
+  c += (y >= q[c + 4]) ? 4 : 0;
+  c += (y >= q[c + 2]) ? 2 : 0;
+  c += (y >= q[c + 1]) ? 1 : 0;
+  return c;
+}
+
 template <int QF>
 MUON_DEVICE int quant_code(float y, const float* q) {
   if (QF == MUON_Q_8BIT) {
-    int c = (y >= q[128]) ? 128 : 0;
-    c += (y >= q[c + 64]) ? 64 : 0;
-    c += (y >= q[c + 32]) ? 32 : 0;
-    c += (y >= q[c + 16]) ? 16 : 0;
-    c += (y >= q[c + 8]) ? 8 : 0;
-    c += (y >= q[c + 4]) ? 4 : 0;
-    c += (y >= q[c + 2]) ? 2 : 0;
-    c += (y >= q[c + 1]) ? 1 : 0;
+    const int c = quant_search8(y, q);
     const int up = c + 1 > 255 ? 255 : c + 1;
     const float lo = q[c], hi = q[up];
     const float res = y - lo;
@@ -167,6 +178,7 @@ struct LpTileArgs {
   int block_shift;          // log2(block)
   void* x0;                 // X0 of matrix 0 of this launch
   int64_t x_pitch, x_mstride;
+  const uint8_t* qtab;      // 8/4-bit: bucket table (MUON_QTAB_SIZE bytes), then thresholds
   float* partials;          // partials of matrix 0 of this launch
   int64_t parts;            // partial slots per matrix
   int tiles_c, tiles_used;  // column tiles (cols / 256), tiles with data or padding
@@ -214,23 +226,110 @@ MUON_DEVICE float code_value(int code, const float* q) {
   return q[code];
 }
 
+// ---- faster exact code search ------------------------------------------------------
+// Order-preserving integer key of a non-NaN fp32 value (larger value, larger key), and
+// the value of a key (the smallest value of bucket b is the value of key b << SHIFT).
+MUON_DEVICE uint32_t f32_order_key(float v) {
+  const uint32_t b = __float_as_uint(v);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+MUON_DEVICE float f32_from_order_key(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// The code as a function of y (search, then the half-step rule, in fp32) never
+// decreases as y grows: within [q[c], q[c+1]) the rounded difference y - q[c] grows with
+// y, and at q[c+1] the search moves up. So code(y) is the number of thresholds
+// thr[k] <= key(y), thr[k] = the smallest order key whose value codes to at least k + 1
+// (k < nq - 1; the entries from nq - 1 on are 0xffffffff). The thresholds are found by
+// bisection over keys with quant_code itself, so the count reproduces it bit for bit.
+// One thread per threshold; one workgroup.
+template <int QF>
+__global__ __launch_bounds__(256) void build_qthr_kernel(const float* qmap, uint32_t* thr) {
+  constexpr int NQ = QF == MUON_Q_8BIT ? 256 : 16;
+  __shared__ float q[256];
+  const int k = threadIdx.x;
+  q[k] = qmap[k < NQ ? k : 0];
+  __syncthreads();
+  uint32_t t = 0xffffffffu;
+  if (k < NQ - 1) {
+    uint32_t lo = f32_order_key(-__builtin_inff()), hi = f32_order_key(__builtin_inff());
+    while (lo < hi) {
+      const uint32_t mid = lo + (hi - lo) / 2;
+      if (quant_code<QF>(f32_from_order_key(mid), q) >= k + 1)
+        hi = mid;
+      else
+        lo = mid + 1;
+    }
+    t = lo;
+  }
+  thr[k] = t;
+  if (k < MUON_QTHR_PAD) thr[256 + k] = 0xffffffffu;
+}
+
+// qtab[b] = the number of thresholds <= b << SHIFT (the code of the smallest value of
+// key bucket b). For y in bucket b the code is qtab[b] plus the thresholds of bucket b
+// up to key(y): at most 2 for the standard 8-bit map (1 for the 4-bit map), which the
+// lookup steps over; a map with more takes the full count. One thread per bucket.
+__global__ __launch_bounds__(256) void build_qtab_kernel(const uint32_t* thr, int nq,
+                                                         uint8_t* qtab) {
+  const uint32_t b = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t key = b << MUON_QTAB_SHIFT;
+  int lo = 0, hi = nq - 1;  // thr[nq - 1] = 0xffffffff bounds the count
+  while (lo < hi) {
+    const int mid = (lo + hi) / 2;
+    if (thr[mid] <= key)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  qtab[b] = (uint8_t)lo;
+}
+
+// quant_code<QF> (8- or 4-bit) through the thresholds: a table read and two compares,
+// branch-free so the compiler can overlap the lookups of many values. Sets `more` when the
+// bucket holds more thresholds than that (then quant_code_thr_all gives the code).
+MUON_DEVICE int quant_code_thr(float y, const uint32_t* thr, const uint8_t* qtab, bool& more) {
+  const uint32_t ky = f32_order_key(y);
+  const int c0 = qtab[ky >> MUON_QTAB_SHIFT];
+  const int c = c0 + (ky >= thr[c0] ? 1 : 0) + (ky >= thr[c0 + 1] ? 1 : 0);
+  more = more || ky >= thr[c0 + 2];
+  return (y != y) ? 0 : c;  // NaN: the search gives 0 and the half-step test fails
+}
+
+// The code as the full count of thresholds <= key(y).
+template <int NQ>
+MUON_DEVICE int quant_code_thr_all(float y, const uint32_t* thr) {
+  const uint32_t ky = f32_order_key(y);
+  int lo = 0, hi = NQ - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi) / 2;
+    if (thr[mid] <= ky)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return (y != y) ? 0 : lo;
+}
+
 template <int GDT, int QF, bool TALL>
 __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
 #pragma clang fp contract(off)
+  constexpr bool MAP = QF != MUON_Q_FP8;
   __shared__ float q[256];
+  __shared__ __align__(16) uint8_t qtab[MAP ? MUON_QTAB_SIZE : 16];
+  __shared__ __align__(16) uint32_t qthr[MAP ? 256 + MUON_QTHR_PAD : 4];
   __shared__ bf16_t tileT[TALL ? LPT_ROWS : 1][TALL ? LPT_PITCH : 1];
   __shared__ float wsum[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (QF != MUON_Q_FP8) q[tid] = a.qmap[tid < (QF == MUON_Q_8BIT ? 256 : 16) ? tid : 0];
   const int mat = blockIdx.y;
-  const int t = (int)(mat / a.nb);
-  const int64_t mb = mat % a.nb;
   float* part = a.partials + (int64_t)mat * a.parts;
   if ((int)blockIdx.x >= a.tiles_used) {
     if (tid == 0) part[blockIdx.x] = 0.0f;
     return;
   }
-  __syncthreads();
+  const int t = (int)(mat / a.nb);
+  const int64_t mb = mat % a.nb;
   const int tr = blockIdx.x / a.tiles_c, tcol = blockIdx.x % a.tiles_c;
   const int64_t r0 = (int64_t)tr * LPT_ROWS, c0 = (int64_t)tcol * LPT_COLS;
   const void* gp = a.grads[t];
@@ -241,58 +340,101 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
   const int64_t c = c0 + chunk * 8;
   const int block_lanes = 1 << (a.block_shift - 3);
   const float mom = a.momentum;
+  constexpr int NP = LPT_ROWS / 8;
+
+  // every global load of the tile first (gradient, code bytes, old scale per pass)
+  float g[NP][8];
+  typename LpCodes<QF>::T cw[NP];
+  float osc[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int64_t r = r0 + p * 8 + rsub;
+    if (r < a.rows) {
+      const int64_t e = (mb * a.rows + r) * a.cols + c;  // element index in the tensor
+      Vec8<GDT>::load(gp, e, g[p]);
+      cw[p] = LpCodes<QF>::load(codes, e);
+      osc[p] = scales[e >> a.block_shift];
+    }
+  }
+  if (MAP) {
+    q[tid] = a.qmap[tid < (QF == MUON_Q_8BIT ? 256 : 16) ? tid : 0];
+#pragma unroll
+    for (int i = 0; i < MUON_QTAB_SIZE / 16 / 256; ++i)
+      ((uint4*)qtab)[i * 256 + tid] = ((const uint4*)a.qtab)[i * 256 + tid];
+    const uint32_t* gthr = (const uint32_t*)(a.qtab + MUON_QTAB_SIZE);
+    qthr[tid] = gthr[tid];
+    if (tid < MUON_QTHR_PAD) qthr[256 + tid] = gthr[256 + tid];
+  }
+  __syncthreads();
+
   bf16_t* x0 = (bf16_t*)a.x0 + (int64_t)mat * a.x_mstride;
   float ss = 0.0f;
-#pragma unroll 2
-  for (int p = 0; p < LPT_ROWS / 8; ++p) {
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
     const int rl = p * 8 + rsub;
     const int64_t r = r0 + rl;
     const bool valid = r < a.rows;
-    float xv[8];
+    uint32_t xw[4];  // X as bf16 pairs (RNE), element 2i in the low half
     if (valid) {
-      const int64_t e = (mb * a.rows + r) * a.cols + c;  // element index in the tensor
-      const int64_t blk = e >> a.block_shift;
-      float g[8];
-      Vec8<GDT>::load(gp, e, g);
-      const typename LpCodes<QF>::T cw = LpCodes<QF>::load(codes, e);
-      const float old_scale = scales[blk];
-      float m[8];
+      const int64_t e = (mb * a.rows + r) * a.cols + c;
+      float m[8], gq[8];
       float amax = 0.0f;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        if (a.maximize) g[k] = -g[k];
-        float v = code_value<QF>(LpCodes<QF>::get(cw, k), q) * old_scale;
+        if (a.maximize) g[p][k] = -g[p][k];
+        float v = code_value<QF>(LpCodes<QF>::get(cw[p], k), q) * osc[p];
         v = v * mom;
-        m[k] = v + g[k];
+        m[k] = v + g[p][k];
         amax = fmaxf(amax, fabsf(m[k]));
       }
       // absmax over the block_lanes consecutive lanes of this block (all in one row)
       for (int off = 1; off < block_lanes; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
       float sc = amax > 1e-12f ? amax : 1e-12f;
       if (QF == MUON_Q_FP8) sc = sc / 448.0f;
+      float ys[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ys[k] = m[k] / sc;
       int cq[8];
+      if (QF == MUON_Q_FP8) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) cq[k] = f32_to_e4m3fn(ys[k]);
+      } else {
+        bool more = false;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) cq[k] = quant_code_thr(ys[k], qthr, qtab, more);
+        if (more) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            cq[k] = quant_code_thr_all<QF == MUON_Q_8BIT ? 256 : 16>(ys[k], qthr);
+        }
+      }
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        cq[k] = quant_code<QF>(m[k] / sc, q);
-        float gq = m[k];
+        gq[k] = m[k];
         if (a.nesterov) {
           const float tt = m[k] * mom;
-          gq = g[k] + tt;
+          gq[k] = g[p][k] + tt;
         }
-        xv[k] = Elem<MUON_DT_BF16>::round(gq);
-        ss += xv[k] * xv[k];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f2x v = {gq[2 * i], gq[2 * i + 1]};
+        xw[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2x));
+        const float lo = __uint_as_float(xw[i] << 16), hi = __uint_as_float(xw[i] & 0xffff0000u);
+        ss += lo * lo;
+        ss += hi * hi;
       }
       LpCodes<QF>::store(codes, e, cq);
-      if ((chunk & (block_lanes - 1)) == 0) scales[blk] = sc;
+      if ((chunk & (block_lanes - 1)) == 0) scales[e >> a.block_shift] = sc;
     } else {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) xv[k] = 0.0f;
+      for (int i = 0; i < 4; ++i) xw[i] = 0u;
     }
     if (TALL) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) tileT[rl][chunk * 8 + k] = f32_to_bf16(xv[k]);
+      for (int i = 0; i < 4; ++i) *(uint32_t*)&tileT[rl][chunk * 8 + 2 * i] = xw[i];
     } else {
-      Vec8<MUON_DT_BF16>::store(x0, r * a.x_pitch + c, xv);
+      *(uint4*)(x0 + r * a.x_pitch + c) = make_uint4(xw[0], xw[1], xw[2], xw[3]);
     }
   }
   if (TALL) {
@@ -473,6 +615,7 @@ int muon_launch_lp_prepass_tiled(int ntensors, void* const* grads, int gdt, void
   a.x_mstride = mst;
   a.partials = (float*)((char*)ws + L.off_part) + mat0 * L.parts;
   a.parts = L.parts;
+  a.qtab = (const uint8_t*)ws + L.off_qtab;
   const int64_t rows_pad = L.tall ? L.n_pad : L.m_pad;
   a.tiles_c = (int)(cols / LPT_COLS);
   a.tiles_used = (int)((rows_pad / LPT_ROWS) * a.tiles_c);
@@ -480,6 +623,17 @@ int muon_launch_lp_prepass_tiled(int ntensors, void* const* grads, int gdt, void
   a.momentum = momentum;
   a.nesterov = nesterov;
   a.maximize = maximize;
+  if (qf != MUON_Q_FP8 && mat0 == 0) {
+    // thresholds and bucket table of this map, rebuilt per call (a few microseconds)
+    uint8_t* tab = (uint8_t*)ws + L.off_qtab;
+    uint32_t* thr = (uint32_t*)(tab + MUON_QTAB_SIZE);
+    if (qf == MUON_Q_8BIT)
+      hipLaunchKernelGGL(build_qthr_kernel<MUON_Q_8BIT>, dim3(1), dim3(256), 0, s, qmap, thr);
+    else
+      hipLaunchKernelGGL(build_qthr_kernel<MUON_Q_4BIT>, dim3(1), dim3(256), 0, s, qmap, thr);
+    hipLaunchKernelGGL(build_qtab_kernel, dim3(MUON_QTAB_SIZE / 256), dim3(256), 0, s,
+                       (const uint32_t*)thr, qf == MUON_Q_8BIT ? 256 : 16, tab);
+  }
   dim3 grid((unsigned)L.parts, (unsigned)(ntensors * nb));
   switch (gdt) {
     case MUON_DT_F32: launch_lp_tile_q<MUON_DT_F32>(qf, L.tall, a, grid, s); break;
