@@ -124,6 +124,55 @@ def cpu_baseline(config: str = "llama", min_seconds: float = 10.0) -> dict:
     }
 
 
+def blas_ceiling(config: str, dev, reps: int = 3) -> dict:
+    """Library reference for the orthogonalization: per bucket of the workload, the three
+    products of one iteration with torch.bmm (hipBLASLt, dense: X X^T and A A computed in
+    full) on random bf16 operands. Reports each product's dense TFLOP/s and the time the
+    library would take for the workload's 5 iterations, next to the symmetric-minimal
+    FLOPs the step is credited with."""
+    import torch
+
+    counts: dict[tuple, int] = {}
+    for s in _shapes(config):
+        key = (min(s[-2:]), max(s[-2:]))
+        counts[key] = counts.get(key, 0) + math.prod(s[:-2])
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        ev0.record()
+        for _ in range(reps):
+            fn()
+        ev1.record()
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) / reps
+
+    out, total_ms, total_flops = {}, 0.0, 0.0
+    gen = torch.Generator(device=dev).manual_seed(0)
+    for (m, n), count in counts.items():
+        X = torch.randn(count, m, n, device=dev, generator=gen).bfloat16()
+        XT = X.transpose(1, 2).contiguous()  # transposed operands made contiguous
+        A = torch.randn(count, m, m, device=dev, generator=gen).bfloat16()
+        t_xx = timed(lambda: torch.bmm(X, XT))
+        t_aa = timed(lambda: torch.bmm(A, A))
+        t_bx = timed(lambda: torch.bmm(A, X))
+        d = 2.0 * count
+        out[f"{m}x{n}x{count}"] = {
+            "xxT_ms": round(t_xx, 3), "xxT_tflops": round(d * m * m * n / t_xx / 1e9, 1),
+            "aa_ms": round(t_aa, 3), "aa_tflops": round(d * m * m * m / t_aa / 1e9, 1),
+            "bx_ms": round(t_bx, 3), "bx_tflops": round(d * m * m * n / t_bx / 1e9, 1),
+        }
+        total_ms += 5 * (t_xx + t_aa + t_bx)
+        total_flops += 5 * count * (m * (m + 1) * n + m * (m + 1) * m + 2 * m * m * n)
+        del X, XT, A
+        torch.cuda.empty_cache()
+    return {"blas_ceiling": "torch.bmm (hipBLASLt), bf16, dense products", "config": config,
+            "buckets": out, "orth_ms_per_step": round(total_ms, 3),
+            "orth_tflops_symmetric_minimal": round(total_flops / (total_ms * 1e-3) / 1e12, 1)}
+
+
 def _measured_traffic(kernel: str, config: str, lp):
     """HBM bytes per dispatch of `kernel` from the committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE, each scaled by a 1 GiB copy), for the workload it was
@@ -151,6 +200,9 @@ def main() -> None:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device-to-device copy 5 times (PMC calibration)")
+    ap.add_argument("--blas-ceiling", action="store_true",
+                    help="only time the iteration's three products per bucket with torch.bmm "
+                         "(hipBLASLt) as a library reference")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -175,6 +227,9 @@ def main() -> None:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": src.numel() * 2, "dispatches": 5}))
+        return
+    if args.blas_ceiling:
+        print(json.dumps(blas_ceiling(args.config, dev)), flush=True)
         return
     shapes = _shapes(args.config)
     strategy = args.strategy or ("newton_schulz" if args.config == "moe" else "polar_express")
