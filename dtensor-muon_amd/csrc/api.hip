@@ -32,8 +32,12 @@ int muon_launch_scale(const OrthLayout& L, void* x, int wdt, int64_t batch, cons
                       hipStream_t s);
 int muon_launch_postpass(int ntensors, void* const* params, const float* adj, int pdt,
                          const void* u, int udt, int64_t u_pitch, int64_t u_mstride, int u_trans,
-                         int64_t nb, int64_t rows, int64_t cols, float wd, int cautious,
-                         hipStream_t s);
+                         const float* rscale, int64_t rs_mstride, int64_t nb, int64_t rows,
+                         int64_t cols, float wd, int cautious, hipStream_t s);
+int muon_launch_normuon_stats(int ntensors, void* const* vars, int vdt, const void* u, int udt,
+                              int64_t u_pitch, int64_t u_mstride, int u_trans, int64_t nb,
+                              int64_t rows, int64_t cols, float* ss, int64_t ss_mstride,
+                              const int64_t* split_start, int nsplits, float w, hipStream_t s);
 int muon_launch_extract(const void* src, int wdt, int64_t pitch, int64_t mstride, int trans,
                         void* dst, int odt, int64_t rows, int64_t cols, int64_t batch,
                         hipStream_t s);
@@ -145,6 +149,7 @@ OrthLayout muon_orth_layout(int dtype, int64_t batch, int64_t rows, int64_t cols
   L.off_part = take((size_t)(batch * L.parts * 4));
   L.off_scale = take((size_t)(batch * 4));
   L.off_qtab = take((size_t)MUON_QTAB_BYTES);
+  L.off_rows = take((size_t)(batch * L.n_pad * 4));  // per stored row (NorMuon)
   L.total = off;
   return L;
 }
@@ -400,8 +405,98 @@ int muon_postpass(int ntensors, void* const* params, int p_dtype, const void* u,
   for (int t0 = 0; t0 < ntensors; t0 += MUON_MAX_TENSORS) {
     const int cnt = std::min(MUON_MAX_TENSORS, ntensors - t0);
     int rc = muon_launch_postpass(cnt, params + t0, adjusted_lrs + t0, p_dtype,
-                                  ubase + (int64_t)t0 * nb * mst * es, udt, pitch, mst, trans, nb,
-                                  rows, cols, wd, cautious, s);
+                                  ubase + (int64_t)t0 * nb * mst * es, udt, pitch, mst, trans,
+                                  nullptr, 0, nb, rows, cols, wd, cautious, s);
+    if (rc != MUON_OK) return rc;
+  }
+  return MUON_OK;
+}
+
+int muon_normuon_postpass(int ntensors, void* const* params, int p_dtype,
+                          void* const* variances, int v_dtype, const void* u, int u_dtype,
+                          void* ws, int ws_dtype, int64_t ws_batch, int steps, int64_t nb,
+                          int64_t rows, int64_t cols, const int64_t* split_sizes, int nsplits,
+                          const float* adjusted_lrs, float wd, int cautious, double beta2,
+                          void* stream) {
+  if (!io_dtype_ok(p_dtype) || !io_dtype_ok(v_dtype)) {
+    muon_set_error("normuon_postpass: unsupported param/variance dtype (%d, %d)", p_dtype,
+                   v_dtype);
+    return MUON_ERR_DTYPE;
+  }
+  if (ntensors < 0 || nb <= 0 || rows <= 0 || cols <= 0) {
+    muon_set_error("normuon_postpass: bad extents");
+    return MUON_ERR_SHAPE;
+  }
+  if (!ws || !iter_dtype_ok(ws_dtype) || (int64_t)ntensors * nb > ws_batch) {
+    muon_set_error("normuon_postpass: a workspace for the %lld matrices is required",
+                   (long long)ntensors * nb);
+    return MUON_ERR_ARG;
+  }
+  // row blocks: the whole matrix, or split_sizes summing to rows
+  int64_t starts[MUON_MAX_SPLITS + 1];
+  int nb_split = 1;
+  starts[0] = 0;
+  starts[1] = rows;
+  if (split_sizes && nsplits > 0) {
+    if (nsplits > MUON_MAX_SPLITS) {
+      muon_set_error("normuon_postpass: %d row blocks exceed the maximum %d", nsplits,
+                     MUON_MAX_SPLITS);
+      return MUON_ERR_ARG;
+    }
+    int64_t acc = 0;
+    for (int i = 0; i < nsplits; ++i) {
+      if (split_sizes[i] <= 0) {
+        muon_set_error("normuon_postpass: row block %d has size %lld", i,
+                       (long long)split_sizes[i]);
+        return MUON_ERR_SHAPE;
+      }
+      starts[i] = acc;
+      acc += split_sizes[i];
+    }
+    if (acc != rows) {
+      muon_set_error("normuon_postpass: row blocks sum to %lld, not %lld rows", (long long)acc,
+                     (long long)rows);
+      return MUON_ERR_SHAPE;
+    }
+    starts[nsplits] = rows;
+    nb_split = nsplits;
+  }
+  OrthLayout L = muon_orth_layout(ws_dtype, ws_batch, rows, cols);
+  const char* ubase;
+  int udt, trans = 0;
+  int64_t pitch, mst;
+  if (u) {
+    if (!io_dtype_ok(u_dtype)) {
+      muon_set_error("normuon_postpass: unsupported update dtype %d", u_dtype);
+      return MUON_ERR_DTYPE;
+    }
+    ubase = (const char*)u;
+    udt = u_dtype;
+    pitch = cols;
+    mst = rows * cols;
+  } else {
+    int64_t off;
+    int rc = muon_orth_result(ws_dtype, ws_batch, rows, cols, steps, &off, &pitch, &mst, &trans);
+    if (rc != MUON_OK) return rc;
+    ubase = (const char*)ws + off;
+    udt = ws_dtype;
+  }
+  const int es = udt == MUON_DT_F32 ? 4 : 2;
+  const int pes = p_dtype == MUON_DT_F32 ? 4 : 2;
+  hipStream_t s = (hipStream_t)stream;
+  float* ss = (float*)((char*)ws + L.off_rows);
+  const int64_t ss_mst = L.n_pad;  // stored rows <= n <= n_pad
+  const float w = (float)(1.0 - beta2);
+  Timed timed(MUON_K_POSTPASS, (2.0 * es + 2.0 * pes) * (double)ntensors * nb * rows * cols, s);
+  for (int t0 = 0; t0 < ntensors; t0 += MUON_MAX_TENSORS) {
+    const int cnt = std::min(MUON_MAX_TENSORS, ntensors - t0);
+    const char* uc = ubase + (int64_t)t0 * nb * mst * es;
+    float* ssc = ss + (int64_t)t0 * nb * ss_mst;
+    int rc = muon_launch_normuon_stats(cnt, variances + t0, v_dtype, uc, udt, pitch, mst, trans,
+                                       nb, rows, cols, ssc, ss_mst, starts, nb_split, w, s);
+    if (rc != MUON_OK) return rc;
+    rc = muon_launch_postpass(cnt, params + t0, adjusted_lrs + t0, p_dtype, uc, udt, pitch, mst,
+                              trans, ssc, ss_mst, nb, rows, cols, wd, cautious, s);
     if (rc != MUON_OK) return rc;
   }
   return MUON_OK;

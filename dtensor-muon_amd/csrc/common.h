@@ -194,7 +194,7 @@ struct OrthLayout {
   int es;              // element size of the iteration dtype
   int64_t batch;       // capacity in matrices
   int64_t parts;       // norm partials per matrix
-  size_t off_x0, off_x1, off_a, off_b, off_part, off_scale, off_qtab, total;
+  size_t off_x0, off_x1, off_a, off_b, off_part, off_scale, off_qtab, off_rows, total;
 };
 
 // Code-search tables of the 8/4-bit quantized state (lp.hip): one byte per bucket of the

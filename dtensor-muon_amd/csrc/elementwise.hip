@@ -244,6 +244,8 @@ struct PostArgs {
   float adj[MUON_MAX_TENSORS];
   const void* u;        // matrix 0 of this launch; (TRANS) U(r, c) at u[c * u_pitch + r]
   int64_t u_pitch, u_mstride;
+  const float* rscale;  // (ROWSCALE) per stored row multiplier, matrix 0 of this launch
+  int64_t rs_mstride;
   int64_t nb, rows, cols;
   int tiles_c;
   float wd;
@@ -275,7 +277,9 @@ MUON_DEVICE float apply_elem(float p, float u, float wd, int cautious, float adj
 // workspace after the iteration); the 64 x 64 block u[c0 .. c0+63][r0 .. r0+63] is read
 // with coalesced 16-byte loads and transposed through LDS. Its extents are padded to the
 // 256-element tile, so the block is in bounds.
-template <int PDT, int UDT, int VEC, bool TRANS>
+// ROWSCALE (NorMuon): u is first multiplied by its row's scale and the result is an fp32
+// tensor, so the apply runs in fp32 whatever U's storage dtype (normuon.py:44-55, 125-134).
+template <int PDT, int UDT, int VEC, bool TRANS, bool ROWSCALE>
 __global__ __launch_bounds__(256) void postpass_kernel(PostArgs a) {
 #pragma clang fp contract(off)
   const int mat = blockIdx.y;
@@ -319,8 +323,14 @@ __global__ __launch_bounds__(256) void postpass_kernel(PostArgs a) {
       } else {
         Vec8<UDT>::load(a.u, ui, u);
       }
+      if constexpr (ROWSCALE) {
+        const float rs = a.rscale[(int64_t)mat * a.rs_mstride + r];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = apply_elem<PDT, UDT>(p[e], u[e], a.wd, a.cautious, adj);
+        for (int e = 0; e < 8; ++e) u[e] = u[e] * rs;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        o[e] = apply_elem<PDT, ROWSCALE ? MUON_DT_F32 : UDT>(p[e], u[e], a.wd, a.cautious, adj);
       Vec8<PDT>::store(pp, pi, o);
     } else {
 #pragma unroll
@@ -330,11 +340,139 @@ __global__ __launch_bounds__(256) void postpass_kernel(PostArgs a) {
         const int64_t pi = mb * a.rows * a.cols + r * a.cols + c;
         const int64_t ui = (int64_t)mat * a.u_mstride + r * a.u_pitch + c;
         const float p = Elem<PDT>::load(pp, pi);
-        const float u = TRANS ? ut[r - r0][cl + e] : Elem<UDT>::load(a.u, ui);
-        Elem<PDT>::store(pp, pi, apply_elem<PDT, UDT>(p, u, a.wd, a.cautious, adj));
+        float u = TRANS ? ut[r - r0][cl + e] : Elem<UDT>::load(a.u, ui);
+        if (ROWSCALE) u = u * a.rscale[(int64_t)mat * a.rs_mstride + r];
+        Elem<PDT>::store(pp, pi,
+                         apply_elem<PDT, ROWSCALE ? MUON_DT_F32 : UDT>(p, u, a.wd, a.cautious, adj));
       }
     }
   }
+}
+
+// ---- NorMuon ---------------------------------------------------------------------------
+// ss[r] = sum over the columns of stored row r of U^2 (fp32, fixed order), for the 64
+// stored rows r0 .. r0+63 of one matrix per workgroup. TRANS: U is the wide iterate of a
+// tall matrix, stored row r = its column r (lanes over r, coalesced; the 4 waves split the
+// columns and are combined in order). Otherwise lanes stride over the columns of a row
+// (VEC consecutive values each) and a butterfly sums them.
+struct RowSsArgs {
+  const void* u;  // matrix 0 of this launch
+  int64_t u_pitch, u_mstride, rows, cols;
+  float* ss;      // matrix 0 of this launch, pitch ss_mstride
+  int64_t ss_mstride;
+};
+
+template <int UDT, int VEC, bool TRANS>
+__global__ __launch_bounds__(256) void row_sumsq_kernel(RowSsArgs a) {
+#pragma clang fp contract(off)
+  __shared__ float part[4][64];
+  const int mat = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t r0 = (int64_t)blockIdx.x * 64;
+  const int64_t base = (int64_t)mat * a.u_mstride;
+  float* ss = a.ss + (int64_t)mat * a.ss_mstride;
+  if constexpr (TRANS) {
+    const int64_t r = r0 + lane;
+    float s = 0.0f;
+    if (r < a.rows)
+      for (int64_t c = wave; c < a.cols; c += 4) {
+        const float v = Elem<UDT>::load(a.u, base + c * a.u_pitch + r);
+        s += v * v;
+      }
+    part[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && r < a.rows) ss[r] = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
+  } else {
+    for (int i = 0; i < 16; ++i) {
+      const int64_t r = r0 + wave * 16 + i;
+      if (r >= a.rows) break;
+      float s = 0.0f;
+      if constexpr (VEC == 8) {
+        for (int64_t c = (int64_t)lane * 8; c < a.cols; c += 512) {
+          float v[8];
+          Vec8<UDT>::load(a.u, base + r * a.u_pitch + c, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) s += v[e] * v[e];
+        }
+      } else {
+        for (int64_t c = lane; c < a.cols; c += 64) {
+          const float v = Elem<UDT>::load(a.u, base + r * a.u_pitch + c);
+          s += v * v;
+        }
+      }
+      s = warp_sum(s);
+      if (lane == 0) ss[r] = s;
+    }
+  }
+}
+
+// Per (row block, matrix): v' = lerp(v, ss / cols, w) into the variance state, row
+// multipliers d = 1 / (sqrt(v') + 1e-8), and the Frobenius rescale
+// f = ||U|| / max(||U d||, 1e-8) with ||U||^2 = sum ss and ||U d||^2 = sum ss d^2 (double,
+// fixed order); ss[r] is replaced by d_r * f.
+struct NormuonArgs {
+  float* ss;  // matrix 0 of this launch
+  int64_t ss_mstride;
+  void* vars[MUON_MAX_TENSORS];
+  int64_t nb, rows, cols;
+  int64_t split_start[MUON_MAX_SPLITS + 1];
+  float w;    // lerp weight 1 - beta2
+};
+
+MUON_DEVICE float torch_lerp(float a, float b, float w) {
+#pragma clang fp contract(off)
+  // at::lerp for floating types: a + w (b - a) for |w| < 0.5, else b - (b - a)(1 - w)
+  if (fabsf(w) < 0.5f) {
+    const float d = b - a;
+    return a + w * d;
+  }
+  const float d = b - a;
+  const float om = 1.0f - w;
+  return b - d * om;
+}
+
+template <int VDT>
+__global__ __launch_bounds__(256) void normuon_finalize_kernel(NormuonArgs a) {
+#pragma clang fp contract(off)
+  __shared__ double r1[256], r2[256];
+  __shared__ float fac;
+  const int mat = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x;
+  const int t = (int)(mat / a.nb);
+  const int64_t mb = mat % a.nb;
+  float* ss = a.ss + (int64_t)mat * a.ss_mstride;
+  void* vp = a.vars[t];
+  const int64_t rs = a.split_start[blk], re = a.split_start[blk + 1];
+  const float colsf = (float)a.cols;
+  double s1 = 0.0, s2 = 0.0;
+  for (int64_t r = rs + tid; r < re; r += 256) {
+    const float q = ss[r];
+    const float mean = q / colsf;
+    const int64_t vi = mb * a.rows + r;
+    const float vn = torch_lerp(Elem<VDT>::load(vp, vi), mean, a.w);
+    Elem<VDT>::store(vp, vi, vn);
+    const float den = sqrtf(vn) + 1e-8f;
+    const float d = 1.0f / den;
+    s1 += (double)q;
+    s2 += (double)q * (double)d * (double)d;
+    ss[r] = d;
+  }
+  r1[tid] = s1;
+  r2[tid] = s2;
+  __syncthreads();
+  for (int h = 128; h > 0; h >>= 1) {
+    if (tid < h) {
+      r1[tid] += r1[tid + h];
+      r2[tid] += r2[tid + h];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const float norm_u = sqrtf((float)r1[0]);
+    const float norm_new = fmaxf(sqrtf((float)r2[0]), 1e-8f);
+    fac = norm_u / norm_new;
+  }
+  __syncthreads();
+  const float f = fac;
+  for (int64_t r = rs + tid; r < re; r += 256) ss[r] = ss[r] * f;
 }
 
 // Copy the stored-layout result out of the workspace (with dtype conversion).
@@ -404,10 +542,17 @@ int launch_prepass_b(int bdt, int wdt, const PrepassArgs& a, dim3 grid, bool vec
 
 template <int PDT, int UDT, bool TRANS>
 void launch_post_t(const PostArgs& a, dim3 grid, bool vec8, hipStream_t s) {
-  if (vec8)
-    hipLaunchKernelGGL((postpass_kernel<PDT, UDT, 8, TRANS>), grid, dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL((postpass_kernel<PDT, UDT, 1, TRANS>), grid, dim3(256), 0, s, a);
+  if (a.rscale) {
+    if (vec8)
+      hipLaunchKernelGGL((postpass_kernel<PDT, UDT, 8, TRANS, true>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((postpass_kernel<PDT, UDT, 1, TRANS, true>), grid, dim3(256), 0, s, a);
+  } else {
+    if (vec8)
+      hipLaunchKernelGGL((postpass_kernel<PDT, UDT, 8, TRANS, false>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((postpass_kernel<PDT, UDT, 1, TRANS, false>), grid, dim3(256), 0, s, a);
+  }
 }
 
 // A transposed U comes from the workspace only (bf16 or fp32).
@@ -602,9 +747,11 @@ int muon_launch_scale(const OrthLayout& L, void* x, int wdt, int64_t batch, cons
 
 int muon_launch_postpass(int ntensors, void* const* params, const float* adj, int pdt,
                          const void* u, int udt, int64_t u_pitch, int64_t u_mstride, int u_trans,
-                         int64_t nb, int64_t rows, int64_t cols, float wd, int cautious,
-                         hipStream_t s) {
+                         const float* rscale, int64_t rs_mstride, int64_t nb, int64_t rows,
+                         int64_t cols, float wd, int cautious, hipStream_t s) {
   PostArgs a;
+  a.rscale = rscale;
+  a.rs_mstride = rs_mstride;
   for (int i = 0; i < ntensors; ++i) {
     a.params[i] = params[i];
     a.adj[i] = adj[i];
@@ -657,5 +804,70 @@ int muon_launch_extract(const void* src, int wdt, int64_t pitch, int64_t mstride
     return rc;
   }
   MUON_CHECK_LAUNCH("extract");
+  return MUON_OK;
+}
+
+// NorMuon row statistics and finalize for nmat matrices of rows x cols starting at u
+// (pitch / matrix stride in elements, transposed as the post-pass reads it), scratch ss
+// (pitch ss_mstride per matrix); splits: nsplits + 1 row offsets.
+int muon_launch_normuon_stats(int ntensors, void* const* vars, int vdt, const void* u, int udt,
+                              int64_t u_pitch, int64_t u_mstride, int u_trans, int64_t nb,
+                              int64_t rows, int64_t cols, float* ss, int64_t ss_mstride,
+                              const int64_t* split_start, int nsplits, float w, hipStream_t s) {
+  const int64_t nmat = (int64_t)ntensors * nb;
+  RowSsArgs ra;
+  ra.u = u;
+  ra.u_pitch = u_pitch;
+  ra.u_mstride = u_mstride;
+  ra.rows = rows;
+  ra.cols = cols;
+  ra.ss = ss;
+  ra.ss_mstride = ss_mstride;
+  dim3 grid((unsigned)((rows + 63) / 64), (unsigned)nmat);
+  const bool vec8 = !u_trans && (cols % 8) == 0 && (u_pitch % 8) == 0 && (u_mstride % 8) == 0 &&
+                    !((uintptr_t)u & 15);
+#define ROWSS(UDT_)                                                                        \
+  do {                                                                                     \
+    if (u_trans)                                                                           \
+      hipLaunchKernelGGL((row_sumsq_kernel<UDT_, 1, true>), grid, dim3(256), 0, s, ra);     \
+    else if (vec8)                                                                         \
+      hipLaunchKernelGGL((row_sumsq_kernel<UDT_, 8, false>), grid, dim3(256), 0, s, ra);    \
+    else                                                                                   \
+      hipLaunchKernelGGL((row_sumsq_kernel<UDT_, 1, false>), grid, dim3(256), 0, s, ra);    \
+  } while (0)
+  switch (udt) {
+    case MUON_DT_F32: ROWSS(MUON_DT_F32); break;
+    case MUON_DT_BF16: ROWSS(MUON_DT_BF16); break;
+    case MUON_DT_F16: ROWSS(MUON_DT_F16); break;
+    default:
+      muon_set_error("normuon: unsupported update dtype %d", udt);
+      return MUON_ERR_DTYPE;
+  }
+#undef ROWSS
+  NormuonArgs na;
+  na.ss = ss;
+  na.ss_mstride = ss_mstride;
+  for (int i = 0; i < ntensors; ++i) na.vars[i] = vars[i];
+  na.nb = nb;
+  na.rows = rows;
+  na.cols = cols;
+  for (int i = 0; i <= nsplits; ++i) na.split_start[i] = split_start[i];
+  na.w = w;
+  dim3 fgrid((unsigned)nsplits, (unsigned)nmat);
+  switch (vdt) {
+    case MUON_DT_F32:
+      hipLaunchKernelGGL((normuon_finalize_kernel<MUON_DT_F32>), fgrid, dim3(256), 0, s, na);
+      break;
+    case MUON_DT_BF16:
+      hipLaunchKernelGGL((normuon_finalize_kernel<MUON_DT_BF16>), fgrid, dim3(256), 0, s, na);
+      break;
+    case MUON_DT_F16:
+      hipLaunchKernelGGL((normuon_finalize_kernel<MUON_DT_F16>), fgrid, dim3(256), 0, s, na);
+      break;
+    default:
+      muon_set_error("normuon: unsupported variance dtype %d", vdt);
+      return MUON_ERR_DTYPE;
+  }
+  MUON_CHECK_LAUNCH("normuon_stats");
   return MUON_OK;
 }

@@ -56,6 +56,12 @@ _SIGNATURES = {
         [_c_int, _pp, _c_int, _vp, _c_int, _vp, _c_int, _c_i64, _c_int, _c_i64, _c_i64, _c_i64,
          ctypes.POINTER(_c_f32), _c_f32, _c_int, _vp],
     ),
+    "muon_normuon_postpass": (
+        _c_int,
+        [_c_int, _pp, _c_int, _pp, _c_int, _vp, _c_int, _vp, _c_int, _c_i64, _c_int, _c_i64,
+         _c_i64, _c_i64, ctypes.POINTER(_c_i64), _c_int, ctypes.POINTER(_c_f32), _c_f32, _c_int,
+         ctypes.c_double, _vp],
+    ),
     "muon_lp_quantize": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp]),
     "muon_lp_dequantize": (_c_int, [_vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _vp]),
     "muon_timing_enable": (_c_int, [_c_int]),
@@ -168,6 +174,13 @@ def ptr_array(tensors: Sequence[torch.Tensor | None]):
 
 def f32_array(values: Sequence[float]):
     arr = (ctypes.c_float * max(len(values), 1))()
+    for i, v in enumerate(values):
+        arr[i] = v
+    return arr
+
+
+def i64_array(values: Sequence[int]):
+    arr = (ctypes.c_int64 * max(len(values), 1))()
     for i, v in enumerate(values):
         arr[i] = v
     return arr

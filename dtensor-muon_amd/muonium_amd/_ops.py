@@ -271,6 +271,94 @@ def fused_step(
     )
 
 
+def _splits(split_sizes):
+    if split_sizes is None:
+        return None, 0
+    return _lib.i64_array(list(split_sizes)), len(split_sizes)
+
+
+def fused_normuon_step(
+    params: Sequence[Tensor],
+    grads: Sequence[Tensor],
+    bufs: Sequence[Tensor],
+    variances: Sequence[Tensor],
+    lrs: Sequence[float],
+    *,
+    momentum: float,
+    nesterov: bool,
+    maximize: bool,
+    write_back_grad: bool,
+    weight_decay: float,
+    cautious_wd: bool,
+    coeffs: Sequence[tuple[float, float, float]],
+    prescale: float,
+    beta2: float,
+    eps: float = 1e-7,
+) -> None:
+    """fused_step for the "normuon" algorithm: the post-pass normalizes U per stored row
+    (second-moment EMA into ``variances``, Frobenius rescale) before the apply."""
+    lib = _lib.load()
+    g0 = grads[0]
+    device = g0.device
+    _lib.ensure_device(device)
+    _check_cuda_contig(list(params) + list(grads) + list(bufs) + list(variances),
+                       "NorMuon step tensors")
+    nb, rows, cols = matrix_view(g0)
+    count = len(grads)
+    ws, cap = workspace(device, torch.bfloat16, count * nb, rows, cols)
+    s = _lib.stream(device)
+    steps = len(coeffs)
+    _lib.check(
+        lib.muon_prepass(count, _lib.ptr_array(grads), _lib.ptr_array(bufs),
+                         _lib.dtype_code(g0.dtype), _lib.dtype_code(bufs[0].dtype), nb, rows, cols,
+                         momentum, int(nesterov), int(maximize), int(write_back_grad),
+                         ws.data_ptr(), _lib.DT_BF16, cap, s),
+        "muon_prepass",
+    )
+    _lib.check(
+        lib.muon_orth_run(ws.data_ptr(), _lib.DT_BF16, cap, count * nb, rows, cols,
+                          _flat_coeffs(coeffs), steps, prescale, eps, s),
+        "muon_orth_run",
+    )
+    _lib.check(
+        lib.muon_normuon_postpass(
+            count, _lib.ptr_array(params), _lib.dtype_code(params[0].dtype),
+            _lib.ptr_array(variances), _lib.dtype_code(variances[0].dtype), None, 0,
+            ws.data_ptr(), _lib.DT_BF16, cap, steps, nb, rows, cols, None, 0,
+            _lib.f32_array(lrs), float(weight_decay), int(cautious_wd), float(beta2), s,
+        ),
+        "muon_normuon_postpass",
+    )
+
+
+def normuon_postpass(
+    params: Sequence[Tensor], us: Sequence[Tensor], variances: Sequence[Tensor],
+    lrs: Sequence[float], *, weight_decay: float, cautious_wd: bool, beta2: float,
+    split_sizes=None, shape=None,
+) -> None:
+    """NorMuon's normalization and apply for explicit updates ``us`` (one tensor per
+    param, the elements in the param's order), per row block with ``split_sizes``."""
+    lib = _lib.load()
+    p0 = params[0]
+    _lib.ensure_device(p0.device)
+    _check_cuda_contig(list(params) + list(variances), "NorMuon tensors")
+    nb, rows, cols = matrix_view(p0 if shape is None else shape)
+    ws, cap = workspace(p0.device, torch.bfloat16, nb, rows, cols)
+    sp, nsp = _splits(split_sizes)
+    s = _lib.stream(p0.device)
+    for p, u, v, lr in zip(params, us, variances, lrs):
+        u = u.contiguous()
+        _lib.check(
+            lib.muon_normuon_postpass(
+                1, _lib.ptr_array([p]), _lib.dtype_code(p.dtype), _lib.ptr_array([v]),
+                _lib.dtype_code(v.dtype), u.data_ptr(), _lib.dtype_code(u.dtype), ws.data_ptr(),
+                _lib.DT_BF16, cap, 0, nb, rows, cols, sp, nsp, _lib.f32_array([lr]),
+                float(weight_decay), int(cautious_wd), float(beta2), s,
+            ),
+            "muon_normuon_postpass",
+        )
+
+
 def fused_lp_step(
     params: Sequence[Tensor],
     grads: Sequence[Tensor],

@@ -1,9 +1,9 @@
 """NorMuon: Muon with neuron-wise update normalization (arXiv:2510.05491).
 
-Mirrors muonium/optim/algorithms/normuon.py:16-203. Momentum, orthogonalization and
-the weight-decay/apply pass run on the MI355X kernels; the per-row normalization of
-the orthogonalized update (a handful of row/matrix reductions) is expressed with torch
-device ops for now.
+Mirrors muonium/optim/algorithms/normuon.py:16-203. Momentum, orthogonalization, the
+per-row normalization of the orthogonalized update and the weight-decay/apply pass all
+run on the MI355X kernels (``muon_normuon_postpass``). ``_normuon_normalize`` keeps the
+reference's torch formulation for callers that normalize a tensor by hand.
 """
 
 from __future__ import annotations
@@ -21,7 +21,7 @@ from .base import (
     orthogonalize_single,
     register_muon_algorithm,
 )
-from .muon import _Contig, momentum_seam, schedule
+from .muon import _Contig, fused_orth_available, is_quantized, momentum_seam, schedule
 
 
 def _normuon_normalize(
@@ -50,28 +50,37 @@ def _normuon_step(params, grads, bufs, variances, lr_ratios, *, lr, weight_decay
                   momentum, nesterov, maximize, ns_steps, orthogonalization_strategy,
                   split_sizes, muon_beta2, batched):
     lrs = _ops.adjusted_lrs(lr_ratios, lr)
-    schedule(orthogonalization_strategy, ns_steps)
-    P, G, B = _Contig(params), _Contig(grads), _Contig(bufs)
-    gq = momentum_seam(G.work, B.work, momentum=momentum, nesterov=nesterov,
-                       maximize=maximize, batched=batched)
-    if batched:
-        us = orthogonalize_batch(gq, ns_steps=ns_steps, strategy=orthogonalization_strategy,
-                                 split_sizes=split_sizes)
-    else:
-        us = [orthogonalize_single(gq[0], ns_steps=ns_steps, strategy=orthogonalization_strategy,
-                                   split_sizes=split_sizes)]
-    normalized = []
-    for u, v in zip(us, variances, strict=True):
-        un, v_new = _normuon_normalize(u, v.to(torch.float32), muon_beta2, split_sizes)
-        v.copy_(v_new)
-        normalized.append(un.contiguous())
+    coeffs, prescale = schedule(orthogonalization_strategy, ns_steps)
+    quantized = is_quantized(bufs[0])
+    P, G, V = _Contig(params), _Contig(grads), _Contig(variances)
+    B = None if quantized else _Contig(bufs)
     pview = [p.view(g.shape) for p, g in zip(P.work, G.work)]
-    _ops.postpass(pview, normalized, lrs, weight_decay=weight_decay, cautious_wd=cautious_wd,
-                  shape=G.work[0].shape)
+    if not quantized and fused_orth_available(split_sizes, batched):
+        _ops.fused_normuon_step(
+            pview, G.work, B.work, V.work, lrs, momentum=momentum, nesterov=nesterov,
+            maximize=maximize, write_back_grad=batched and nesterov and not maximize,
+            weight_decay=weight_decay, cautious_wd=cautious_wd, coeffs=coeffs,
+            prescale=prescale, beta2=muon_beta2,
+        )
+    else:
+        gq = momentum_seam(G.work, bufs if quantized else B.work, momentum=momentum,
+                           nesterov=nesterov, maximize=maximize, batched=batched)
+        if batched:
+            us = orthogonalize_batch(gq, ns_steps=ns_steps, strategy=orthogonalization_strategy,
+                                     split_sizes=split_sizes)
+        else:
+            us = [orthogonalize_single(gq[0], ns_steps=ns_steps,
+                                       strategy=orthogonalization_strategy,
+                                       split_sizes=split_sizes)]
+        _ops.normuon_postpass(pview, [u.reshape(g.shape) for u, g in zip(us, G.work)], V.work,
+                              lrs, weight_decay=weight_decay, cautious_wd=cautious_wd,
+                              beta2=muon_beta2, split_sizes=split_sizes, shape=G.work[0].shape)
     P.writeback()
     if batched and nesterov and not maximize:
         G.writeback()
-    B.writeback()
+    if B is not None:
+        B.writeback()
+    V.writeback()
 
 
 @register_muon_algorithm

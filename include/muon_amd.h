@@ -135,6 +135,29 @@ int muon_postpass(int ntensors, void* const* params, int p_dtype, const void* u,
                   int64_t rows, int64_t cols, const float* adjusted_lrs, float wd,
                   int cautious, void* stream);
 
+/* ---- NorMuon post-pass ------------------------------------------------------------
+ * muon_postpass for the "normuon" algorithm: the update U (from the workspace when
+ * u == NULL, else the contiguous tensor u of u_dtype, as in muon_postpass) is first
+ * normalized per stored row (normuon.py:16-55), per row block when split_sizes is given
+ * (nsplits blocks of stored rows summing to `rows`, at most MUON_MAX_SPLITS):
+ *   r_i   = mean_j U(i, j)^2                          (fp32)
+ *   v_i'  = lerp(v_i, r_i, 1 - beta2)                 (torch.lerp; v = variances[t], one
+ *                                                      value per stored row, v_dtype)
+ *   U'    = U(i, :) / (sqrt(v_i') + 1e-8)
+ *   U''   = U' * ||U||_F / max(||U'||_F, 1e-8)        (norms per matrix and row block)
+ * and v_i' is stored into the variance state; then cautious weight decay and the apply
+ * run on U'' in fp32 exactly as muon_postpass. The workspace (same quadruple as the other
+ * calls; required also with an explicit u) holds the per-row scratch.
+ * Replaces: muonium/optim/algorithms/normuon.py:16-55 (_normuon_normalize), :118-134
+ * (NorMuon.update after the orthogonalization) and :182-203 (foreach_update). */
+#define MUON_MAX_SPLITS 16
+int muon_normuon_postpass(int ntensors, void* const* params, int p_dtype,
+                          void* const* variances, int v_dtype, const void* u, int u_dtype,
+                          void* ws, int ws_dtype, int64_t ws_batch, int steps, int64_t nb,
+                          int64_t rows, int64_t cols, const int64_t* split_sizes, int nsplits,
+                          const float* adjusted_lrs, float wd, int cautious, double beta2,
+                          void* stream);
+
 /* ---- Quantized momentum (MuonLP) -------------------------------------------------
  * State of one tensor of `numel` values: codes (uint8; numel bytes for 8-bit and
  * fp8, numel/2 for 4-bit with element 2i in the high nibble) and one fp32 scale per

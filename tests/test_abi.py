@@ -43,8 +43,9 @@ def test_workspace_size_formula():
     a = 2 * 256 * 256 * 2
     parts = 2 * (256 // 64) * (512 // 64) * 4
     # two ping-pong copies of the wide iterate, A, B, norm partials, per-matrix scale,
-    # the quantized-state search tables (16 KB bucket table + 260 thresholds, padded)
-    assert nbytes == 2 * x + 2 * a + parts + 256 + 16384 + 1280
+    # the quantized-state search tables (16 KB bucket table + 260 thresholds, padded), and
+    # one fp32 per stored row (n_pad) per matrix for NorMuon's row statistics
+    assert nbytes == 2 * x + 2 * a + parts + 256 + 16384 + 1280 + 2 * 512 * 4
     assert lib.muon_orth_workspace_bytes(_lib.DT_BF16, 1, 300, 130) < nbytes
     assert lib.muon_orth_workspace_bytes(7, 1, 4, 4) == -1
     assert lib.muon_orth_workspace_bytes(_lib.DT_F32, 1, 0, 4) == -1
