@@ -32,8 +32,9 @@ int muon_launch_scale(const OrthLayout& L, void* x, int wdt, int64_t batch, cons
                       hipStream_t s);
 int muon_launch_postpass(int ntensors, void* const* params, const float* adj, int pdt,
                          const void* u, int udt, int64_t u_pitch, int64_t u_mstride, int u_trans,
-                         const float* rscale, int64_t rs_mstride, int64_t nb, int64_t rows,
-                         int64_t cols, float wd, int cautious, hipStream_t s);
+                         const float* rscale, int64_t rs_mstride, const float* uscale,
+                         int64_t nb, int64_t rows, int64_t cols, float wd, int cautious,
+                         hipStream_t s);
 int muon_launch_normuon_stats(int ntensors, void* const* vars, int vdt, const void* u, int udt,
                               int64_t u_pitch, int64_t u_mstride, int u_trans, int64_t nb,
                               int64_t rows, int64_t cols, float* ss, int64_t ss_mstride,
@@ -161,7 +162,7 @@ static bool io_dtype_ok(int dt) {
 
 extern "C" {
 
-int muon_amd_abi_version(void) { return 2; }
+int muon_amd_abi_version(void) { return 3; }
 
 const char* muon_amd_last_error(void) { return g_err; }
 
@@ -365,8 +366,8 @@ int muon_orth_extract(const void* ws, int ws_dtype, int64_t ws_batch, int64_t ba
 
 int muon_postpass(int ntensors, void* const* params, int p_dtype, const void* u, int u_dtype,
                   const void* ws, int ws_dtype, int64_t ws_batch, int steps, int64_t nb,
-                  int64_t rows, int64_t cols, const float* adjusted_lrs, float wd,
-                  int cautious, void* stream) {
+                  int64_t rows, int64_t cols, const float* adjusted_lrs, const float* u_scales,
+                  float wd, int cautious, void* stream) {
   if (!io_dtype_ok(p_dtype)) {
     muon_set_error("postpass: unsupported param dtype %d", p_dtype);
     return MUON_ERR_DTYPE;
@@ -406,7 +407,8 @@ int muon_postpass(int ntensors, void* const* params, int p_dtype, const void* u,
     const int cnt = std::min(MUON_MAX_TENSORS, ntensors - t0);
     int rc = muon_launch_postpass(cnt, params + t0, adjusted_lrs + t0, p_dtype,
                                   ubase + (int64_t)t0 * nb * mst * es, udt, pitch, mst, trans,
-                                  nullptr, 0, nb, rows, cols, wd, cautious, s);
+                                  nullptr, 0, u_scales ? u_scales + t0 : nullptr, nb, rows, cols,
+                                  wd, cautious, s);
     if (rc != MUON_OK) return rc;
   }
   return MUON_OK;
@@ -496,7 +498,7 @@ int muon_normuon_postpass(int ntensors, void* const* params, int p_dtype,
                                        nb, rows, cols, ssc, ss_mst, starts, nb_split, w, s);
     if (rc != MUON_OK) return rc;
     rc = muon_launch_postpass(cnt, params + t0, adjusted_lrs + t0, p_dtype, uc, udt, pitch, mst,
-                              trans, ssc, ss_mst, nb, rows, cols, wd, cautious, s);
+                              trans, ssc, ss_mst, nullptr, nb, rows, cols, wd, cautious, s);
     if (rc != MUON_OK) return rc;
   }
   return MUON_OK;

@@ -246,6 +246,8 @@ struct PostArgs {
   int64_t u_pitch, u_mstride;
   const float* rscale;  // (ROWSCALE) per stored row multiplier, matrix 0 of this launch
   int64_t rs_mstride;
+  float uscale[MUON_MAX_TENSORS];  // per tensor: u <- round_UDT(u * uscale) when has_uscale
+  int has_uscale;
   int64_t nb, rows, cols;
   int tiles_c;
   float wd;
@@ -328,6 +330,10 @@ __global__ __launch_bounds__(256) void postpass_kernel(PostArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) u[e] = u[e] * rs;
       }
+      if (a.has_uscale) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) u[e] = Elem<UDT>::round(u[e] * a.uscale[t]);
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         o[e] = apply_elem<PDT, ROWSCALE ? MUON_DT_F32 : UDT>(p[e], u[e], a.wd, a.cautious, adj);
@@ -342,6 +348,7 @@ __global__ __launch_bounds__(256) void postpass_kernel(PostArgs a) {
         const float p = Elem<PDT>::load(pp, pi);
         float u = TRANS ? ut[r - r0][cl + e] : Elem<UDT>::load(a.u, ui);
         if (ROWSCALE) u = u * a.rscale[(int64_t)mat * a.rs_mstride + r];
+        if (a.has_uscale) u = Elem<UDT>::round(u * a.uscale[t]);
         Elem<PDT>::store(pp, pi,
                          apply_elem<PDT, ROWSCALE ? MUON_DT_F32 : UDT>(p, u, a.wd, a.cautious, adj));
       }
@@ -747,11 +754,14 @@ int muon_launch_scale(const OrthLayout& L, void* x, int wdt, int64_t batch, cons
 
 int muon_launch_postpass(int ntensors, void* const* params, const float* adj, int pdt,
                          const void* u, int udt, int64_t u_pitch, int64_t u_mstride, int u_trans,
-                         const float* rscale, int64_t rs_mstride, int64_t nb, int64_t rows,
-                         int64_t cols, float wd, int cautious, hipStream_t s) {
+                         const float* rscale, int64_t rs_mstride, const float* uscale,
+                         int64_t nb, int64_t rows, int64_t cols, float wd, int cautious,
+                         hipStream_t s) {
   PostArgs a;
   a.rscale = rscale;
   a.rs_mstride = rs_mstride;
+  a.has_uscale = uscale != nullptr;
+  for (int i = 0; i < ntensors; ++i) a.uscale[i] = uscale ? uscale[i] : 1.0f;
   for (int i = 0; i < ntensors; ++i) {
     a.params[i] = params[i];
     a.adj[i] = adj[i];

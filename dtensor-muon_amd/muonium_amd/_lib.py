@@ -54,7 +54,7 @@ _SIGNATURES = {
     "muon_postpass": (
         _c_int,
         [_c_int, _pp, _c_int, _vp, _c_int, _vp, _c_int, _c_i64, _c_int, _c_i64, _c_i64, _c_i64,
-         ctypes.POINTER(_c_f32), _c_f32, _c_int, _vp],
+         ctypes.POINTER(_c_f32), ctypes.POINTER(_c_f32), _c_f32, _c_int, _vp],
     ),
     "muon_normuon_postpass": (
         _c_int,

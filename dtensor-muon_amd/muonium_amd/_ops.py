@@ -216,7 +216,7 @@ def postpass(
         _lib.check(
             lib.muon_postpass(len(ps), _lib.ptr_array(ps), _lib.dtype_code(p0.dtype),
                               u.data_ptr(), _lib.dtype_code(u.dtype), None, 1, 0, 0, nb, rows,
-                              cols, _lib.f32_array([lrs[i] for i in idx]),
+                              cols, _lib.f32_array([lrs[i] for i in idx]), None,
                               float(weight_decay), int(cautious_wd), s),
             "muon_postpass",
         )
@@ -237,10 +237,12 @@ def fused_step(
     coeffs: Sequence[tuple[float, float, float]],
     prescale: float,
     eps: float = 1e-7,
+    u_scales: Sequence[float] | None = None,
 ) -> None:
     """One Muon step over a same-shape bucket: momentum pre-pass into the batched bf16
     workspace, the iteration, and the weight-decay/apply post-pass reading the
-    result straight from the workspace."""
+    result straight from the workspace. ``u_scales`` (one per tensor) rescales each
+    update first, rounded to bf16: the split_sizes row-block correction."""
     lib = _lib.load()
     g0 = grads[0]
     device = g0.device
@@ -266,7 +268,9 @@ def fused_step(
     _lib.check(
         lib.muon_postpass(count, _lib.ptr_array(params), _lib.dtype_code(params[0].dtype), None,
                           0, ws.data_ptr(), _lib.DT_BF16, cap, steps, nb, rows, cols,
-                          _lib.f32_array(lrs), float(weight_decay), int(cautious_wd), s),
+                          _lib.f32_array(lrs),
+                          None if u_scales is None else _lib.f32_array(u_scales),
+                          float(weight_decay), int(cautious_wd), s),
         "muon_postpass",
     )
 
@@ -404,7 +408,7 @@ def fused_lp_step(
     _lib.check(
         lib.muon_postpass(count, _lib.ptr_array(params), _lib.dtype_code(params[0].dtype), None,
                           0, ws.data_ptr(), _lib.DT_BF16, cap, steps, nb, rows, cols,
-                          _lib.f32_array(lrs), float(weight_decay), int(cautious_wd), s),
+                          _lib.f32_array(lrs), None, float(weight_decay), int(cautious_wd), s),
         "muon_postpass",
     )
 

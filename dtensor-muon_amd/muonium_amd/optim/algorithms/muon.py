@@ -24,7 +24,13 @@ from muonium_amd import _ops
 from muonium_amd.orthogonalize import OrthogonalizationStrategy
 
 from . import base as _base
-from .base import MuonAlgorithm, orthogonalize_batch, orthogonalize_single, register_muon_algorithm
+from .base import (
+    MuonAlgorithm,
+    orthogonalize_batch,
+    orthogonalize_single,
+    register_muon_algorithm,
+    split_lr_scales,
+)
 
 
 def fused_orth_available(split_sizes, batched: bool) -> bool:
@@ -96,7 +102,15 @@ def muon_step(
     G = _Contig(grads)
     B = None if quantized else _Contig(bufs)
     pview = [p.view(g.shape) for p, g in zip(P.work, G.work)]
-    if fused_orth_available(split_sizes, batched):
+    if split_sizes is not None and not quantized and G.work[0].dim() == 2 and \
+            fused_orth_available(None, batched):
+        _fused_split_step(
+            pview, G.work, B.work, lrs, split_sizes, momentum=momentum, nesterov=nesterov,
+            maximize=maximize, write_back_grad=batched and nesterov and not maximize,
+            weight_decay=weight_decay, cautious_wd=cautious_wd, coeffs=coeffs,
+            prescale=prescale,
+        )
+    elif fused_orth_available(split_sizes, batched):
         if quantized:
             _ops.fused_lp_step(
                 pview, G.work, bufs, lrs, momentum=momentum, nesterov=nesterov,
@@ -127,6 +141,33 @@ def muon_step(
         G.writeback()
     if B is not None:
         B.writeback()
+
+
+def _fused_split_step(params, grads, bufs, lrs, split_sizes, **kw) -> None:
+    """The fused step for 2D tensors split into row blocks (base.py:56-99): every block is a
+    contiguous row slice, i.e. a matrix of its own, so equal-height blocks of all tensors run
+    through one prepass / iteration / post-pass sequence, each block's update rescaled by
+    its split_lr_scales entry (rounded to the update's bf16, as `u * scales[i]` is)."""
+    rows, cols = grads[0].shape
+    scales = split_lr_scales((rows, cols), tuple(split_sizes))
+    offsets, acc = [], 0
+    for h in split_sizes:
+        offsets.append(acc)
+        acc += h
+    by_height: dict[int, list[int]] = {}
+    for j, h in enumerate(split_sizes):
+        by_height.setdefault(h, []).append(j)
+    for h, blocks in by_height.items():
+        ps, gs, bs, block_lrs, block_scales = [], [], [], [], []
+        for p, g, b, lr in zip(params, grads, bufs, lrs):
+            for j in blocks:
+                o = offsets[j]
+                ps.append(p[o:o + h])
+                gs.append(g[o:o + h])
+                bs.append(b[o:o + h])
+                block_lrs.append(lr)
+                block_scales.append(scales[j])
+        _ops.fused_step(ps, gs, bs, block_lrs, u_scales=block_scales, **kw)
 
 
 def _offloaded(fn, params, grads, *state_lists, **kw):

@@ -128,12 +128,14 @@ int muon_orth_extract(const void* ws, int ws_dtype, int64_t ws_batch, int64_t ba
  *   p = round(p - adjusted_lrs[t] * v)                                 (muon.py:71-77)
  * in fp32 with no contraction; when wd == 0 the product adjusted_lr*u keeps u's dtype
  * (eager type promotion of a 0-dim fp32 tensor times a bf16 tensor: adjusted_lr is cast
- * to u's dtype, the product rounded to it).
+ * to u's dtype, the product rounded to it). With u_scales (one per tensor, NULL for none)
+ * u is first replaced by u * u_scales[t] rounded to u's dtype: the split_sizes row-block
+ * rescale `u * scales[i]` of base.py:98 applied to a block handed over as its own tensor.
  * Replaces: muonium/optim/algorithms/muon.py:59-77 and :121-140. */
 int muon_postpass(int ntensors, void* const* params, int p_dtype, const void* u, int u_dtype,
                   const void* ws, int ws_dtype, int64_t ws_batch, int steps, int64_t nb,
-                  int64_t rows, int64_t cols, const float* adjusted_lrs, float wd,
-                  int cautious, void* stream);
+                  int64_t rows, int64_t cols, const float* adjusted_lrs, const float* u_scales,
+                  float wd, int cautious, void* stream);
 
 /* ---- NorMuon post-pass ------------------------------------------------------------
  * muon_postpass for the "normuon" algorithm: the update U (from the workspace when

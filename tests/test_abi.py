@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_text():
     lib = _lib.load()
-    assert lib.muon_amd_abi_version() == 2
+    assert lib.muon_amd_abi_version() == 3
     assert isinstance(_lib.last_error(), str)
 
 
@@ -76,7 +76,7 @@ def test_result_location_follows_orientation():
         (lambda L: L.muon_prepass(1, None, None, 1, 0, 1, 4, 4, 0.9, 1, 0, 0, None, 1, 1, None), 5),
         (lambda L: L.muon_orth_run(None, 1, 1, 2, 4, 4, None, 1, 1.0, 1e-7, None), 5),
         (lambda L: L.muon_orth_run(None, 5, 1, 1, 4, 4, None, 1, 1.0, 1e-7, None), 2),
-        (lambda L: L.muon_postpass(1, None, 9, None, 1, None, 1, 1, 1, 1, 4, 4, None, 0.0, 0, None), 2),
+        (lambda L: L.muon_postpass(1, None, 9, None, 1, None, 1, 1, 1, 1, 4, 4, None, None, 0.0, 0, None), 2),
         (lambda L: L.muon_lp_quantize(None, None, None, None, 3, 256, 256, None), 5),
         (lambda L: L.muon_lp_quantize(None, None, None, None, 8, 300, 256, None), 1),
         (lambda L: L.muon_lp_dequantize(None, None, None, 4, 254, 127, None, None), 1),

@@ -391,3 +391,44 @@ def test_split_sizes_match_oracle():
         split_sizes=(64, 16, 16), orth_batch=hip_batch,
     )
     assert torch.equal(p.detach().cpu(), ref_p)
+
+
+@pytest.mark.parametrize("foreach", [True, False])
+@pytest.mark.parametrize(
+    "shape,split,dtype,hp",
+    [((300, 128), (128, 172), torch.float32, (0.9, True, 0.1, True)),
+     ((192, 96), (96, 64, 32), torch.bfloat16, (0.95, True, 0.1, True)),
+     ((64, 256), (16, 48), torch.float32, (0.9, False, 0.0, False)),
+     ((160, 64), (32, 64, 32, 32), torch.bfloat16, (0.5, True, 0.05, False))],
+    ids=["tall-block", "qkv-bf16", "wide-blocks-nowd", "repeat-heights-bf16"],
+)
+def test_split_sizes_fused_blocks_exact(shape, split, dtype, hp, foreach):
+    """split_sizes row blocks through the fused kernels (equal heights batched, per-block
+    rescale) equal the oracle's base.py:73-99 split/scale/cat plus muon.py update exactly,
+    given the HIP orthogonalizer per block height, over two steps and two params."""
+    from muonium_amd.orthogonalize import foreach_zeropower
+
+    mom, nesterov, wd, cautious = hp
+    gen = torch.Generator().manual_seed(21)
+    p0 = [torch.randn(shape, generator=gen).to(dtype) for _ in range(2)]
+    params = [nn.Parameter(p.clone().to(DEV)) for p in p0]
+    opt = Muon([{"params": params, "split_sizes": split}], lr=0.05, wd=wd, momentum=mom,
+               nesterov=nesterov, use_cautious_wd=cautious, foreach=foreach)
+    hip_batch = lambda blocks: [u.cpu() for u in foreach_zeropower([b.to(DEV) for b in blocks],
+                                                                  strategy="polar_express")]
+    ref_p = [p.clone() for p in p0]
+    ref_buf = [torch.zeros(shape) for _ in p0]
+    for _ in range(2):
+        gs = [torch.randn(shape, generator=gen).to(dtype) for _ in p0]
+        for p, g in zip(params, gs):
+            p.grad = g.clone().to(DEV)
+        opt.step()
+        for i, g in enumerate(gs):
+            ref_p[i], ref_buf[i], _, _ = muon_ref.muon_update(
+                ref_p[i], g, ref_buf[i], muon_ref.lr_ratio(shape), lr=0.05, weight_decay=wd,
+                cautious_wd=cautious, momentum=mom, nesterov=nesterov, maximize=False,
+                split_sizes=split, orth_batch=hip_batch,
+            )
+    for p, rp, rb in zip(params, ref_p, ref_buf):
+        assert torch.equal(p.detach().cpu(), rp)
+        assert torch.equal(opt.state[p]["momentum_buffer"].cpu(), rb)
