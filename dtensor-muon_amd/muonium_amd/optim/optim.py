@@ -24,6 +24,7 @@ from torch.optim.optimizer import (
 
 from muonium_amd.orthogonalize import OrthogonalizationStrategy
 from muonium_amd.utils import group_tensors_by_shape, move_tensors_to_device
+from muonium_amd.utils.offload import pipeline_supported, run_offloaded
 
 from .algorithms import BufferSpec, MuonAlgorithm, get_algorithm
 from .algorithms.base import ADAM_ALGORITHMS
@@ -402,6 +403,24 @@ class Muon(torch.optim.Optimizer):
                 batches = [idx[i : i + self.batch_size] for i in range(0, len(idx), self.batch_size)]
             else:
                 batches = [idx]
+            if device.type != "cuda":
+                host = [
+                    ([dev_p[i] for i in sel], [dev_g[i] for i in sel],
+                     {k: [v[i] for i in sel] for k, v in dev_state.items()},
+                     [dev_lr[i] for i in sel])
+                    for sel in batches
+                ]
+                if torch.cuda.is_available() and all(pipeline_supported(b) for b in host):
+                    # pinned-memory round trip, copies overlapped with the updates
+                    run_offloaded(
+                        host,
+                        lambda p, g, st, lr: algorithm.foreach_update(p, g, st, lr, **hp),
+                        # the built-in algorithms rewrite the grads only under Nesterov
+                        # without maximize (muon.py:117-118); copy them back for any other
+                        grads_modified=(nesterov and not maximize)
+                        or not type(algorithm).__module__.startswith("muonium_amd."),
+                    )
+                    continue
             for sel in batches:
                 p_orig = [dev_p[i] for i in sel]
                 g_orig = [dev_g[i] for i in sel]

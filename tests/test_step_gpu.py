@@ -432,3 +432,38 @@ def test_split_sizes_fused_blocks_exact(shape, split, dtype, hp, foreach):
     for p, rp, rb in zip(params, ref_p, ref_buf):
         assert torch.equal(p.detach().cpu(), rp)
         assert torch.equal(opt.state[p]["momentum_buffer"].cpu(), rb)
+
+
+@pytest.mark.parametrize(
+    "algo,nesterov,maximize,dtype",
+    [("muon", True, False, torch.float32), ("muon", True, True, torch.bfloat16),
+     ("muon", False, False, torch.float32), ("normuon", True, False, torch.float32)],
+)
+def test_offloaded_batches_pipeline_matches_device_run(algo, nesterov, maximize, dtype):
+    """Host-resident params, foreach with batch_size=2 (three batches, two shapes): the
+    pinned-memory pipelined round trip gives exactly the device-resident run's params,
+    grads and state, and leaves every tensor on the host."""
+    gen = torch.Generator().manual_seed(31)
+    shapes = [(64, 48)] * 3 + [(32, 96)] * 2
+    init = [torch.randn(s, generator=gen).to(dtype) for s in shapes]
+    host = [nn.Parameter(t.clone()) for t in init]
+    dev = [nn.Parameter(t.clone().to(DEV)) for t in init]
+    kw = dict(lr=0.05, wd=0.1, momentum=0.9, nesterov=nesterov, maximize=maximize,
+              foreach=True, batch_size=2)
+    opt_h = Muon([{"params": host, "algorithm": algo}], **kw)
+    opt_d = Muon([{"params": dev, "algorithm": algo}], **kw)
+    for _ in range(2):
+        gs = [torch.randn(s, generator=gen).to(dtype) for s in shapes]
+        for h, d, g in zip(host, dev, gs):
+            h.grad = g.clone()
+            d.grad = g.clone().to(DEV)
+        opt_h.step()
+        opt_d.step()
+    torch.cuda.synchronize()
+    for h, d in zip(host, dev):
+        assert h.device.type == "cpu" and h.grad.device.type == "cpu"
+        assert torch.equal(h.detach(), d.detach().cpu())
+        assert torch.equal(h.grad, d.grad.cpu())
+        for key, val in opt_d.state[d].items():
+            assert opt_h.state[h][key].device.type == "cpu"
+            assert torch.equal(opt_h.state[h][key], val.cpu()), key
