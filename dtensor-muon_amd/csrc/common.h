@@ -123,6 +123,73 @@ struct Vec8<MUON_DT_F16> {
   }
 };
 
+// Non-temporal 16-byte global access (streamed data that no kernel re-reads soon: the
+// elementwise passes move every byte once).
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_nt;
+MUON_DEVICE uint4 ld_nt(const void* p) {
+  const u32x4_nt v = __builtin_nontemporal_load((const u32x4_nt*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+MUON_DEVICE void st_nt(void* p, uint4 w) {
+  const u32x4_nt v = {w.x, w.y, w.z, w.w};
+  __builtin_nontemporal_store(v, (u32x4_nt*)p);
+}
+
+// Eight consecutive elements kept as raw bits (16 B for 2-byte types, 32 B for fp32),
+// loaded and stored non-temporally; unpack()/pack() convert as Vec8 does.
+template <int DT>
+struct Raw8 {
+  static constexpr int N = DT == MUON_DT_F32 ? 2 : 1;
+  uint4 w[N];
+  MUON_DEVICE void load(const void* p, int64_t i) {
+    const char* b = (const char*)p + i * (DT == MUON_DT_F32 ? 4 : 2);
+#pragma unroll
+    for (int k = 0; k < N; ++k) w[k] = ld_nt(b + 16 * k);
+  }
+  MUON_DEVICE void store(void* p, int64_t i) const {
+    char* b = (char*)p + i * (DT == MUON_DT_F32 ? 4 : 2);
+#pragma unroll
+    for (int k = 0; k < N; ++k) st_nt(b + 16 * k, w[k]);
+  }
+  MUON_DEVICE void unpack(float (&v)[8]) const {
+    if constexpr (DT == MUON_DT_F32) {
+      const uint32_t u[8] = {w[0].x, w[0].y, w[0].z, w[0].w, w[1].x, w[1].y, w[1].z, w[1].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = __uint_as_float(u[e]);
+    } else {
+      const uint32_t u[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if constexpr (DT == MUON_DT_BF16) {
+          v[2 * k] = bf16_to_f32((bf16_t)(u[k] & 0xffffu));
+          v[2 * k + 1] = bf16_to_f32((bf16_t)(u[k] >> 16));
+        } else {
+          v[2 * k] = f16_to_f32((uint16_t)(u[k] & 0xffffu));
+          v[2 * k + 1] = f16_to_f32((uint16_t)(u[k] >> 16));
+        }
+      }
+    }
+  }
+  MUON_DEVICE void pack(const float (&v)[8]) {
+    if constexpr (DT == MUON_DT_F32) {
+      w[0] = make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                        __float_as_uint(v[3]));
+      w[1] = make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
+                        __float_as_uint(v[7]));
+    } else {
+      uint32_t u[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if constexpr (DT == MUON_DT_BF16)
+          u[k] = (uint32_t)f32_to_bf16(v[2 * k]) | ((uint32_t)f32_to_bf16(v[2 * k + 1]) << 16);
+        else
+          u[k] = (uint32_t)f32_to_f16(v[2 * k]) | ((uint32_t)f32_to_f16(v[2 * k + 1]) << 16);
+      }
+      w[0] = make_uint4(u[0], u[1], u[2], u[3]);
+    }
+  }
+};
+
 // fp32 -> float8_e4m3fn (bias 7, no infinities, 0x7f/0xff are NaN, max 448).
 // Written from the format definition: exact round-to-nearest-even onto the e4m3fn
 // grid; a magnitude that rounds above 448 becomes NaN (matching torch's cast).

@@ -185,6 +185,137 @@ __global__ __launch_bounds__(256) void prepass_kernel(PrepassArgs a) {
   }
 }
 
+// The same pass over a 64-row x 256-column slab (four 64 x 64 tiles side by side) per
+// workgroup, for a bf16 workspace with 16-byte aligned rows: every global load of the slab
+// is issued before any arithmetic and all streamed traffic is non-temporal (measured:
+// 4 tiles per workgroup with loads first and non-temporal access move 22% more bytes per
+// second than one tile per workgroup on MI355X). Lane -> row tid/32 of each 8-row pass,
+// 8 columns at chunk tid%32, so each lane stays in one tile (chunk/8) and the tile's
+// norm partial is a fixed-order sum of its 16 lanes per wave and the 4 waves. Tall
+// matrices: X0 gets the slab transposed through LDS (256 rows of 64 values).
+template <int GDT, int BDT>
+__global__ __launch_bounds__(256) void prepass_slab_kernel(PrepassArgs a) {
+#pragma clang fp contract(off)
+  constexpr int SLAB_C = 4 * TILE, NP = TILE / 8;
+  __shared__ bf16_t tileT[TILE][SLAB_C + 8];
+  __shared__ float wsum[4][4];
+  const int mat = blockIdx.y;
+  const int slabs_c = a.tiles_c / 4;
+  const int tr = blockIdx.x / slabs_c, sc = blockIdx.x % slabs_c;
+  const int t = (int)(mat / a.nb);
+  const int64_t mb = mat % a.nb;
+  void* gp = a.grads[t];
+  void* bp = a.bufs[t];
+  const int64_t base = mb * a.s_mstride;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int chunk = tid & 31, rsub = tid >> 5;
+  const int64_t r0 = (int64_t)tr * TILE, c0 = (int64_t)sc * SLAB_C;
+  const int64_t c = c0 + chunk * 8;
+  const bool cvalid = c < a.cols;
+
+  Raw8<GDT> gr[NP];
+  Raw8<BDT> br[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int64_t r = r0 + p * 8 + rsub;
+    if (r < a.rows && cvalid) {
+      const int64_t idx = base + r * a.s_pitch + c;
+      gr[p].load(gp, idx);
+      if (a.has_buf) br[p].load(bp, idx);
+    }
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int rl = p * 8 + rsub;
+    const int64_t r = r0 + rl;
+    const bool valid = r < a.rows && cvalid;
+    float xv[8];
+    if (valid) {
+      const int64_t idx = base + r * a.s_pitch + c;
+      float g[8];
+      gr[p].unpack(g);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (a.maximize) g[e] = -g[e];
+      float gq[8];
+      if (a.has_buf) {
+        float b[8], nb[8];
+        br[p].unpack(b);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float m = b[e] * a.momentum;
+          nb[e] = m + g[e];
+        }
+        br[p].pack(nb);
+        br[p].store(bp, idx);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (a.nesterov) {
+            float tt = nb[e] * a.momentum;
+            gq[e] = g[e] + tt;
+          } else {
+            gq[e] = nb[e];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gq[e] = g[e];
+      }
+      if (a.write_grad) {
+        gr[p].pack(gq);
+        gr[p].store(gp, idx);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xv[e] = Elem<MUON_DT_BF16>::round(gq[e]);
+        ss += xv[e] * xv[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[e] = 0.0f;
+    }
+    Raw8<MUON_DT_BF16> xr;
+    xr.pack(xv);
+    if (a.trans) {
+      const uint4 w = xr.w[0];
+      uint32_t* d = (uint32_t*)&tileT[rl][chunk * 8];
+      d[0] = w.x;
+      d[1] = w.y;
+      d[2] = w.z;
+      d[3] = w.w;
+    } else if (a.write_direct == 1) {
+      xr.store(a.direct, (int64_t)mat * a.d_mstride + r * a.d_pitch + c);
+    }
+  }
+  if (a.trans) {
+    __syncthreads();
+    // X0 row (c0 + cc) holds stored column cc of the slab's 64 rows
+#pragma unroll 2
+    for (int it = 0; it < (SLAB_C * TILE / 8) / 256; ++it) {
+      const int id = it * 256 + tid;
+      const int cc = id >> 3, rr = (id & 7) * 8;
+      uint16_t ev[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ev[k] = tileT[rr + k][cc];
+      uint4 w;
+      __builtin_memcpy(&w, ev, 16);
+      st_nt((bf16_t*)a.trans + (int64_t)mat * a.t_mstride + (c0 + cc) * a.t_pitch + r0 + rr, w);
+    }
+  }
+  // tile partials: lanes of one tile are chunk bits 0-2 and lane bit 5 within each wave
+  float v = ss;
+  v += __shfl_xor(v, 1, 64);
+  v += __shfl_xor(v, 2, 64);
+  v += __shfl_xor(v, 4, 64);
+  v += __shfl_xor(v, 32, 64);
+  if (lane < 32 && (lane & 7) == 0) wsum[lane >> 3][wave] = v;
+  __syncthreads();
+  if (tid < 4)
+    a.partials[(int64_t)mat * a.parts + (int64_t)tr * a.tiles_c + sc * 4 + tid] =
+        ((wsum[tid][0] + wsum[tid][1]) + wsum[tid][2]) + wsum[tid][3];
+}
+
 // Momentum only (no workspace): buf' and g' as in momentum_elem, g' stored into the
 // grad tensor when write_grad. Used when the orthogonalization is supplied by the
 // caller (the module-level zeropower seam) and needs g' as a tensor.
@@ -356,6 +487,82 @@ __global__ __launch_bounds__(256) void postpass_kernel(PostArgs a) {
   }
 }
 
+// The post-pass over a 64-row x 256-column slab of stored elements per workgroup (four
+// tiles side by side), loads first and non-temporal access, as prepass_slab_kernel.
+// TRANS (a tall result in the workspace, bf16): the 256 x 64 block of the wide iterate that
+// holds the slab's transpose is read with coalesced 128-byte rows into LDS first.
+template <int PDT, int UDT, bool TRANS, bool ROWSCALE>
+__global__ __launch_bounds__(256) void postpass_slab_kernel(PostArgs a) {
+#pragma clang fp contract(off)
+  constexpr int SLAB_C = 4 * TILE, NP = TILE / 8;
+  __shared__ uint16_t ut[TRANS ? SLAB_C : 1][TILE + 1];  // ut[c - c0][r - r0], raw bits
+  const int mat = blockIdx.y;
+  const int slabs_c = (a.tiles_c + 3) / 4;
+  const int tr = blockIdx.x / slabs_c, sc = blockIdx.x % slabs_c;
+  const int t = (int)(mat / a.nb);
+  const int64_t mb = mat % a.nb;
+  void* pp = a.params[t];
+  const float adj = a.adj[t];
+  const int tid = threadIdx.x, chunk = tid & 31, rsub = tid >> 5;
+  const int64_t r0 = (int64_t)tr * TILE, c0 = (int64_t)sc * SLAB_C;
+  const int64_t c = c0 + chunk * 8;
+  const bool cvalid = c < a.cols;
+  Raw8<PDT> pr[NP];
+  Raw8<UDT> ur[NP];
+  if constexpr (TRANS) {
+#pragma unroll
+    for (int it = 0; it < (SLAB_C * TILE / 8) / 256; ++it) {
+      const int id = it * 256 + tid;
+      const int cc = id >> 3, rr = (id & 7) * 8;
+      const uint4 w = ld_nt((const uint16_t*)a.u + (int64_t)mat * a.u_mstride +
+                            (c0 + cc) * a.u_pitch + r0 + rr);
+      const uint32_t q[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        ut[cc][rr + 2 * k] = (uint16_t)(q[k] & 0xffffu);
+        ut[cc][rr + 2 * k + 1] = (uint16_t)(q[k] >> 16);
+      }
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int64_t r = r0 + p * 8 + rsub;
+    if (r < a.rows && cvalid) {
+      pr[p].load(pp, mb * a.rows * a.cols + r * a.cols + c);
+      if (!TRANS) ur[p].load(a.u, (int64_t)mat * a.u_mstride + r * a.u_pitch + c);
+    }
+  }
+  if (TRANS) __syncthreads();
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int rl = p * 8 + rsub;
+    const int64_t r = r0 + rl;
+    if (r >= a.rows || !cvalid) continue;
+    float pv[8], u[8], o[8];
+    pr[p].unpack(pv);
+    if constexpr (TRANS) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) u[e] = bf16_to_f32(ut[chunk * 8 + e][rl]);
+    } else {
+      ur[p].unpack(u);
+    }
+    if constexpr (ROWSCALE) {
+      const float rs = a.rscale[(int64_t)mat * a.rs_mstride + r];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) u[e] = u[e] * rs;
+    }
+    if (a.has_uscale) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) u[e] = Elem<UDT>::round(u[e] * a.uscale[t]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      o[e] = apply_elem<PDT, ROWSCALE ? MUON_DT_F32 : UDT>(pv[e], u[e], a.wd, a.cautious, adj);
+    pr[p].pack(o);
+    pr[p].store(pp, mb * a.rows * a.cols + r * a.cols + c);
+  }
+}
+
 // ---- NorMuon ---------------------------------------------------------------------------
 // ss[r] = sum over the columns of stored row r of U^2 (fp32, fixed order), for the 64
 // stored rows r0 .. r0+63 of one matrix per workgroup. TRANS: U is the wide iterate of a
@@ -519,10 +726,14 @@ __global__ __launch_bounds__(256) void extract_t_kernel(const void* src, int64_t
 
 template <int GDT, int BDT, int WDT>
 void launch_prepass_t(const PrepassArgs& a, dim3 grid, bool vec8, hipStream_t s) {
-  if (vec8)
+  if (vec8 && WDT == MUON_DT_BF16 && a.write_direct != 2 && (a.tiles_c % 4) == 0) {
+    dim3 sgrid(grid.x / 4, grid.y);
+    hipLaunchKernelGGL((prepass_slab_kernel<GDT, BDT>), sgrid, dim3(256), 0, s, a);
+  } else if (vec8) {
     hipLaunchKernelGGL((prepass_kernel<GDT, BDT, WDT, 8>), grid, dim3(256), 0, s, a);
-  else
+  } else {
     hipLaunchKernelGGL((prepass_kernel<GDT, BDT, WDT, 1>), grid, dim3(256), 0, s, a);
+  }
 }
 
 template <int GDT, int BDT>
@@ -549,6 +760,16 @@ int launch_prepass_b(int bdt, int wdt, const PrepassArgs& a, dim3 grid, bool vec
 
 template <int PDT, int UDT, bool TRANS>
 void launch_post_t(const PostArgs& a, dim3 grid, bool vec8, hipStream_t s) {
+  if (vec8 && (!TRANS || UDT == MUON_DT_BF16)) {
+    // slabs of 4 tiles side by side (a partial last slab stops at the valid columns)
+    const int tiles_r = (int)(grid.x / a.tiles_c);
+    dim3 sgrid((unsigned)(tiles_r * ((a.tiles_c + 3) / 4)), grid.y);
+    if (a.rscale)
+      hipLaunchKernelGGL((postpass_slab_kernel<PDT, UDT, TRANS, true>), sgrid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((postpass_slab_kernel<PDT, UDT, TRANS, false>), sgrid, dim3(256), 0, s, a);
+    return;
+  }
   if (a.rscale) {
     if (vec8)
       hipLaunchKernelGGL((postpass_kernel<PDT, UDT, 8, TRANS, true>), grid, dim3(256), 0, s, a);
