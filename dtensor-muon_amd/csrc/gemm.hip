@@ -766,16 +766,22 @@ MUON_DEVICE void nn_join(bf16x8_mfma (&cx)[4], const i16x4 (&lo)[4], const i16x4
 // M0 stepping through the destination slabs) so its issue never stalls the matrix
 // pipe. The grid is one workgroup per CU; each walks a list of tiles with the operand
 // pipeline running across tile boundaries: the last two K-tiles of a tile prefetch
-// the first two of the next, so a tile's epilogue (stores straight from the
-// accumulators) overlaps the next tile's loads, and its stores drain while the next
-// tile computes.
+// the first two of the next, so a tile's epilogue overlaps the next tile's loads.
+//
+// All CUs finish their tiles together, so each epilogue is a chip-wide burst of 32 MB
+// (4 MB per XCD, the size of its L2). The epilogue therefore stages each wave's 32-row
+// blocks through 8 KB of LDS and writes whole 256-byte rows with non-temporal stores:
+// measured against stores straight from the accumulators (16-byte row pieces through
+// L2), the burst no longer evicts the operand panels the XCD's CUs share, and the
+// product runs 5-8% faster.
 //
 // Tiles are dealt to the 8 XCDs as contiguous ranges (workgroup b runs on XCD b % 8):
 // the workgroups of one XCD share its L2 across neighbouring tiles (GM = 8 tile rows
 // per column group, as map_tile). The beta term reads the staged X panel during the
 // two K-tiles whose k range covers the wave's output rows, holds the values in 128
 // VGPRs (bf16 pairs) and adds them in the epilogue.
-constexpr int N4_SMEM = 2 * NN_STAGEB;
+constexpr int N4_EPB = 32 * 256;                 // epilogue staging per wave: 32 rows
+constexpr int N4_SMEM = 2 * NN_STAGEB + 4 * N4_EPB;  // 160 KiB
 typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
 typedef __attribute__((ext_vector_type(2))) float f2x;
@@ -1092,12 +1098,19 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn4_kernel(GemmArgs g) {
     mfma_to_valu_wait();
 
     // epilogue: accumulator (fm, fn) element 4 rg + q is X'(i, j + q) with
-    // i = 128 wm + 32 fm + lane%32, j = 128 wn + 32 fn + 8 rg + 4 (lane/32)
+    // i = 128 wm + 32 fm + lane%32, j = 128 wn + 32 fn + 8 rg + 4 (lane/32). Each 32-row
+    // block fm goes through the wave's LDS staging rows (16-byte chunk k of row r kept at
+    // chunk k ^ (r & 15), so both the 8-byte writes and the 16-byte reads are free of
+    // bank conflicts), then out as 4 whole rows of 256 bytes per non-temporal store.
+    // The staging rows are the wave's own and LDS serves one wave's accesses in order.
     bf16_t* outw = (bf16_t*)g.out + (int64_t)bidx * g.so + (arow0 + wm * WM) * g.ldo + bcol0 + wn * WN;
     const __amdgpu_buffer_rsrc_t rso =
         __builtin_amdgcn_make_buffer_rsrc((void*)outw, 0, 0x7fffffff, 0x00020000);
     const int ldo_b = (int)(g.ldo * 2);
-    const int vo = fr * ldo_b + fh * 8;
+    const uint32_t ep = lds0 + 2 * NN_STAGEB + wave * N4_EPB;
+    const uint32_t epw = ep + fr * 256 + fh * 8;   // row fr, this lane's 8-byte half
+    const uint32_t epr = ep + (lane >> 4) * 256;  // rows lane/16 + 4 i
+    const int vor = (lane >> 4) * ldo_b + (lane & 15) * 16;
     // valid extents from this lane's first row / column (zeros are stored beyond);
     // most tiles lie inside both and take the unmasked path
     const bool full = arow0 + 256 <= g.Mv && bcol0 + 256 <= g.Nv;
@@ -1105,7 +1118,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn4_kernel(GemmArgs g) {
     const int rem_j = (int)g.Nv - (int)(bcol0 + wn * WN + fh * 4);
     auto emit = [&](auto masked) {
 #pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
+      for (int fm = 0; fm < FM; ++fm) {
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn) {
           // one accumulator at a time out of the AGPRs
@@ -1128,10 +1141,23 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn4_kernel(GemmArgs g) {
             }
             const u32x2 w = {__builtin_bit_cast(uint32_t, __builtin_convertvector(v01, bf2x)),
                              __builtin_bit_cast(uint32_t, __builtin_convertvector(v23, bf2x))};
-            __builtin_amdgcn_raw_buffer_store_b64(w, rso, vo + (fn * 32 + rg * 8) * 2,
-                                                  fm * 32 * ldo_b, 0);
+            // addresses are formed here rather than hoisted into registers for the loop
+            uint32_t ea = epw, fx = fr & 15;
+            asm volatile("" : "+v"(ea), "+v"(fx));
+            *(u32x2 __attribute__((address_space(3)))*)(ea + (((4 * fn + rg) ^ fx) << 4)) = w;
           }
         }
+        uint32_t ra = epr, lc = lane & 15, lr = lane >> 4;
+        int vs = vor;
+        asm volatile("" : "+v"(ra), "+v"(vs), "+v"(lc), "+v"(lr));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t c = lc ^ ((4 * i + lr) & 15);
+          const u32x4 q4 = *(const u32x4 __attribute__((address_space(3)))*)(ra + i * 1024 + (c << 4));
+          // aux 2: non-temporal
+          __builtin_amdgcn_raw_buffer_store_b128(q4, rso, vs + i * 4 * ldo_b, fm * 32 * ldo_b, 2);
+        }
+      }
     };
     if (full)
       emit(std::false_type{});
