@@ -10,6 +10,7 @@
 // tiled kernel (below) keeps each block in registers and finds 8-bit codes through a
 // bucket table that gives the same result as the search.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 
@@ -312,6 +313,30 @@ MUON_DEVICE int quant_code_thr_all(float y, const uint32_t* thr) {
   return (y != y) ? 0 : lo;
 }
 
+// Max over aligned groups of `lanes` consecutive lanes (a power of two, 1 to 32): DPP
+// moves within rows of 16 (quad xor 1 and 2, then the 8- and 16-lane mirrors, which pair
+// every lane with one of the other half) and a swizzle for xor 16; each level applies
+// only while the group is wider than the distance it covers.
+MUON_DEVICE float group_max(float v, int lanes) {
+  auto dpp = [](float x, auto ctrl) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), decltype(ctrl)::value,
+                                           0xF, 0xF, false));
+  };
+  float t = dpp(v, std::integral_constant<int, 0xB1>{});  // quad_perm [1,0,3,2]
+  v = lanes > 1 ? fmaxf(v, t) : v;
+  t = dpp(v, std::integral_constant<int, 0x4E>{});        // quad_perm [2,3,0,1]
+  v = lanes > 2 ? fmaxf(v, t) : v;
+  t = dpp(v, std::integral_constant<int, 0x141>{});       // row_half_mirror
+  v = lanes > 4 ? fmaxf(v, t) : v;
+  t = dpp(v, std::integral_constant<int, 0x140>{});       // row_mirror
+  v = lanes > 8 ? fmaxf(v, t) : v;
+  // bitmask swizzle within 32 lanes: and 0x1f, or 0, xor 0x10
+  t = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+  v = lanes > 16 ? fmaxf(v, t) : v;
+  return v;
+}
+
 template <int GDT, int QF, bool TALL>
 __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
 #pragma clang fp contract(off)
@@ -342,30 +367,51 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
   const float mom = a.momentum;
   constexpr int NP = LPT_ROWS / 8;
 
-  // every global load of the tile first (gradient, code bytes, old scale per pass)
-  float g[NP][8];
+  // The table loads go first, then every data load of the tile (gradient, code bytes,
+  // old scale per pass) from a clamped row (rows past the end re-read the last row and
+  // are not used), with nothing consumed in between, so all of them are in flight at
+  // once. The barrier that publishes the tables waits for this wave's table writes only
+  // (a __syncthreads would wait for every outstanding load of the tile), and pass p
+  // starts as soon as its own data has arrived.
+  uint4 tq0 = {}, tq1 = {}, tq2 = {}, tq3 = {};
+  float tqm = 0.0f;
+  uint32_t tt0 = 0, tt1 = 0;
+  if (MAP) {
+    static_assert(MUON_QTAB_SIZE == 4 * 256 * 16, "one 16-byte table piece per thread and step");
+    const uint4* gt = (const uint4*)a.qtab + tid;
+    const uint32_t* gthr = (const uint32_t*)(a.qtab + MUON_QTAB_SIZE);
+    tqm = a.qmap[tid < (QF == MUON_Q_8BIT ? 256 : 16) ? tid : 0];
+    tq0 = gt[0];
+    tq1 = gt[256];
+    tq2 = gt[512];
+    tq3 = gt[768];
+    tt0 = gthr[tid];
+    tt1 = gthr[256 + (tid & (MUON_QTHR_PAD - 1))];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  Raw8<GDT> graw[NP];
   typename LpCodes<QF>::T cw[NP];
   float osc[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int64_t r = r0 + p * 8 + rsub;
-    if (r < a.rows) {
-      const int64_t e = (mb * a.rows + r) * a.cols + c;  // element index in the tensor
-      Vec8<GDT>::load(gp, e, g[p]);
-      cw[p] = LpCodes<QF>::load(codes, e);
-      osc[p] = scales[e >> a.block_shift];
-    }
+    const int64_t rr = r < a.rows ? r : a.rows - 1;
+    const int64_t e = (mb * a.rows + rr) * a.cols + c;  // element index in the tensor
+    graw[p].load(gp, e);
+    cw[p] = LpCodes<QF>::load(codes, e);
+    osc[p] = scales[e >> a.block_shift];
   }
   if (MAP) {
-    q[tid] = a.qmap[tid < (QF == MUON_Q_8BIT ? 256 : 16) ? tid : 0];
-#pragma unroll
-    for (int i = 0; i < MUON_QTAB_SIZE / 16 / 256; ++i)
-      ((uint4*)qtab)[i * 256 + tid] = ((const uint4*)a.qtab)[i * 256 + tid];
-    const uint32_t* gthr = (const uint32_t*)(a.qtab + MUON_QTAB_SIZE);
-    qthr[tid] = gthr[tid];
-    if (tid < MUON_QTHR_PAD) qthr[256 + tid] = gthr[256 + tid];
+    q[tid] = tqm;
+    ((uint4*)qtab)[tid] = tq0;
+    ((uint4*)qtab)[256 + tid] = tq1;
+    ((uint4*)qtab)[512 + tid] = tq2;
+    ((uint4*)qtab)[768 + tid] = tq3;
+    qthr[tid] = tt0;
+    if (tid < MUON_QTHR_PAD) qthr[256 + tid] = tt1;
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt and expcnt untouched
+    __builtin_amdgcn_s_barrier();
   }
-  __syncthreads();
 
   bf16_t* x0 = (bf16_t*)a.x0 + (int64_t)mat * a.x_mstride;
   float ss = 0.0f;
@@ -377,18 +423,20 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
     uint32_t xw[4];  // X as bf16 pairs (RNE), element 2i in the low half
     if (valid) {
       const int64_t e = (mb * a.rows + r) * a.cols + c;
+      float g[8];
+      graw[p].unpack(g);
       float m[8], gq[8];
       float amax = 0.0f;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        if (a.maximize) g[p][k] = -g[p][k];
+        if (a.maximize) g[k] = -g[k];
         float v = code_value<QF>(LpCodes<QF>::get(cw[p], k), q) * osc[p];
         v = v * mom;
-        m[k] = v + g[p][k];
+        m[k] = v + g[k];
         amax = fmaxf(amax, fabsf(m[k]));
       }
       // absmax over the block_lanes consecutive lanes of this block (all in one row)
-      for (int off = 1; off < block_lanes; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+      amax = group_max(amax, block_lanes);
       float sc = amax > 1e-12f ? amax : 1e-12f;
       if (QF == MUON_Q_FP8) sc = sc / 448.0f;
       float ys[8];
@@ -413,7 +461,7 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
         gq[k] = m[k];
         if (a.nesterov) {
           const float tt = m[k] * mom;
-          gq[k] = g[p][k] + tt;
+          gq[k] = g[k] + tt;
         }
       }
 #pragma unroll
