@@ -65,7 +65,9 @@ MUON_DEVICE int quant_code(float y, const float* q) {
     const float half = (hi - lo) * 0.5f;
     return res >= half ? up : c;
   } else {
-    return f32_to_e4m3fn(y);
+    // a NaN quotient codes as the positive NaN 0x7f (the canonical NaN a GPU division
+    // returns; its sign is not defined by IEEE 754)
+    return y != y ? 0x7f : f32_to_e4m3fn(y);
   }
 }
 
@@ -85,6 +87,25 @@ MUON_DEVICE float dequant(const uint8_t* codes, int64_t e, const float* q, float
 template <int QF>
 constexpr int unit_size() {
   return QF == MUON_Q_4BIT ? 2 : 1;
+}
+
+// Block absmax as the bit patterns of |v|: for non-negative floats the unsigned order is
+// the numeric order, and NaN patterns sort above infinity, so a NaN in the block wins as
+// it does in torch's amax (and the oracle's np.max).
+MUON_DEVICE uint32_t abs_bits(float v) { return __float_as_uint(v) & 0x7fffffffu; }
+MUON_DEVICE uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
+  return v;
+}
+// Block scale from the absmax: clipped below at 1e-12 (a NaN absmax stays NaN, as
+// torch's clamp keeps it), divided by 448 for fp8.
+template <int QF>
+MUON_DEVICE float block_scale(uint32_t amax_bits) {
+  const float amax = __uint_as_float(amax_bits);
+  float sc = amax < 1e-12f ? 1e-12f : amax;
+  if (QF == MUON_Q_FP8) sc = sc / 448.0f;
+  return sc;
 }
 
 template <int GDT, int QF>
@@ -107,7 +128,7 @@ __global__ __launch_bounds__(256) void lp_prepass_kernel(LpArgs a) {
   const int64_t units = a.block / US;
 
   // pass 1: momentum in fp32 and the block absmax of the new buffer
-  float amax = 0.0f;
+  uint32_t ab = 0;
   for (int64_t u = lane; u < units; u += 64) {
 #pragma unroll
     for (int k = 0; k < US; ++k) {
@@ -116,12 +137,10 @@ __global__ __launch_bounds__(256) void lp_prepass_kernel(LpArgs a) {
       if (a.maximize) g = -g;
       float m = dequant<QF>(codes, e, q, old_scale) * a.momentum;
       m = m + g;
-      amax = fmaxf(amax, fabsf(m));
+      ab = max(ab, abs_bits(m));
     }
   }
-  amax = warp_max(amax);
-  float sc = amax > 1e-12f ? amax : 1e-12f;
-  if (QF == MUON_Q_FP8) sc = sc / 448.0f;
+  const float sc = block_scale<QF>(wave_max_u32(ab));
 
   // pass 2: recompute, quantize with the new scale, emit X = cast(g') in the stored layout
   const int64_t mat_elems = a.rows * a.cols;
@@ -232,7 +251,7 @@ MUON_DEVICE float code_value(int code, const float* q) {
 // the value of a key (the smallest value of bucket b is the value of key b << SHIFT).
 MUON_DEVICE uint32_t f32_order_key(float v) {
   const uint32_t b = __float_as_uint(v);
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);  // negative: ~b; else b | sign
 }
 MUON_DEVICE float f32_from_order_key(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
@@ -287,15 +306,17 @@ __global__ __launch_bounds__(256) void build_qtab_kernel(const uint32_t* thr, in
   qtab[b] = (uint8_t)lo;
 }
 
-// quant_code<QF> (8- or 4-bit) through the thresholds: a table read and two compares,
-// branch-free so the compiler can overlap the lookups of many values. Sets `more` when the
-// bucket holds more thresholds than that (then quant_code_thr_all gives the code).
+// quant_code<QF> (8- or 4-bit) of a non-NaN y through the thresholds: a table read and
+// two compares, branch-free so the compiler can overlap the lookups of many values. Sets
+// `more` when the bucket holds more thresholds than that (then quant_code_thr_all gives
+// the code). A NaN y gets an in-range code here; the caller routes it to
+// quant_code_thr_all.
 MUON_DEVICE int quant_code_thr(float y, const uint32_t* thr, const uint8_t* qtab, bool& more) {
   const uint32_t ky = f32_order_key(y);
   const int c0 = qtab[ky >> MUON_QTAB_SHIFT];
   const int c = c0 + (ky >= thr[c0] ? 1 : 0) + (ky >= thr[c0 + 1] ? 1 : 0);
   more = more || ky >= thr[c0 + 2];
-  return (y != y) ? 0 : c;  // NaN: the search gives 0 and the half-step test fails
+  return c;
 }
 
 // The code as the full count of thresholds <= key(y).
@@ -313,29 +334,20 @@ MUON_DEVICE int quant_code_thr_all(float y, const uint32_t* thr) {
   return (y != y) ? 0 : lo;
 }
 
-// Max over aligned groups of `lanes` consecutive lanes (a power of two, 1 to 32): DPP
-// moves within rows of 16 (quad xor 1 and 2, then the 8- and 16-lane mirrors, which pair
-// every lane with one of the other half) and a swizzle for xor 16; each level applies
-// only while the group is wider than the distance it covers.
-MUON_DEVICE float group_max(float v, int lanes) {
-  auto dpp = [](float x, auto ctrl) {
-    return __builtin_bit_cast(
-        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), decltype(ctrl)::value,
-                                           0xF, 0xF, false));
-  };
-  float t = dpp(v, std::integral_constant<int, 0xB1>{});  // quad_perm [1,0,3,2]
-  v = lanes > 1 ? fmaxf(v, t) : v;
-  t = dpp(v, std::integral_constant<int, 0x4E>{});        // quad_perm [2,3,0,1]
-  v = lanes > 2 ? fmaxf(v, t) : v;
-  t = dpp(v, std::integral_constant<int, 0x141>{});       // row_half_mirror
-  v = lanes > 4 ? fmaxf(v, t) : v;
-  t = dpp(v, std::integral_constant<int, 0x140>{});       // row_mirror
-  v = lanes > 8 ? fmaxf(v, t) : v;
+// Unsigned max over aligned groups of `lanes` consecutive lanes (a power of two, 1 to
+// 32; wave-uniform, so each level is a scalar branch): DPP moves within rows of 16 (quad
+// xor 1 and 2, then the 8- and 16-lane mirrors, which pair every lane with one of the
+// other half) and a swizzle for xor 16.
+MUON_DEVICE uint32_t group_max_u32(uint32_t v, int lanes) {
+  if (lanes > 1) v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true));
+  if (lanes > 2) v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true));
+  if (lanes > 4) v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, true));
+  if (lanes > 8) v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, true));
   // bitmask swizzle within 32 lanes: and 0x1f, or 0, xor 0x10
-  t = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-  v = lanes > 16 ? fmaxf(v, t) : v;
+  if (lanes > 16) v = max(v, (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401F));
   return v;
 }
+typedef __attribute__((ext_vector_type(2))) __bf16 bf2v;
 
 template <int GDT, int QF, bool TALL>
 __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
@@ -425,20 +437,18 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
       const int64_t e = (mb * a.rows + r) * a.cols + c;
       float g[8];
       graw[p].unpack(g);
-      float m[8], gq[8];
-      float amax = 0.0f;
+      const float gs = a.maximize ? -1.0f : 1.0f;  // g * gs is exact: the fma rounds once
+      float m[8];
+      uint32_t ab = 0;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        if (a.maximize) g[k] = -g[k];
         float v = code_value<QF>(LpCodes<QF>::get(cw[p], k), q) * osc[p];
         v = v * mom;
-        m[k] = v + g[k];
-        amax = fmaxf(amax, fabsf(m[k]));
+        m[k] = __builtin_fmaf(g[k], gs, v);
+        ab = max(ab, abs_bits(m[k]));
       }
       // absmax over the block_lanes consecutive lanes of this block (all in one row)
-      amax = group_max(amax, block_lanes);
-      float sc = amax > 1e-12f ? amax : 1e-12f;
-      if (QF == MUON_Q_FP8) sc = sc / 448.0f;
+      const float sc = block_scale<QF>(group_max_u32(ab, block_lanes));
       float ys[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) ys[k] = m[k] / sc;
@@ -446,31 +456,35 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
       if (QF == MUON_Q_FP8) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) cq[k] = f32_to_e4m3fn(ys[k]);
+        if (!(sc <= 3.40282347e38f)) {
+          // NaN or infinite scale: NaN quotients code as the positive NaN 0x7f
+#pragma unroll
+          for (int k = 0; k < 8; ++k) cq[k] = ys[k] != ys[k] ? 0x7f : cq[k];
+        }
       } else {
         bool more = false;
 #pragma unroll
         for (int k = 0; k < 8; ++k) cq[k] = quant_code_thr(ys[k], qthr, qtab, more);
-        if (more) {
+        // y is NaN only when the scale is NaN or infinite: those blocks take the full
+        // count, which codes NaN as 0
+        if (more || !(sc <= 3.40282347e38f)) {
 #pragma unroll
           for (int k = 0; k < 8; ++k)
             cq[k] = quant_code_thr_all<QF == MUON_Q_8BIT ? 256 : 16>(ys[k], qthr);
         }
       }
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        gq[k] = m[k];
-        if (a.nesterov) {
-          const float tt = m[k] * mom;
-          gq[k] = g[k] + tt;
-        }
-      }
-#pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const f2x v = {gq[2 * i], gq[2 * i + 1]};
+        float gq0 = m[2 * i], gq1 = m[2 * i + 1];
+        if (a.nesterov) {
+          gq0 = __builtin_fmaf(g[2 * i], gs, m[2 * i] * mom);
+          gq1 = __builtin_fmaf(g[2 * i + 1], gs, m[2 * i + 1] * mom);
+        }
+        const f2x v = {gq0, gq1};
         xw[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2x));
-        const float lo = __uint_as_float(xw[i] << 16), hi = __uint_as_float(xw[i] & 0xffff0000u);
-        ss += lo * lo;
-        ss += hi * hi;
+        // sum of squares of the two bf16 values (products exact in fp32)
+        ss = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2v, xw[i]),
+                                             __builtin_bit_cast(bf2v, xw[i]), ss, false);
       }
       LpCodes<QF>::store(codes, e, cq);
       if ((chunk & (block_lanes - 1)) == 0) scales[e >> a.block_shift] = sc;
@@ -536,11 +550,9 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* src, uint8_t
   const int64_t e0 = blk * block;
   constexpr int US = unit_size<QF>();
   const int64_t units = block / US;
-  float amax = 0.0f;
-  for (int64_t e = lane; e < block; e += 64) amax = fmaxf(amax, fabsf(src[e0 + e]));
-  amax = warp_max(amax);
-  float sc = amax > 1e-12f ? amax : 1e-12f;
-  if (QF == MUON_Q_FP8) sc = sc / 448.0f;
+  uint32_t ab = 0;
+  for (int64_t e = lane; e < block; e += 64) ab = max(ab, abs_bits(src[e0 + e]));
+  const float sc = block_scale<QF>(wave_max_u32(ab));
   for (int64_t u = lane; u < units; u += 64) {
     int cq[US];
 #pragma unroll

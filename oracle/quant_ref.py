@@ -14,6 +14,9 @@ algorithm (itself following bitsandbytes' dynamic quantization map):
 
 Quantizing a value y = x / scale: binary search for the largest code with
 map[code] <= y, then step up one code when y - map[code] >= (map[code+1] - map[code]) / 2.
+A NaN anywhere in a block makes its absmax, and so its scale, NaN (torch's amax and clamp
+propagate NaN, as np.max and np.maximum do here); every value of such a block then
+quantizes a NaN quotient: code 0 for the maps (every comparison fails), 0x7f for fp8.
 
 Parity of these codes with torchao itself is UNPINNED (torchao is absent); the tests
 pin the restatement with brute-force nearest-code search, the map's structure,
@@ -146,6 +149,9 @@ def quantize(x: np.ndarray, block: int, fmt: str, qmap: np.ndarray | None = None
     scale = _block_scale(x, block, fmt == "fp8")
     y = (x.reshape(-1, block) / scale[:, None]).astype(np.float32).reshape(-1)
     if fmt == "fp8":
+        # the reference divides on the GPU, whose NaN results are the positive canonical
+        # NaN (x86 gives inf / inf a negative one): NaN quotients code as 0x7f
+        y = np.where(np.isnan(y), np.float32(np.nan), y)
         return f32_to_e4m3fn(y), scale
     codes = quantize_codes(y, qmap)
     if fmt == "4bit":

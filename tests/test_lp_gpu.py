@@ -230,3 +230,62 @@ def test_lp_tiled_step_matches_oracle(fmt, cls, block, shape):
         r = _rel(got - ref_p, -adj * U.float())
         assert r < 1e-2, f"step {step}: {r:.3e}"
         ref_p = got.clone()
+
+
+def _same_scales(got, want):
+    """Scales bit-exact where finite; NaN exactly where the oracle has NaN."""
+    gn, wn = np.isnan(got), np.isnan(want)
+    assert np.array_equal(gn, wn)
+    assert np.array_equal(got[~gn].view(np.uint32), want[~wn].view(np.uint32))
+
+
+@pytest.mark.filterwarnings("ignore:invalid value encountered:RuntimeWarning")
+@pytest.mark.parametrize("fmt,cls,block", TILED[:3])
+@pytest.mark.parametrize("path", ["quantize", "general", "tiled-wide", "tiled-tall"])
+def test_lp_nan_and_inf_blocks_match_oracle(fmt, cls, block, path):
+    """A NaN in a block makes the block's scale NaN and codes every value of it as a NaN
+    quotient (0 for the maps, 0x7f for fp8), as torch's amax / clamp do in the reference;
+    an infinite value makes the scale infinite (its own quotient NaN, the others 0).
+    Covered for the standalone quantizer, the general pre-pass (columns not a multiple
+    of 256) and the tiled pre-pass in both orientations, two steps each."""
+    from muonium_amd import _lib
+
+    shape = {"quantize": (64, 256), "general": (128, 96), "tiled-wide": (256, 768),
+             "tiled-tall": (512, 256)}[path]
+    gen = torch.Generator().manual_seed(9)
+    g = torch.randn(shape, generator=gen)
+    g[0, 5] = float("nan")
+    g[7, 60] = float("inf")
+    g[9, 1] = float("-inf")
+    st = _state(cls, shape, block)
+    if path == "quantize":
+        st.copy_(g.to(DEV))
+        codes, scales = quant_ref.quantize(g.numpy(), block, fmt, _qmap(fmt))
+        assert np.array_equal(st.codes.cpu().numpy(), codes)
+        _same_scales(st.scale.cpu().numpy(), scales)
+        assert np.isnan(scales).sum() >= 1 and np.isinf(scales).sum() >= 2
+        return
+    lib = _lib.load()
+    dev = torch.device(DEV)
+    _lib.ensure_device(dev)
+    rows, cols = shape
+    codes = np.zeros(st.codes.numel(), np.uint8)
+    scales = np.zeros(st.scale.numel(), np.float32)
+    ws = torch.zeros(lib.muon_orth_workspace_bytes(_lib.DT_BF16, 1, rows, cols), dtype=torch.uint8,
+                     device=dev)
+    gd = g.to(dev)
+    for step in range(2):
+        rc = lib.muon_lp_prepass(1, _lib.ptr_array([gd]), _lib.DT_F32, _lib.ptr_array([st.codes]),
+                                 _lib.ptr_array([st.scale]),
+                                 st.qmap.data_ptr() if st.qmap is not None else None, st.qformat, block,
+                                 1, rows, cols, 0.9, 1, 0, ws.data_ptr(), _lib.DT_BF16, 1,
+                                 _lib.stream(dev))
+        assert rc == 0, _lib.last_error()
+        torch.cuda.synchronize()
+        codes, scales, _ = quant_ref.lp_momentum_step(
+            codes, scales, g.numpy(), block=block, fmt=fmt, qmap=_qmap(fmt), momentum=0.9,
+            nesterov=True, maximize=False,
+        )
+        assert np.array_equal(st.codes.cpu().numpy(), codes), f"codes differ at step {step}"
+        _same_scales(st.scale.cpu().numpy(), scales)
+    assert np.isnan(scales).sum() >= 3  # the inf blocks turn NaN at the second step
