@@ -39,12 +39,17 @@ CONFIGS = {
     "gpt2": (12, [(768, 2304, 1), (768, 768, 1), (768, 3072, 1), (3072, 768, 1)],
              "GPT-2-small-shaped: 12 x {768x2304, 768x768, 768x3072, 3072x768}"),
     "moe": (16, [(64 * 1408, 2048, 0)], "MoE: 16 x {gate, up (64,1408,2048), down (64,2048,1408)}"),
+    # the same tensors with flatten=True: each becomes one (64, 2883584) matrix
+    "moe_flat": (16, [(64 * 1408, 2048, 0)],
+                 "MoE, flatten=True: 16 x {gate, up (64,1408,2048), down (64,2048,1408)} as (64, 2883584)"),
+    # one fp32 parameter, Newton-Schulz, per-parameter driver
+    "plumbing": (1, [(256, 512, 1)], "plumbing: one fp32 256x512 parameter, Newton-Schulz, foreach=False"),
 }
 
 
 def _shapes(config: str):
     layers, per_layer, _ = CONFIGS[config]
-    if config == "moe":
+    if config in ("moe", "moe_flat"):
         return [(64, 1408, 2048)] * (2 * layers) + [(64, 2048, 1408)] * layers
     out = []
     for _ in range(layers):
@@ -232,31 +237,35 @@ def main() -> None:
         print(json.dumps(blas_ceiling(args.config, dev)), flush=True)
         return
     shapes = _shapes(args.config)
-    strategy = args.strategy or ("newton_schulz" if args.config == "moe" else "polar_express")
+    strategy = args.strategy or ("newton_schulz" if args.config in ("moe", "moe_flat", "plumbing")
+                                 else "polar_express")
+    flatten = args.config == "moe_flat"
+    pdtype = torch.float32 if args.config == "plumbing" else torch.bfloat16
     print(f"[bench] config={args.config} tensors={len(shapes)} strategy={strategy} "
           f"lp={args.lp}", file=sys.stderr, flush=True)
 
     gen = torch.Generator(device=dev).manual_seed(0)
     params = []
     for s in shapes:
-        p = torch.empty(s, dtype=torch.bfloat16, device=dev)
+        p = torch.empty(s, dtype=pdtype, device=dev)
         p.normal_(0.0, 0.02, generator=gen)
         q = torch.nn.Parameter(p)
         rows = s[-2]
         z = torch.randn(*s[:-2], rows, 1, device=dev, generator=gen)
         g = torch.randn(s, device=dev, generator=gen) * torch.exp(z)
-        q.grad = g.to(torch.bfloat16)
+        q.grad = g.to(pdtype)
         del g, z
         params.append(q)
     numel = sum(p.numel() for p in params)
     kw = dict(lr=1e-3, wd=0.1, use_cautious_wd=True, momentum=0.95, nesterov=True, ns_steps=5,
               orthogonalization_strategy=strategy)
+    groups = [{"params": params, "flatten": flatten}]  # flatten is a group key
     if args.lp:
         cls = {"8bit": Muon8bit, "4bit": Muon4bit, "fp8": MuonFp8}[args.lp]
         block = args.block_size or {"8bit": 256, "4bit": 128, "fp8": 256}[args.lp]
-        opt = cls(params, foreach=True, block_size=block, **kw)
+        opt = cls(groups, foreach=True, block_size=block, **kw)
     else:
-        opt = Muon(params, foreach=True, **kw)
+        opt = Muon(groups, foreach=args.config != "plumbing", **kw)
     torch.cuda.synchronize()
     print(f"[bench] params={numel / 1e9:.3f}e9, warmup {args.warmup}", file=sys.stderr, flush=True)
 
@@ -282,7 +291,9 @@ def main() -> None:
     print(f"[bench] {args.steps} steps: {ms_per_step:.2f} ms/step (wall {wall:.2f}s)",
           file=sys.stderr, flush=True)
 
-    flops_step = sum(orth_flops(s, 5) for s in shapes)
+    # the matrices the iteration sees: flatten=True collapses (e, r, c) to (e, r * c)
+    orth_shapes = [(s[0], math.prod(s[1:])) if flatten and len(s) > 2 else s for s in shapes]
+    flops_step = sum(orth_flops(s, 5) for s in orth_shapes)
     value = flops_step / (ms_per_step * 1e-3) / 1e12
     orth_ms = sum(kern[k][0] for k in ("syrk_xx", "syrk_aa", "gemm_bx")) / args.steps
     kernels = {}
@@ -319,7 +330,9 @@ def main() -> None:
     upd_bytes = sum(kern[k][2] for k in ("prepass", "postpass", "lp_prepass")) / args.steps
 
     cpu = None
-    if not args.no_cpu_baseline:
+    # the oracle's per-parameter loop restates the per-matrix problem; it is not run for
+    # the flatten=True workload (a different matrix per tensor)
+    if not args.no_cpu_baseline and args.config != "moe_flat":
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
         cpu = cpu_baseline(args.config)
 

@@ -467,3 +467,24 @@ def test_offloaded_batches_pipeline_matches_device_run(algo, nesterov, maximize,
         for key, val in opt_d.state[d].items():
             assert opt_h.state[h][key].device.type == "cpu"
             assert torch.equal(opt_h.state[h][key], val.cpu()), key
+
+
+def test_plumbing_config_is_bit_repeatable():
+    """Survey config 1: one fp32 256 x 512 parameter (p ~ N(0,1) seed 1, g ~ N(0,1) seed 0),
+    Newton-Schulz 5, cautious wd 0.1, Nesterov 0.95, foreach=False: two runs of the step from
+    the same state give bit-identical parameters and momentum."""
+    p0 = torch.randn(256, 512, generator=torch.Generator().manual_seed(1))
+    g0 = torch.randn(256, 512, generator=torch.Generator().manual_seed(0))
+    outs = []
+    for _ in range(2):
+        p = nn.Parameter(p0.clone().to(DEV))
+        p.grad = g0.clone().to(DEV)
+        opt = Muon([p], lr=1e-3, wd=0.1, use_cautious_wd=True, momentum=0.95, nesterov=True,
+                   ns_steps=5, orthogonalization_strategy="newton_schulz", foreach=False)
+        for _ in range(3):
+            opt.step()
+        torch.cuda.synchronize()
+        outs.append((p.detach().cpu(), opt.state[p]["momentum_buffer"].cpu()))
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1])
+    assert not torch.equal(outs[0][0], p0)
