@@ -334,6 +334,15 @@ MUON_DEVICE int quant_code_thr_all(float y, const uint32_t* thr) {
   return (y != y) ? 0 : lo;
 }
 
+// Workgroup barrier for LDS data: release and acquire fences scoped to LDS around the
+// barrier, so LDS accesses are ordered across it (lgkmcnt(0), s_barrier) while, unlike
+// __syncthreads, outstanding global loads and stores are not waited for.
+MUON_DEVICE void lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Unsigned max over aligned groups of `lanes` consecutive lanes (a power of two, 1 to
 // 32; wave-uniform, so each level is a scalar branch): DPP moves within rows of 16 (quad
 // xor 1 and 2, then the 8- and 16-lane mirrors, which pair every lane with one of the
@@ -356,7 +365,11 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
   __shared__ float q[256];
   __shared__ __align__(16) uint8_t qtab[MAP ? MUON_QTAB_SIZE : 16];
   __shared__ __align__(16) uint32_t qthr[MAP ? 256 + MUON_QTHR_PAD : 4];
-  __shared__ bf16_t tileT[TALL ? LPT_ROWS : 1][TALL ? LPT_PITCH : 1];
+  // the tall transpose tile: one 32-row half at a time for the map formats (their tables
+  // take 18 KB of LDS, and four workgroups per CU need a quarter of the CU's 160 KB), the
+  // whole 64 rows for fp8
+  constexpr int TROWS = MAP ? LPT_ROWS / 2 : LPT_ROWS;
+  __shared__ bf16_t tileT[TALL ? TROWS : 1][TALL ? LPT_PITCH : 1];
   __shared__ float wsum[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int mat = blockIdx.y;
@@ -421,8 +434,7 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
     ((uint4*)qtab)[768 + tid] = tq3;
     qthr[tid] = tt0;
     if (tid < MUON_QTHR_PAD) qthr[256 + tid] = tt1;
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt and expcnt untouched
-    __builtin_amdgcn_s_barrier();
+    lds_sync();
   }
 
   bf16_t* x0 = (bf16_t*)a.x0 + (int64_t)mat * a.x_mstride;
@@ -494,24 +506,28 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
     }
     if (TALL) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) *(uint32_t*)&tileT[rl][chunk * 8 + 2 * i] = xw[i];
+      for (int i = 0; i < 4; ++i) *(uint32_t*)&tileT[rl % TROWS][chunk * 8 + 2 * i] = xw[i];
+      if ((p + 1) % (TROWS / 8) == 0) {
+        // X0 row (c0 + cc) holds stored column cc: TROWS consecutive values, this tile's
+        // rows r0 + p0 ..
+        constexpr int SEGS = TROWS / 8;  // 16-byte pieces per X0 row
+        const int p0 = (p + 1) * 8 - TROWS;
+        lds_sync();
+#pragma unroll
+        for (int it = 0; it < (LPT_COLS * SEGS) / 256; ++it) {
+          const int id = it * 256 + tid;
+          const int cc = id / SEGS, rr = (id % SEGS) * 8;
+          uint16_t ev[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) ev[k] = tileT[rr + k][cc];
+          uint4 w;
+          __builtin_memcpy(&w, ev, 16);
+          *(uint4*)(x0 + (c0 + cc) * a.x_pitch + r0 + p0 + rr) = w;
+        }
+        if (p != NP - 1) lds_sync();  // the next rows reuse the tile
+      }
     } else {
       *(uint4*)(x0 + r * a.x_pitch + c) = make_uint4(xw[0], xw[1], xw[2], xw[3]);
-    }
-  }
-  if (TALL) {
-    // X0 row (c0 + cc) holds stored column cc: 64 consecutive values from the 64 rows
-    __syncthreads();
-#pragma unroll 2
-    for (int it = 0; it < (LPT_COLS * LPT_ROWS / 8) / 256; ++it) {
-      const int id = it * 256 + tid;
-      const int cc = id >> 3, rr = (id & 7) * 8;
-      uint16_t ev[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) ev[k] = tileT[rr + k][cc];
-      uint4 w;
-      __builtin_memcpy(&w, ev, 16);
-      *(uint4*)(x0 + (c0 + cc) * a.x_pitch + r0 + rr) = w;
     }
   }
   ss = warp_sum(ss);
