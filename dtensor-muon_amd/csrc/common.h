@@ -190,38 +190,20 @@ struct Raw8 {
   }
 };
 
-// fp32 -> float8_e4m3fn (bias 7, no infinities, 0x7f/0xff are NaN, max 448).
-// Written from the format definition: exact round-to-nearest-even onto the e4m3fn
-// grid; a magnitude that rounds above 448 becomes NaN (matching torch's cast).
-// Branch-free (both the subnormal and the normal rounding are formed, one selected).
+// fp32 -> float8_e4m3fn (bias 7, no infinities, 0x7f/0xff are NaN, max 448) by the
+// hardware conversion (v_cvt_pk_fp8_f32: OCP e4m3, round to nearest even; a magnitude that
+// rounds above 448 becomes NaN, as torch's cast does). Compared on the GPU with a direct
+// restatement of the format (exact RNE onto the e4m3fn grid) for all 2^32 inputs: identical
+// except for NaN inputs, which the hardware codes 0xff whatever their sign; torch codes a
+// NaN as 0x7f | sign, and so does this function.
 MUON_DEVICE uint8_t f32_to_e4m3fn(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t sign = (u >> 24) & 0x80u;
-  const uint32_t a = u & 0x7fffffffu;
-  // |f| < 2^-6: subnormal range of e4m3 (step 2^-9). |f| * 2^9 rounded to an integer with
-  // ties-to-even is exact in fp32 (power-of-two scaling); 8 is the smallest normal 0x08.
-  const uint32_t sub = (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.0f);
-  // normal range: keep 3 mantissa bits, round to nearest even on the dropped 20 bits
-  uint32_t q = ((((a >> 23) - 120u) << 3) | ((a >> 20) & 7u)) & 0xffu;
-  const uint32_t rem = a & 0xfffffu;
-  q += (rem > 0x80000u || (rem == 0x80000u && (q & 1u))) ? 1u : 0u;
-  uint32_t r = a < 0x3c800000u ? sub : q;
-  // values >= 464 (the midpoint between 448 and the next, unrepresentable, grid point
-  // 480) round above the largest finite value; 464 itself ties to even (448). NaN and
-  // infinity land here too.
-  r = a > 0x43e80000u ? 0x7fu : r;
-  return (uint8_t)(sign | r);
+  const uint32_t h = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(f, 0.0f, 0, false) & 0xffu;
+  return f != f ? (uint8_t)(0x7fu | ((__float_as_uint(f) >> 24) & 0x80u)) : (uint8_t)h;
 }
 
-MUON_DEVICE float e4m3fn_to_f32(uint8_t v) {
-  const uint32_t sign = ((uint32_t)v & 0x80u) << 24;
-  const uint32_t e = (v >> 3) & 0xfu;
-  const uint32_t m = v & 0x7u;
-  const float sub = (float)m * 0.001953125f;  // m * 2^-9, exact
-  uint32_t bits = e == 0 ? __float_as_uint(sub) : (((e + 120u) << 23) | (m << 20));
-  bits = (e == 0xf && m == 0x7) ? 0x7fc00000u : bits;
-  return __uint_as_float(sign | bits);
-}
+// float8_e4m3fn -> fp32 by the hardware conversion (v_cvt_f32_fp8); equal to the format's
+// definition on all 256 codes (the two NaN codes give a NaN).
+MUON_DEVICE float e4m3fn_to_f32(uint8_t v) { return __builtin_amdgcn_cvt_f32_fp8((int)v, 0); }
 
 MUON_DEVICE float warp_sum(float v) {
   // Fixed butterfly order over the 64-lane wavefront: deterministic.

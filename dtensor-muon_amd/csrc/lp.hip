@@ -454,7 +454,20 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
       uint32_t ab = 0;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        float v = code_value<QF>(LpCodes<QF>::get(cw[p], k), q) * osc[p];
+        float v;
+        if constexpr (QF == MUON_Q_FP8) {
+          // hardware e4m3 conversion straight from byte k of the loaded code word
+          const int wd = (int)(k < 4 ? cw[p].x : cw[p].y);
+          switch (k & 3) {  // the byte selector must be a constant; k is unrolled
+            case 0: v = __builtin_amdgcn_cvt_f32_fp8(wd, 0); break;
+            case 1: v = __builtin_amdgcn_cvt_f32_fp8(wd, 1); break;
+            case 2: v = __builtin_amdgcn_cvt_f32_fp8(wd, 2); break;
+            default: v = __builtin_amdgcn_cvt_f32_fp8(wd, 3); break;
+          }
+          v = v * osc[p];
+        } else {
+          v = code_value<QF>(LpCodes<QF>::get(cw[p], k), q) * osc[p];
+        }
         v = v * mom;
         m[k] = __builtin_fmaf(g[k], gs, v);
         ab = max(ab, abs_bits(m[k]));
@@ -465,14 +478,24 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) ys[k] = m[k] / sc;
       int cq[8];
-      if (QF == MUON_Q_FP8) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) cq[k] = f32_to_e4m3fn(ys[k]);
+      uint2 c8 = {0u, 0u};  // fp8: the 8 code bytes, packed by the conversion itself
+      if constexpr (QF == MUON_Q_FP8) {
+        // v_cvt_pk_fp8_f32 writes two codes into the low or high half of the word
+        uint32_t w0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ys[0], ys[1], 0, false);
+        w0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ys[2], ys[3], (int)w0, true);
+        uint32_t w1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ys[4], ys[5], 0, false);
+        w1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ys[6], ys[7], (int)w1, true);
         if (!(sc <= 3.40282347e38f)) {
           // NaN or infinite scale: NaN quotients code as the positive NaN 0x7f
 #pragma unroll
-          for (int k = 0; k < 8; ++k) cq[k] = ys[k] != ys[k] ? 0x7f : cq[k];
+          for (int k = 0; k < 8; ++k) {
+            if (ys[k] != ys[k]) {
+              uint32_t& w = k < 4 ? w0 : w1;
+              w = (w & ~(0xffu << (8 * (k & 3)))) | (0x7fu << (8 * (k & 3)));
+            }
+          }
         }
+        c8 = make_uint2(w0, w1);
       } else {
         bool more = false;
 #pragma unroll
@@ -498,7 +521,10 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
         ss = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2v, xw[i]),
                                              __builtin_bit_cast(bf2v, xw[i]), ss, false);
       }
-      LpCodes<QF>::store(codes, e, cq);
+      if constexpr (QF == MUON_Q_FP8)
+        *(uint2*)(codes + e) = c8;
+      else
+        LpCodes<QF>::store(codes, e, cq);
       if ((chunk & (block_lanes - 1)) == 0) scales[e >> a.block_shift] = sc;
     } else {
 #pragma unroll

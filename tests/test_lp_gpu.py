@@ -289,3 +289,39 @@ def test_lp_nan_and_inf_blocks_match_oracle(fmt, cls, block, path):
         assert np.array_equal(st.codes.cpu().numpy(), codes), f"codes differ at step {step}"
         _same_scales(st.scale.cpu().numpy(), scales)
     assert np.isnan(scales).sum() >= 3  # the inf blocks turn NaN at the second step
+
+
+def test_fp8_codes_exact_at_every_rounding_boundary():
+    """The fp8 quantizer codes y with the hardware e4m3 conversion; against the oracle's
+    restatement of the format at every rounding decision: each midpoint between adjacent
+    e4m3 values and 3 ulps either side, each grid point +-1 ulp, fp32 denormals, the 448
+    edge, both signs, and 4M random values. Every block holds 448 (its absmax), so the
+    block scale is exactly 1 and y = x."""
+    grid = quant_ref.e4m3fn_to_f32(np.arange(0x7f, dtype=np.uint8))  # 0 .. 448
+    vals = []
+    u = lambda x: np.asarray(x, np.float32).view(np.uint32).astype(np.int64)
+    f = lambda b: np.asarray(b, np.uint32).view(np.float32)
+    mids = ((grid[:-1].astype(np.float64) + grid[1:]) / 2).astype(np.float32)
+    for k in range(-3, 4):
+        vals.append(f(np.maximum(u(mids) + k, 0)))
+        vals.append(f(np.maximum(u(grid) + k // 3, 0)))
+    vals.append(f(np.arange(0, 4096, dtype=np.uint32)))                    # fp32 denormals
+    vals.append(np.array([448.0, np.nextafter(np.float32(448), np.float32(0))], np.float32))
+    gen = np.random.default_rng(3)
+    vals.append(gen.uniform(-448, 448, 4 << 20).astype(np.float32))
+    x = np.concatenate([np.concatenate(vals[:-1]), -np.concatenate(vals[:-1]), vals[-1]])
+    x = np.clip(x, -448, 448).astype(np.float32)
+    block = 256
+    per = block - 1
+    nb = -(-x.size // per)
+    xb = np.zeros((nb, block), np.float32)
+    xb[:, 0] = 448.0
+    flat = np.zeros(nb * per, np.float32)
+    flat[: x.size] = x
+    xb[:, 1:] = flat.reshape(nb, per)
+    xt = torch.from_numpy(xb.reshape(-1))
+    st = OptimStateFp8.zeros(xt.shape, block, DEV)
+    st.copy_(xt.to(DEV))
+    codes, scale = quant_ref.quantize(xb.reshape(-1), block, "fp8", None)
+    assert np.all(scale == 1.0)
+    assert np.array_equal(st.codes.cpu().numpy(), codes)
