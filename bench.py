@@ -312,20 +312,39 @@ def main() -> None:
 
     gms, gn, gwork = kern["gemm_bx"]
     avg_ms = gms / max(gn, 1)
-    achieved = (gwork / max(gn, 1)) / (avg_ms * 1e-3) / 1e12
-    traffic, traffic_src = _measured_traffic("gemm_bf16_nn4_kernel", args.config, args.lp)
-    roofline = {
-        "bound": "mfma",
-        "kernel": "gemm_bf16_nn4_kernel (X' = a X + B X)",
-        "achieved": round(achieved, 1),
-        "peak": PEAK_BF16_TFLOPS,
-        "unit": "TFLOP/s",
-        "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-        "traffic": traffic,
-        "traffic_source": traffic_src,
-        "avg_launch_ms": round(avg_ms, 4),
-        "flop_per_launch": gwork / max(gn, 1),
-    }
+    if all(min(s[-2:]) <= 64 for s in orth_shapes) and pdtype == torch.bfloat16:
+        # iterates of at most 64 rows run in short.hip: the B X launch streams X in and X'
+        # out (bf16, 4 m n bytes per matrix), HBM-bound; it also forms the next Gram
+        # partials from registers
+        bx_bytes = sum(5 * 4 * (math.prod(s[:-2]) if len(s) > 2 else 1) * min(s[-2:]) * max(s[-2:])
+                       for s in orth_shapes) * args.steps / max(gn, 1)
+        achieved = bx_bytes / (avg_ms * 1e-3) / 1e9
+        roofline = {
+            "bound": "hbm",
+            "kernel": "short_bx_kernel (X' = a X + B X, 64-row iterate)",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "avg_launch_ms": round(avg_ms, 4),
+            "bytes_per_launch": bx_bytes,
+        }
+    else:
+        achieved = (gwork / max(gn, 1)) / (avg_ms * 1e-3) / 1e12
+        traffic, traffic_src = _measured_traffic("gemm_bf16_nn4_kernel", args.config, args.lp)
+        roofline = {
+            "bound": "mfma",
+            "kernel": "gemm_bf16_nn4_kernel (X' = a X + B X)",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": traffic,
+            "traffic_source": traffic_src,
+            "avg_launch_ms": round(avg_ms, 4),
+            "flop_per_launch": gwork / max(gn, 1),
+        }
     upd_ms = sum(kern[k][0] for k in ("prepass", "postpass", "lp_prepass")) / args.steps
     upd_bytes = sum(kern[k][2] for k in ("prepass", "postpass", "lp_prepass")) / args.steps
 

@@ -53,6 +53,14 @@ int muon_launch_lp_prepass(int ntensors, void* const* grads, int gdt, void* cons
                            int64_t nb, int64_t rows, int64_t cols, float momentum,
                            int nesterov, int maximize, void* direct, int64_t d_pitch,
                            int64_t d_mstride, hipStream_t s);
+int64_t muon_short_parts(int64_t n_pad);
+int muon_launch_short_gram(const OrthLayout& L, const void* x, float* part, int64_t batch,
+                           hipStream_t s);
+int muon_launch_short_poly(const OrthLayout& L, float* part, void* bm, int64_t batch, float pa,
+                           float pb, const float* scale, int first, hipStream_t s);
+int muon_launch_short_bx(const OrthLayout& L, const void* x, void* xo, const void* bm,
+                         float* part, int64_t batch, float alpha, float beta, const float* scale,
+                         int first, int gram, hipStream_t s);
 
 enum { MODE_GEMM = 0, MODE_SYRK = 1 };
 
@@ -119,8 +127,10 @@ class Timed {
 }  // namespace
 
 // Padding granule of the workspace extents: the bf16 tile (256); fp32 tiles (128)
-// divide it.
+// divide it. A short bf16 iterate (m <= 64) pads its rows to SHORT_ROWS only.
 static const int64_t PAD = 256;
+static const int64_t SHORT_ROWS = 64;
+static const int64_t SHORT_PART_BYTES = 3 * 1024 * 4;
 
 OrthLayout muon_orth_layout(int dtype, int64_t batch, int64_t rows, int64_t cols) {
   OrthLayout L;
@@ -130,11 +140,13 @@ OrthLayout muon_orth_layout(int dtype, int64_t batch, int64_t rows, int64_t cols
   L.tall = rows > cols;
   L.m = std::min(rows, cols);
   L.n = std::max(rows, cols);
-  L.m_pad = round_up(std::max<int64_t>(L.m, 1), PAD);
+  L.short_m = dtype == MUON_DT_BF16 && L.m <= SHORT_ROWS;
+  L.m_pad = L.short_m ? SHORT_ROWS : round_up(std::max<int64_t>(L.m, 1), PAD);
   L.n_pad = round_up(std::max<int64_t>(L.n, 1), PAD);
   L.es = dtype == MUON_DT_F32 ? 4 : 2;
   L.batch = batch;
   L.parts = (L.m_pad / 64) * (L.n_pad / 64);
+  L.gparts = L.short_m ? muon_short_parts(L.n_pad) : 0;
   size_t off = 0;
   auto take = [&](size_t bytes) {
     size_t o = off;
@@ -151,6 +163,7 @@ OrthLayout muon_orth_layout(int dtype, int64_t batch, int64_t rows, int64_t cols
   L.off_scale = take((size_t)(batch * 4));
   L.off_qtab = take((size_t)MUON_QTAB_BYTES);
   L.off_rows = take((size_t)(batch * L.n_pad * 4));  // per stored row (NorMuon)
+  L.off_gpart = take((size_t)(batch * L.gparts * SHORT_PART_BYTES));
   L.total = off;
   return L;
 }
@@ -309,6 +322,34 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
     return muon_launch_scale(L, X[0], ws_dtype, batch, scale, s);
   }
   const double bm = (double)batch, md = (double)L.m, nd = (double)L.n;
+  if (L.short_m) {
+    // 64-row iterate: B X streams X once per iteration and leaves the next iteration's
+    // Gram partials behind, so its launch also carries the next X X^T's work
+    float* part = (float*)(w + L.off_gpart);
+    {
+      Timed t(MUON_K_SYRK_XX, bm * md * (md + 1) * nd, s);
+      rc = muon_launch_short_gram(L, X[0], part, batch, s);
+    }
+    if (rc != MUON_OK) return rc;
+    for (int it = 0; it < steps; ++it) {
+      const float a = (float)coeffs[3 * it], b = (float)coeffs[3 * it + 1],
+                  c = (float)coeffs[3 * it + 2];
+      const int first = it == 0;
+      const int more = it + 1 < steps;
+      {
+        Timed t(MUON_K_SYRK_AA, bm * md * (md + 1) * md, s);
+        rc = muon_launch_short_poly(L, part, B, batch, c, b, scale, first, s);
+      }
+      if (rc != MUON_OK) return rc;
+      {
+        Timed t(MUON_K_GEMM_BX, bm * 2.0 * md * md * nd + (more ? bm * md * (md + 1) * nd : 0.0), s);
+        rc = muon_launch_short_bx(L, X[it & 1], X[(it + 1) & 1], B, part, batch, 1.0f, a, scale,
+                                  first, more, s);
+      }
+      if (rc != MUON_OK) return rc;
+    }
+    return MUON_OK;
+  }
   for (int it = 0; it < steps; ++it) {
     const float a = (float)coeffs[3 * it], b = (float)coeffs[3 * it + 1],
                 c = (float)coeffs[3 * it + 2];

@@ -235,15 +235,20 @@ void muon_set_error(const char* fmt, ...);
 // Workspace layout shared by the prepass, iteration and postpass entry points.
 // X0/X1: the wide iterate (m_pad x n_pad, row-major), ping-ponged by the GEMM; the
 // result of a tall matrix is written transposed (n_pad x m_pad) into one of them.
+// A bf16 iterate with at most 64 rows (short) is padded to 64 rows, not 256, and its
+// iterations run in short.hip with Gram partials per column range (off_gpart).
 struct OrthLayout {
   int64_t rows, cols;  // stored (param) matrix shape
   int64_t m, n;        // m = min, n = max: the iteration runs on the wide m x n matrix
   int64_t m_pad, n_pad;
   int tall;            // rows > cols: stored layout is the transpose of X
+  int short_m;         // bf16 and m <= 64: short.hip iterations
   int es;              // element size of the iteration dtype
   int64_t batch;       // capacity in matrices
   int64_t parts;       // norm partials per matrix
-  size_t off_x0, off_x1, off_a, off_b, off_part, off_scale, off_qtab, off_rows, total;
+  int64_t gparts;      // short: Gram partials (column ranges) per matrix
+  size_t off_x0, off_x1, off_a, off_b, off_part, off_scale, off_qtab, off_rows, off_gpart,
+      total;
 };
 
 // Code-search tables of the 8/4-bit quantized state (lp.hip): one byte per bucket of the

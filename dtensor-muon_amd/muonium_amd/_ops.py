@@ -8,6 +8,7 @@ whole bucket.
 
 from __future__ import annotations
 
+import ctypes
 import threading
 
 import numpy as np
@@ -21,13 +22,20 @@ from . import _lib
 # ---------------------------------------------------------------------------------
 # workspace cache: one growable buffer per (device, iteration dtype, padded m, n)
 
-_PAD = 256
 _ws_lock = threading.Lock()
 _ws_cache: dict[tuple, tuple[int, Tensor]] = {}
 
 
-def _pad(x: int) -> int:
-    return (max(x, 1) + _PAD - 1) // _PAD * _PAD
+def _padded_extents(dtype: torch.dtype, rows: int, cols: int) -> tuple[int, int]:
+    """(m_pad, n_pad) of the library's workspace layout for one rows x cols matrix."""
+    off, pitch, mst, trans = (ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64(),
+                              ctypes.c_int())
+    rc = _lib.load().muon_orth_result(_lib.dtype_code(dtype), 1, rows, cols, 0,
+                                      ctypes.byref(off), ctypes.byref(pitch), ctypes.byref(mst),
+                                      ctypes.byref(trans))
+    if rc != 0:
+        raise RuntimeError(f"muonium_amd: bad workspace request {rows}x{cols}: {_lib.last_error()}")
+    return mst.value // pitch.value, pitch.value
 
 
 def workspace(device: torch.device, dtype: torch.dtype, batch: int, rows: int, cols: int):
@@ -36,7 +44,7 @@ def workspace(device: torch.device, dtype: torch.dtype, batch: int, rows: int, c
     The layout only depends on the padded (min, max) extents and the capacity, so
     tall and wide matrices of the same extents share a buffer. Contents need no
     initialization (every launch rewrites what it reads later)."""
-    m, n = _pad(min(rows, cols)), _pad(max(rows, cols))
+    m, n = _padded_extents(dtype, rows, cols)
     key = (device, dtype, m, n)
     with _ws_lock:
         hit = _ws_cache.get(key)

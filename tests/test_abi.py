@@ -51,6 +51,31 @@ def test_workspace_size_formula():
     assert lib.muon_orth_workspace_bytes(_lib.DT_F32, 1, 0, 4) == -1
 
 
+def test_short_workspace_pads_rows_to_64():
+    lib = _lib.load()
+    # bf16 with at most 64 rows on the short side: 64-row iterate, plus per-matrix Gram
+    # partials (12 KB each) over min(256, max(1, panels / 4)) column ranges of 256 columns
+    rows, cols = 48, 70000                 # n_pad 70144: 274 panels -> 68 ranges
+    nbytes = lib.muon_orth_workspace_bytes(_lib.DT_BF16, 3, rows, cols)
+    rup = lambda v: -(-v // 256) * 256
+    x = 3 * 64 * 70144 * 2
+    a = 3 * 64 * 64 * 2
+    parts = 3 * 1 * (70144 // 64) * 4
+    want = (2 * rup(x) + 2 * rup(a) + rup(parts) + 256 + rup(16384 + 1280) + rup(3 * 70144 * 4)
+            + 3 * 68 * 3 * 1024 * 4)
+    assert nbytes == want
+    off, pitch, mst = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    trans = ctypes.c_int()
+    for r, c, t in ((rows, cols, 0), (cols, rows, 1)):
+        assert lib.muon_orth_result(_lib.DT_BF16, 3, r, c, 1, off, pitch, mst, trans) == 0
+        assert (off.value, pitch.value, mst.value, trans.value) == (rup(x), 70144, 64 * 70144, t)
+    # 65 rows, or an fp32 iteration, keep the 256-row tiles
+    assert lib.muon_orth_result(_lib.DT_BF16, 1, 65, 512, 1, off, pitch, mst, trans) == 0
+    assert mst.value == 256 * 512
+    assert lib.muon_orth_result(_lib.DT_F32, 1, 64, 512, 1, off, pitch, mst, trans) == 0
+    assert mst.value == 256 * 512
+
+
 def test_result_location_follows_orientation():
     lib = _lib.load()
     off, pitch, mst = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()

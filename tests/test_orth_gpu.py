@@ -22,12 +22,15 @@ pytestmark = pytest.mark.gpu
 
 BF16_TOL = 1e-2   # HIP bf16 vs the oracle at the same storage points
 FP64_SLACK = 1.25  # HIP bf16 vs fp64: within 1.25x the fused-bf16 oracle's own distance
-TRITON_TOL = 4e-2  # HIP bf16 vs the reference's pe_loop_triton rounding points
+TRITON_TOL = 4e-2  # HIP bf16 vs the reference's pe_loop_triton rounding points (at least)
 FP32_TOL = 1e-5   # HIP fp32 iteration vs the fp64 iteration (non-square inputs)
 FP32_TOL_SQUARE = 3e-5  # square Gaussian inputs: the fp32 iteration itself is ~1.3e-5 off
 
 SHAPES = [(8, 256, 128), (8, 128, 256), (4, 512, 512), (256, 128), (128, 256), (3, 130, 70),
           (2, 70, 300), (1, 768, 2304)]
+# at most 64 rows on the short side: the 64-row iterate of short.hip (one or many column
+# ranges, ragged column counts, tall inputs, a single row)
+SHAPES += [(64, 4096), (3, 48, 1000), (2, 1000, 33), (1, 5000), (2, 64, 70000), (5, 17, 2560)]
 STRATS = ["polar_express", "newton_schulz"]
 
 
@@ -50,7 +53,10 @@ def test_bf16_iteration_matches_oracle(shape, steps, strategy):
     bound = FP64_SLACK * rel_fro(ref, exact) + 2e-3
     assert rel_fro(got, exact) <= bound, f"vs fp64 {rel_fro(got, exact):.3e} > {bound:.3e}"
     tri = muon_ref.polar_iteration_bf16(X, coeffs, prescale=prescale, eps=1e-7, rounding="triton")
-    assert rel_fro(got, tri) <= TRITON_TOL, f"vs triton rounding {rel_fro(got, tri):.3e}"
+    # the two rounding schemes drift apart on short, wide inputs (up to 0.5 for one row of
+    # 5000 at 3 Polar Express steps): allow what separates the fused-bf16 oracle from it
+    tbound = max(TRITON_TOL, FP64_SLACK * rel_fro(ref, tri) + 2e-3)
+    assert rel_fro(got, tri) <= tbound, f"vs triton rounding {rel_fro(got, tri):.3e} > {tbound:.3e}"
 
 
 @pytest.mark.parametrize("strategy", STRATS)
