@@ -85,7 +85,10 @@ MUON_DEVICE void short_write_partial(const ShortArgs& a, float* red, const f32x1
 // columns 64 w .. +63 of every panel of the range; lane l loads rows l % 32 and
 // l % 32 + 32, elements 32 (l / 32) .. +31 of those 64 columns, and its four 16-byte
 // pieces per row are directly the MFMA fragments of both operands: a Gram sum may
-// take its k in any order as long as both operands use the same one.
+// take its k in any order as long as both operands use the same one. One load
+// instruction covers 32 bytes of each of 32 rows, so the loads are ordinary (cached):
+// the four instructions that complete a 128-byte line then hit it in L2 (measured with
+// non-temporal loads instead: 3.7 TB/s against 6.0 TB/s).
 __global__ __launch_bounds__(256) void short_gram_kernel(ShortArgs a) {
   __shared__ __align__(16) float red[4 * SG_PART];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -101,8 +104,8 @@ __global__ __launch_bounds__(256) void short_gram_kernel(ShortArgs a) {
     const int64_t o = (int64_t)pn * SG_PANEL;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      f0[q] = ld_nt(x0 + o + 8 * q);
-      f1[q] = ld_nt(x1 + o + 8 * q);
+      f0[q] = *(const uint4*)(x0 + o + 8 * q);
+      f1[q] = *(const uint4*)(x1 + o + 8 * q);
     }
   };
   if (pb < pe) load(pb);
