@@ -408,8 +408,8 @@ MUON_DEVICE float apply_elem(float p, float u, float wd, int cautious, float adj
 
 // TRANS: U is the wide-orientation iterate of a tall matrix, U(r, c) = u[c][r] (the
 // workspace after the iteration); the 64 x 64 block u[c0 .. c0+63][r0 .. r0+63] is read
-// with coalesced 16-byte loads and transposed through LDS. Its extents are padded to the
-// 256-element tile, so the block is in bounds.
+// with coalesced 16-byte loads and transposed through LDS. Its extents are padded to a
+// multiple of 64, so the block is in bounds.
 // ROWSCALE (NorMuon): u is first multiplied by its row's scale and the result is an fp32
 // tensor, so the apply runs in fp32 whatever U's storage dtype (normuon.py:44-55, 125-134).
 template <int PDT, int UDT, int VEC, bool TRANS, bool ROWSCALE>
@@ -489,8 +489,9 @@ __global__ __launch_bounds__(256) void postpass_kernel(PostArgs a) {
 
 // The post-pass over a 64-row x 256-column slab of stored elements per workgroup (four
 // tiles side by side), loads first and non-temporal access, as prepass_slab_kernel.
-// TRANS (a tall result in the workspace, bf16): the 256 x 64 block of the wide iterate that
-// holds the slab's transpose is read with coalesced 128-byte rows into LDS first.
+// TRANS (a tall result in the workspace, bf16): the rows of the wide iterate that hold the
+// slab's valid columns (at most 256 x 64) are read with coalesced 128-byte rows into LDS
+// first. Only rows below `cols` are read: the iterate may have as few as 64 rows.
 template <int PDT, int UDT, bool TRANS, bool ROWSCALE>
 __global__ __launch_bounds__(256) void postpass_slab_kernel(PostArgs a) {
 #pragma clang fp contract(off)
@@ -514,6 +515,7 @@ __global__ __launch_bounds__(256) void postpass_slab_kernel(PostArgs a) {
     for (int it = 0; it < (SLAB_C * TILE / 8) / 256; ++it) {
       const int id = it * 256 + tid;
       const int cc = id >> 3, rr = (id & 7) * 8;
+      if (c0 + cc >= a.cols) continue;
       const uint4 w = ld_nt((const uint16_t*)a.u + (int64_t)mat * a.u_mstride +
                             (c0 + cc) * a.u_pitch + r0 + rr);
       const uint32_t q[4] = {w.x, w.y, w.z, w.w};
