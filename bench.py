@@ -182,9 +182,10 @@ def _measured_traffic(kernel: str, config: str, lp):
     """HBM bytes per dispatch of `kernel` from the committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE, each scaled by a 1 GiB copy), for the workload it was
     measured on; None elsewhere."""
-    if config != "llama" or lp:
+    files = {"llama": "muon_step_llama3_8b_traffic.json", "moe_flat": "muon_step_moe_flat_traffic.json"}
+    if config not in files or lp:
         return None, None
-    path = os.path.join(ROOT, "profiles", "muon_step_llama3_8b_traffic.json")
+    path = os.path.join(ROOT, "profiles", files[config])
     try:
         with open(path) as f:
             data = json.load(f)
@@ -319,6 +320,7 @@ def main() -> None:
         bx_bytes = sum(5 * 4 * (math.prod(s[:-2]) if len(s) > 2 else 1) * min(s[-2:]) * max(s[-2:])
                        for s in orth_shapes) * args.steps / max(gn, 1)
         achieved = bx_bytes / (avg_ms * 1e-3) / 1e9
+        traffic, traffic_src = _measured_traffic("short_bx_kernel", args.config, args.lp)
         roofline = {
             "bound": "hbm",
             "kernel": "short_bx_kernel (X' = a X + B X, 64-row iterate)",
@@ -326,7 +328,8 @@ def main() -> None:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "avg_launch_ms": round(avg_ms, 4),
             "bytes_per_launch": bx_bytes,
         }
