@@ -64,7 +64,8 @@ def test_qmap_matches_oracle():
 
 @pytest.mark.parametrize("fmt,cls", FORMATS)
 @pytest.mark.parametrize("nesterov,maximize", [(True, False), (False, False), (True, True)])
-@pytest.mark.parametrize("shape", [(128, 96), (96, 128)])  # tall and wide workspace paths
+# tall and wide workspace paths; at most 64 rows on the short side: the 64-row iterate
+@pytest.mark.parametrize("shape", [(128, 96), (96, 128), (512, 48), (48, 512)])
 def test_lp_prepass_codes_bit_exact_and_step(fmt, cls, nesterov, maximize, shape):
     opt_cls = {"8bit": Muon8bit, "4bit": Muon4bit, "fp8": MuonFp8}[fmt]
     block = 256

@@ -64,8 +64,10 @@ def _run(shapes, dtype, foreach, beta2=0.9, steps=2, seed=11, split_sizes=None):
 @pytest.mark.parametrize(
     "shapes,dtype",
     [([(300, 130)] * 3, torch.bfloat16), ([(2, 70, 200)] * 2, torch.float32),
-     ([(64, 512)], torch.float32), ([(520, 260)] * 2, torch.float32)],
-    ids=["tall-bf16-x3", "stacked-fp32-x2", "wide-fp32", "tall-fp32-x2"],
+     ([(64, 512)], torch.float32), ([(520, 260)] * 2, torch.float32),
+     ([(512, 48)] * 2, torch.bfloat16), ([(40, 768)], torch.float32)],
+    ids=["tall-bf16-x3", "stacked-fp32-x2", "wide-fp32", "tall-fp32-x2",
+         "short-tall-bf16-x2", "short-wide-fp32"],
 )
 def test_normuon_matches_oracle_buckets(shapes, dtype, foreach):
     opt, params, p0, ref_p, ref_v = _run(shapes, dtype, foreach)
