@@ -350,6 +350,9 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
     }
     return MUON_OK;
   }
+  // A A and B X contract over the m valid rows of X (the rest of the padding is zero):
+  // the bf16 kernels take K in whole pairs of 64-wide K-tiles
+  const int64_t kq = ws_dtype == MUON_DT_BF16 ? std::min(mp, round_up(L.m, 128)) : mp;
   for (int it = 0; it < steps; ++it) {
     const float a = (float)coeffs[3 * it], b = (float)coeffs[3 * it + 1],
                 c = (float)coeffs[3 * it + 2];
@@ -367,7 +370,7 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
     // B = b*A + c*(A A)
     {
     Timed t(MUON_K_SYRK_AA, bm * md * (md + 1) * md, s);
-    rc = muon_launch_gemm(ws_dtype, MODE_SYRK, false, batch, mp, mp, mp, A, mp, mp * mp, A, mp,
+    rc = muon_launch_gemm(ws_dtype, MODE_SYRK, false, batch, mp, mp, kq, A, mp, mp * mp, A, mp,
                           mp * mp, A, mp, mp * mp, B, mp, mp * mp, nullptr, 0, 0, L.m, L.m, c, b,
                           nullptr, 0, s);
     }
@@ -376,7 +379,7 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
     // result stays in the wide orientation (readers of a tall result transpose on load)
     {
     Timed t(MUON_K_GEMM_BX, bm * 2.0 * md * md * nd, s);
-    rc = muon_launch_gemm(ws_dtype, MODE_GEMM, false, batch, mp, np, mp, B, mp, mp * mp, Xc, np,
+    rc = muon_launch_gemm(ws_dtype, MODE_GEMM, false, batch, mp, np, kq, B, mp, mp * mp, Xc, np,
                           mp * np, Xc, np, mp * np, Xn, np, mp * np, nullptr, 0, 0, L.m, L.n,
                           1.0f, a, scale, first ? 1 : 0, s);
     }

@@ -1017,7 +1017,9 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn4_kernel(GemmArgs g) {
     for (int f = 0; f < 4; ++f) xa[f] = lds0 + st * NN_STAGEB + xoff[f];
   };
   const uint32_t m0w = lds0 + wave * 1024;
-  const int KT = (int)(g.K / V2_BK);  // a multiple of 4 (K is padded to 256)
+  // even: the last two K-tiles of a tile prefetch the next tile's first two into stages
+  // (KT - 2) & 1 and (KT - 1) & 1, and every tile starts reading stage 0
+  const int KT = (int)(g.K / V2_BK);
 
   // current tile and its descriptors; the next tile's (num_records 0 if none)
   int bidx;
@@ -1313,8 +1315,8 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
         muon_set_error("gemm: alpha must be nonzero");
         return MUON_ERR_ARG;
       }
-      if (out_t != nullptr || K % 256 != 0) {
-        muon_set_error("gemm: bf16 NN products take K a multiple of 256 and no transposed output");
+      if (out_t != nullptr || K % 128 != 0) {
+        muon_set_error("gemm: bf16 NN products take K a multiple of 128 and no transposed output");
         return MUON_ERR_ARG;
       }
       // persistent: one workgroup per CU walks the tile list
