@@ -9,6 +9,7 @@ driver — there is no tracing compiler on this path.
 
 from __future__ import annotations
 
+import contextlib
 import functools
 import math
 from typing import cast
@@ -55,6 +56,50 @@ def _group_muon_tensors(
                 )
             )
     return buckets
+
+
+_MAX_SIDE_STREAMS = 4  # GPU_MAX_HW_QUEUES is 4 by default: one hardware queue each
+_side_streams: dict[tuple[int, int], torch.cuda.Stream] = {}
+
+
+def _side_stream(device: torch.device, slot: int) -> torch.cuda.Stream:
+    """Side stream `slot` of `device` (default priority), created once per process."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, slot)
+    stream = _side_streams.get(key)
+    if stream is None:
+        stream = _side_streams[key] = torch.cuda.Stream(device=index)
+    return stream
+
+
+def _concurrent_slots(buckets, algorithm: MuonAlgorithm, batch_size: int | None) -> dict[int, int]:
+    """Side-stream slot per bucket index for buckets too small to fill the device.
+
+    A bucket whose Gram products (upper-triangle 256-row tiles x matrices) launch fewer
+    workgroups than the device has compute units leaves most of it idle (the GPT-2 set:
+    72 workgroups per product on 256 CUs); such buckets run concurrently, one stream per
+    workspace shape, since buckets of one padded shape share the library's workspace.
+    Large buckets stay on the current stream. Built-in algorithms only."""
+    if not type(algorithm).__module__.startswith("muonium_amd."):
+        return {}
+    from muonium_amd import _ops
+
+    cus: dict[torch.device, int] = {}
+    small: dict[int, tuple] = {}
+    for bi, (device, _, dev_g, _, _) in enumerate(buckets):
+        if device.type != "cuda" or dev_g[0].dim() < 2:
+            continue
+        if device not in cus:
+            cus[device] = torch.cuda.get_device_properties(device).multi_processor_count
+        rows, cols = dev_g[0].shape[-2:]
+        nmat = math.prod(dev_g[0].shape[:-2]) * min(len(dev_g), batch_size or len(dev_g))
+        tiles = -(-min(rows, cols) // 256)
+        if tiles * (tiles + 1) // 2 * nmat < cus[device]:
+            small[bi] = (device, _ops._padded_extents(torch.bfloat16, rows, cols))
+    if len(small) < 2:
+        return {}
+    keys: dict[tuple, int] = {}
+    return {bi: keys.setdefault(key, len(keys)) % _MAX_SIDE_STREAMS for bi, key in small.items()}
 
 
 class Muon(torch.optim.Optimizer):
@@ -395,53 +440,71 @@ class Muon(torch.optim.Optimizer):
                 algorithm.update(param, grad, {k: b[i] for k, b in state.items()}, lr_ratio, **hp)
             return
 
-        for device, dev_p, dev_g, dev_state, dev_lr in _group_muon_tensors(
-            params, grads, state, lr_ratios
-        ):
-            idx = list(range(len(dev_g)))
-            if self.batch_size and len(idx) > self.batch_size:
-                batches = [idx[i : i + self.batch_size] for i in range(0, len(idx), self.batch_size)]
+        buckets = _group_muon_tensors(params, grads, state, lr_ratios)
+        slots = _concurrent_slots(buckets, algorithm, self.batch_size)
+        forked: dict[tuple[torch.device, int], torch.cuda.Stream] = {}
+        for bi, (device, dev_p, dev_g, dev_state, dev_lr) in enumerate(buckets):
+            if bi in slots:
+                side = _side_stream(device, slots[bi])
+                if (device, slots[bi]) not in forked:
+                    side.wait_stream(torch.cuda.current_stream(device))
+                    forked[(device, slots[bi])] = side
+                ctx = torch.cuda.stream(side)
             else:
-                batches = [idx]
-            if device.type != "cuda":
-                host = [
-                    ([dev_p[i] for i in sel], [dev_g[i] for i in sel],
-                     {k: [v[i] for i in sel] for k, v in dev_state.items()},
-                     [dev_lr[i] for i in sel])
-                    for sel in batches
-                ]
-                if torch.cuda.is_available() and all(pipeline_supported(b) for b in host):
-                    # pinned-memory round trip, copies overlapped with the updates
-                    run_offloaded(
-                        host,
-                        lambda p, g, st, lr: algorithm.foreach_update(p, g, st, lr, **hp),
-                        # the built-in algorithms rewrite the grads only under Nesterov
-                        # without maximize (muon.py:117-118); copy them back for any other
-                        grads_modified=(nesterov and not maximize)
-                        or not type(algorithm).__module__.startswith("muonium_amd."),
-                    )
-                    continue
-            for sel in batches:
-                p_orig = [dev_p[i] for i in sel]
-                g_orig = [dev_g[i] for i in sel]
-                s_orig = {k: [v[i] for i in sel] for k, v in dev_state.items()}
-                lr_orig = [dev_lr[i] for i in sel]
-                cuda = torch.device("cuda")
-                p_b = move_tensors_to_device(p_orig, device, cuda)
-                g_b = move_tensors_to_device(g_orig, device, cuda)
-                s_b = {k: move_tensors_to_device(v, device, cuda) for k, v in s_orig.items()}
-                lr_b = move_tensors_to_device(lr_orig, device, cuda)
-                algorithm.foreach_update(
-                    cast(list[Tensor], p_b), cast(list[Tensor], g_b), cast(dict, s_b),
-                    cast(list[Tensor], lr_b), **hp,
+                ctx = contextlib.nullcontext()
+            with ctx:
+                self._muon_bucket(algorithm, hp, nesterov, maximize, device, dev_p, dev_g,
+                                  dev_state, dev_lr)
+        for (device, _), side in forked.items():
+            torch.cuda.current_stream(device).wait_stream(side)
+
+    def _muon_bucket(self, algorithm, hp, nesterov, maximize, device, dev_p, dev_g, dev_state,
+                     dev_lr) -> None:
+        """One (device, dtype, shape) bucket of the foreach driver, chunked by batch_size."""
+        idx = list(range(len(dev_g)))
+        if self.batch_size and len(idx) > self.batch_size:
+            batches = [idx[i : i + self.batch_size] for i in range(0, len(idx), self.batch_size)]
+        else:
+            batches = [idx]
+        if device.type != "cuda":
+            host = [
+                ([dev_p[i] for i in sel], [dev_g[i] for i in sel],
+                 {k: [v[i] for i in sel] for k, v in dev_state.items()},
+                 [dev_lr[i] for i in sel])
+                for sel in batches
+            ]
+            if torch.cuda.is_available() and all(pipeline_supported(b) for b in host):
+                # pinned-memory round trip, copies overlapped with the updates
+                run_offloaded(
+                    host,
+                    lambda p, g, st, lr: algorithm.foreach_update(p, g, st, lr, **hp),
+                    # the built-in algorithms rewrite the grads only under Nesterov
+                    # without maximize (muon.py:117-118); copy them back for any other
+                    grads_modified=(nesterov and not maximize)
+                    or not type(algorithm).__module__.startswith("muonium_amd."),
                 )
-                pairs = [(p_orig, p_b), (g_orig, g_b), (lr_orig, lr_b)]
-                pairs.extend((s_orig[k], s_b[k]) for k in s_orig)
-                for originals, moved in pairs:
-                    if originals is not moved:
-                        for o, v in zip(originals, moved, strict=True):
-                            if o is not None and v is not None:
-                                o.copy_(v.to(o.device))
+                return
+        for sel in batches:
+            p_orig = [dev_p[i] for i in sel]
+            g_orig = [dev_g[i] for i in sel]
+            s_orig = {k: [v[i] for i in sel] for k, v in dev_state.items()}
+            lr_orig = [dev_lr[i] for i in sel]
+            cuda = torch.device("cuda")
+            p_b = move_tensors_to_device(p_orig, device, cuda)
+            g_b = move_tensors_to_device(g_orig, device, cuda)
+            s_b = {k: move_tensors_to_device(v, device, cuda) for k, v in s_orig.items()}
+            lr_b = move_tensors_to_device(lr_orig, device, cuda)
+            algorithm.foreach_update(
+                cast(list[Tensor], p_b), cast(list[Tensor], g_b), cast(dict, s_b),
+                cast(list[Tensor], lr_b), **hp,
+            )
+            pairs = [(p_orig, p_b), (g_orig, g_b), (lr_orig, lr_b)]
+            pairs.extend((s_orig[k], s_b[k]) for k in s_orig)
+            for originals, moved in pairs:
+                if originals is not moved:
+                    for o, v in zip(originals, moved, strict=True):
+                        if o is not None and v is not None:
+                            o.copy_(v.to(o.device))
 
     def _step_muon_group(self, group: dict) -> None:
         """optim.py:597-640."""

@@ -488,3 +488,36 @@ def test_plumbing_config_is_bit_repeatable():
     assert torch.equal(outs[0][0], outs[1][0])
     assert torch.equal(outs[0][1], outs[1][1])
     assert not torch.equal(outs[0][0], p0)
+
+
+def test_small_buckets_on_side_streams_match_sequential_buckets():
+    """Buckets too small to fill the device run concurrently on side streams (one per
+    workspace shape); the result is the same, bit for bit, as one bucket at a time, and
+    the step is ordered after earlier work on the caller's stream and before later work."""
+    from muonium_amd.optim import optim as optim_mod
+
+    # workspace shapes (m_pad, n_pad): (256, 512), (256, 256), (256, 768) twice, (256, 512)
+    shapes = [(96, 288), (96, 96), (96, 600), (600, 96), (96, 288)]
+    gen = torch.Generator().manual_seed(31)
+    p0 = [torch.randn(s, generator=gen).bfloat16() for s in shapes]
+    gs = [[torch.randn(s, generator=gen).bfloat16() for s in shapes] for _ in range(2)]
+    runs = []
+    for split_groups in (False, True):
+        params = [nn.Parameter(p.clone().to(DEV)) for p in p0]
+        groups = [{"params": [p]} for p in params] if split_groups else [{"params": params}]
+        opt = Muon(groups, lr=0.05, wd=0.1, momentum=0.9, foreach=True)
+        optim_mod._side_streams.clear()
+        for step in range(2):
+            for p, g in zip(params, gs[step]):
+                # written on the caller's stream right before the step
+                p.grad = torch.empty_like(p).copy_(g.to(DEV))
+            opt.step()
+            if not split_groups:
+                assert len(optim_mod._side_streams) == 3
+            else:
+                assert len(optim_mod._side_streams) == 0
+        runs.append(([p.detach().clone() for p in params],
+                     [opt.state[p]["momentum_buffer"].clone() for p in params]))
+    (pa, ba), (pb, bb) = runs
+    for x, y in zip(pa + ba, pb + bb):
+        assert torch.equal(x, y)
