@@ -257,6 +257,9 @@ struct OrthLayout {
 constexpr int MUON_QTAB_SHIFT = 18;
 constexpr int MUON_QTAB_SIZE = 1 << (32 - MUON_QTAB_SHIFT);
 constexpr int MUON_QTHR_PAD = 4;
+// The last pad slot (never compared: lookups read thresholds 0 .. 257) holds 0 when no key
+// bucket holds more than two thresholds (every standard map), else 1.
+constexpr int MUON_QTHR_FLAG = 256 + MUON_QTHR_PAD - 1;
 constexpr int MUON_QTAB_BYTES = MUON_QTAB_SIZE + (256 + MUON_QTHR_PAD) * 4;
 
 OrthLayout muon_orth_layout(int dtype, int64_t batch, int64_t rows, int64_t cols);

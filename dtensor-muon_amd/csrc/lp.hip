@@ -268,6 +268,7 @@ template <int QF>
 __global__ __launch_bounds__(256) void build_qthr_kernel(const float* qmap, uint32_t* thr) {
   constexpr int NQ = QF == MUON_Q_8BIT ? 256 : 16;
   __shared__ float q[256];
+  __shared__ uint32_t ts[256];
   const int k = threadIdx.x;
   q[k] = qmap[k < NQ ? k : 0];
   __syncthreads();
@@ -283,8 +284,15 @@ __global__ __launch_bounds__(256) void build_qthr_kernel(const float* qmap, uint
     }
     t = lo;
   }
+  // the flag: three consecutive thresholds in one key bucket (sorted, so any bucket with
+  // more than two has such a triple)
+  ts[k] = t;
+  __syncthreads();
+  const int dense = k + 2 < NQ - 1 && (ts[k] >> MUON_QTAB_SHIFT) == (ts[k + 2] >> MUON_QTAB_SHIFT);
+  const int any_dense = __syncthreads_or(dense);
   thr[k] = t;
-  if (k < MUON_QTHR_PAD) thr[256 + k] = 0xffffffffu;
+  if (k < MUON_QTHR_PAD)
+    thr[256 + k] = 256 + k == MUON_QTHR_FLAG ? (any_dense ? 1u : 0u) : 0xffffffffu;
 }
 
 // qtab[b] = the number of thresholds <= b << SHIFT (the code of the smallest value of
@@ -311,11 +319,12 @@ __global__ __launch_bounds__(256) void build_qtab_kernel(const uint32_t* thr, in
 // `more` when the bucket holds more thresholds than that (then quant_code_thr_all gives
 // the code). A NaN y gets an in-range code here; the caller routes it to
 // quant_code_thr_all.
+template <bool CHECK_MORE>
 MUON_DEVICE int quant_code_thr(float y, const uint32_t* thr, const uint8_t* qtab, bool& more) {
   const uint32_t ky = f32_order_key(y);
   const int c0 = qtab[ky >> MUON_QTAB_SHIFT];
   const int c = c0 + (ky >= thr[c0] ? 1 : 0) + (ky >= thr[c0 + 1] ? 1 : 0);
-  more = more || ky >= thr[c0 + 2];
+  if (CHECK_MORE) more = more || ky >= thr[c0 + 2];
   return c;
 }
 
@@ -401,6 +410,7 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
   uint4 tq0 = {}, tq1 = {}, tq2 = {}, tq3 = {};
   float tqm = 0.0f;
   uint32_t tt0 = 0, tt1 = 0;
+  bool sparse_map = false;
   if (MAP) {
     static_assert(MUON_QTAB_SIZE == 4 * 256 * 16, "one 16-byte table piece per thread and step");
     const uint4* gt = (const uint4*)a.qtab + tid;
@@ -412,6 +422,7 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
     tq3 = gt[768];
     tt0 = gthr[tid];
     tt1 = gthr[256 + (tid & (MUON_QTHR_PAD - 1))];
+    sparse_map = gthr[MUON_QTHR_FLAG] == 0u;  // the same address for every thread
     __builtin_amdgcn_sched_barrier(0);
   }
   Raw8<GDT> graw[NP];
@@ -498,8 +509,14 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
         c8 = make_uint2(w0, w1);
       } else {
         bool more = false;
+        if (sparse_map) {
+          // no key bucket holds more than two thresholds: the third compare is never true
 #pragma unroll
-        for (int k = 0; k < 8; ++k) cq[k] = quant_code_thr(ys[k], qthr, qtab, more);
+          for (int k = 0; k < 8; ++k) cq[k] = quant_code_thr<false>(ys[k], qthr, qtab, more);
+        } else {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) cq[k] = quant_code_thr<true>(ys[k], qthr, qtab, more);
+        }
         // y is NaN only when the scale is NaN or infinite: those blocks take the full
         // count, which codes NaN as 0
         if (more || !(sc <= 3.40282347e38f)) {

@@ -326,3 +326,57 @@ def test_fp8_codes_exact_at_every_rounding_boundary():
     codes, scale = quant_ref.quantize(xb.reshape(-1), block, "fp8", None)
     assert np.all(scale == 1.0)
     assert np.array_equal(st.codes.cpu().numpy(), codes)
+
+
+@pytest.mark.parametrize("dense", [False, True], ids=["standard-map", "dense-map"])
+def test_lp_custom_map_codes_exact_and_flag(dense):
+    """A quantization map with 200 of its 256 entries inside one key bucket (key >> 18) has
+    more than two thresholds per bucket: the table flag marks it and the tiled pre-pass
+    takes the full threshold count for it. Codes and scales bit-exact against the oracle's
+    quantizer with the same map; the standard map keeps the flag clear."""
+    from muonium_amd import _lib
+
+    lib = _lib.load()
+    dev = torch.device(DEV)
+    _lib.ensure_device(dev)
+    if dense:
+        qmap = np.unique(np.concatenate([np.linspace(-1.0, 1.0, 56, dtype=np.float32),
+                                         np.float32(0.5) + np.arange(200, dtype=np.float32) * np.float32(4e-7)]))
+        assert qmap.size == 256
+    else:
+        qmap = quant_ref.qmap_8bit(True)
+    qmap = qmap.astype(np.float32)
+    rows, cols, block = 256, 512, 256
+    gen = torch.Generator().manual_seed(9)
+    # fp32 gradients with a block maximum of 1 and every third value within 1e-4 of 0.5, so
+    # y = m / scale falls among the clustered entries
+    g = (0.25 * torch.randn(rows, cols, generator=gen)).clamp(-0.9, 0.9)
+    g[:, 1::3] = 0.5 + 2e-5 * torch.randn(rows, (cols + 1) // 3, generator=gen)
+    g[:, 0] = 1.0
+    g[:, block] = 1.0
+    codes_d = torch.zeros(rows * cols, dtype=torch.uint8, device=dev)
+    scales_d = torch.zeros(rows * cols // block, dtype=torch.float32, device=dev)
+    qmap_d = torch.from_numpy(qmap).to(dev)
+    nbytes = lib.muon_orth_workspace_bytes(_lib.DT_BF16, 1, rows, cols)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    gd = g.to(dev)
+    codes = np.zeros(rows * cols, np.uint8)
+    scales = np.zeros(rows * cols // block, np.float32)
+    for step in range(2):
+        rc = lib.muon_lp_prepass(1, _lib.ptr_array([gd]), _lib.DT_F32, _lib.ptr_array([codes_d]),
+                                 _lib.ptr_array([scales_d]), qmap_d.data_ptr(), 8, block, 1, rows,
+                                 cols, 0.9, 1, 0, ws.data_ptr(), _lib.DT_BF16, 1, _lib.stream(dev))
+        assert rc == 0, _lib.last_error()
+        torch.cuda.synchronize()
+        codes, scales, _ = quant_ref.lp_momentum_step(
+            codes, scales, g.numpy(), block=block, fmt="8bit", qmap=qmap, momentum=0.9,
+            nesterov=True, maximize=False)
+        assert np.array_equal(codes_d.cpu().numpy(), codes), f"codes differ at step {step}"
+        assert np.array_equal(scales_d.cpu().numpy().view(np.uint32), scales.view(np.uint32))
+    # flag word: last threshold pad slot, after the 16 KB bucket table in the qtab region
+    rup = lambda v: -(-v // 256) * 256
+    x, a = 256 * 512 * 2, 256 * 256 * 2
+    off_qtab = 2 * rup(x) + 2 * rup(a) + rup((256 // 64) * (512 // 64) * 4) + rup(4)
+    thr = ws[off_qtab + 16384: off_qtab + 16384 + 260 * 4].cpu().view(torch.int32).numpy().view(np.uint32)
+    assert thr[259] == (1 if dense else 0)
+    assert thr[256] == 0xFFFFFFFF and thr[257] == 0xFFFFFFFF
