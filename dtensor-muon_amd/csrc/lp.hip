@@ -366,6 +366,7 @@ MUON_DEVICE uint32_t group_max_u32(uint32_t v, int lanes) {
   return v;
 }
 typedef __attribute__((ext_vector_type(2))) __bf16 bf2v;
+typedef __attribute__((ext_vector_type(4))) short lp_i16x4;
 
 template <int GDT, int QF, bool TALL>
 __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
@@ -556,16 +557,22 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
         constexpr int SEGS = TROWS / 8;  // 16-byte pieces per X0 row
         const int p0 = (p + 1) * 8 - TROWS;
         lds_sync();
+        // ds_read_b64_tr_b16: within 16 lanes, lane i points at 4 elements of row kb + i/4,
+        // columns jb + 4 (i % 4) .. +3, and receives column jb + i of rows kb .. kb+3; two
+        // such reads give the 8 rows of one X0 piece. Round `it`: column group
+        // 4 wave + it % 4, lane group gg takes rows 32 (it / 4) + 8 gg, so the four lane
+        // groups write 64 contiguous bytes of each X0 row.
+        const int tl = tid & 63, gg = tl >> 4, ti = tl & 15;
 #pragma unroll
         for (int it = 0; it < (LPT_COLS * SEGS) / 256; ++it) {
-          const int id = it * 256 + tid;
-          const int cc = id / SEGS, rr = (id % SEGS) * 8;
-          uint16_t ev[8];
-#pragma unroll
-          for (int k = 0; k < 8; ++k) ev[k] = tileT[rr + k][cc];
-          uint4 w;
-          __builtin_memcpy(&w, ev, 16);
-          *(uint4*)(x0 + (c0 + cc) * a.x_pitch + r0 + p0 + rr) = w;
+          const int jb = 16 * (4 * (tid >> 6) + (it & 3));
+          const int rr = 32 * (it >> 2) + 8 * gg;
+          const lp_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) lp_i16x4*)&tileT[rr + (ti >> 2)][jb + 4 * (ti & 3)]);
+          const lp_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) lp_i16x4*)&tileT[rr + 4 + (ti >> 2)][jb + 4 * (ti & 3)]);
+          const uint4 w = __builtin_bit_cast(uint4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+          *(uint4*)(x0 + (c0 + jb + ti) * a.x_pitch + r0 + p0 + rr) = w;
         }
         if (p != NP - 1) lds_sync();  // the next rows reuse the tile
       }
