@@ -178,8 +178,9 @@ __global__ __launch_bounds__(1024) void short_poly_kernel(ShortArgs a) {
   uint16_t o[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
+    // c = 0 (a custom Newton-Schulz table): B = b A, as the tiled path computes it
     const float rv = ratio * G[i][j0 + q];
-    o[q] = f32_to_bf16(a.pa * (acc[q] + rv));
+    o[q] = f32_to_bf16(a.pa != 0.0f ? a.pa * (acc[q] + rv) : a.pb * G[i][j0 + q]);
   }
   uint2 w;
   w.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);

@@ -155,3 +155,14 @@ def test_strategy_validation_and_dispatch_table():
 def test_empty_batch_is_passthrough():
     X = torch.randn(0, 256, 128, device="cuda", dtype=torch.bfloat16)
     assert pe_loop(X, 5).shape == X.shape
+
+
+@pytest.mark.parametrize("shape", [(48, 1000), (200, 700), (700, 200)])
+def test_newton_schulz_custom_coefficients_without_quintic_term(shape):
+    """ns_loop with c = 0 (B = b A): the short (at most 64 rows) and the tiled iterations
+    both compute B = bf16(b A), within the bf16 bar of the oracle."""
+    X = _inputs(shape, seed=7)
+    got = ns_loop(X.bfloat16().cuda(), 3, a=2.0, b=-1.5, c=0.0, eps=1e-7).cpu()
+    ref = muon_ref.polar_iteration_bf16(X, [(2.0, -1.5, 0.0)] * 3, prescale=1.0, eps=1e-7)
+    assert torch.isfinite(got.float()).all()
+    assert rel_fro(got, ref) <= BF16_TOL, f"{rel_fro(got, ref):.3e}"
