@@ -54,6 +54,7 @@ int muon_launch_lp_prepass(int ntensors, void* const* grads, int gdt, void* cons
                            int nesterov, int maximize, void* direct, int64_t d_pitch,
                            int64_t d_mstride, hipStream_t s);
 int64_t muon_short_parts(int64_t n_pad);
+int muon_launch_zero(void* dst, int64_t bytes, hipStream_t s);
 int muon_launch_short_gram(const OrthLayout& L, const void* x, float* part, int64_t batch,
                            hipStream_t s);
 int muon_launch_short_poly(const OrthLayout& L, float* part, void* bm, int64_t batch, float pa,
@@ -209,7 +210,10 @@ int muon_gram(const void* x, void* y, int dtype, int64_t batch, int64_t M, int64
     return MUON_ERR_SHAPE;
   }
   if (batch == 0 || M == 0) return MUON_OK;
-  return muon_launch_gemm(dtype, MODE_SYRK, true, batch, M, M, std::max<int64_t>(K, 1), x, K,
+  if (K == 0)  // an empty contraction: y = 0 (x is never read)
+    return muon_launch_zero(y, batch * M * M * (dtype == MUON_DT_F32 ? 4 : 2),
+                            (hipStream_t)stream);
+  return muon_launch_gemm(dtype, MODE_SYRK, true, batch, M, M, K, x, K,
                           M * K, x, K, M * K, nullptr, 0, 0, y, M, M * M, nullptr, 0, 0, M, M,
                           1.0f, 0.0f, nullptr, 0, (hipStream_t)stream);
 }

@@ -1104,3 +1104,28 @@ int muon_launch_normuon_stats(int ntensors, void* const* vars, int vdt, const vo
   MUON_CHECK_LAUNCH("normuon_stats");
   return MUON_OK;
 }
+
+// ---- zero fill ---------------------------------------------------------------------
+// A kernel rather than hipMemsetAsync, so that a caller may capture it in a HIP graph.
+// 2-byte stores: every dtype of the library is 2 or 4 bytes wide and aligned to its size.
+namespace {
+__global__ __launch_bounds__(256) void zero_fill_kernel(uint16_t* dst, int64_t halves) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < halves; i += stride)
+    dst[i] = 0;
+}
+}  // namespace
+
+int muon_launch_zero(void* dst, int64_t bytes, hipStream_t s) {
+  if (bytes <= 0) return MUON_OK;
+  if (bytes % 2 || ((uintptr_t)dst & 1)) {
+    muon_set_error("zero_fill: %lld bytes at %p are not whole 2-byte elements", (long long)bytes,
+                   dst);
+    return MUON_ERR_ALIGN;
+  }
+  const int64_t halves = bytes / 2;
+  dim3 grid((unsigned)std::min<int64_t>((halves + 255) / 256, 4096));
+  hipLaunchKernelGGL(zero_fill_kernel, grid, dim3(256), 0, s, (uint16_t*)dst, halves);
+  MUON_CHECK_LAUNCH("zero_fill");
+  return MUON_OK;
+}

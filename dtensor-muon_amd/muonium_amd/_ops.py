@@ -20,7 +20,12 @@ from torch import Tensor
 from . import _lib
 
 # ---------------------------------------------------------------------------------
-# workspace cache: one growable buffer per (device, iteration dtype, padded m, n)
+# workspace cache: one growable buffer per (device, stream, iteration dtype, padded m, n)
+#
+# A buffer is only ever used on the stream that allocated it. Buckets running on
+# different streams (the foreach driver's side streams) therefore never share one,
+# and a capacity regrow frees the old buffer on the only stream that used it, which
+# the caching allocator orders behind that stream's earlier launches.
 
 _ws_lock = threading.Lock()
 _ws_cache: dict[tuple, tuple[int, Tensor]] = {}
@@ -42,10 +47,11 @@ def workspace(device: torch.device, dtype: torch.dtype, batch: int, rows: int, c
     """(buffer, capacity) with room for ``batch`` matrices of rows x cols.
 
     The layout only depends on the padded (min, max) extents and the capacity, so
-    tall and wide matrices of the same extents share a buffer. Contents need no
-    initialization (every launch rewrites what it reads later)."""
+    tall and wide matrices of the same extents share a buffer, on the current stream
+    of ``device`` only. Contents need no initialization (every launch rewrites what
+    it reads later)."""
     m, n = _padded_extents(dtype, rows, cols)
-    key = (device, dtype, m, n)
+    key = (device, torch.cuda.current_stream(device).cuda_stream, dtype, m, n)
     with _ws_lock:
         hit = _ws_cache.get(key)
         if hit is not None and hit[0] >= batch:

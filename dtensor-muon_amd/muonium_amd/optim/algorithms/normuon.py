@@ -2,8 +2,7 @@
 
 Mirrors muonium/optim/algorithms/normuon.py:16-203. Momentum, orthogonalization, the
 per-row normalization of the orthogonalized update and the weight-decay/apply pass all
-run on the MI355X kernels (``muon_normuon_postpass``). ``_normuon_normalize`` keeps the
-reference's torch formulation for callers that normalize a tensor by hand.
+run on the MI355X kernels (``muon_normuon_postpass``).
 """
 
 from __future__ import annotations
@@ -21,34 +20,21 @@ from .base import (
     orthogonalize_single,
     register_muon_algorithm,
 )
-from .muon import _Contig, fused_orth_available, is_quantized, momentum_seam, schedule
-
-
-def _normuon_normalize(
-    u: Tensor, v: Tensor, muon_beta2: float, split_sizes: tuple[int, ...] | None = None
-) -> tuple[Tensor, Tensor]:
-    """Per-row second-moment EMA v' = lerp(v, mean_row(u^2), 1 - beta2), u / (sqrt(v')
-    + 1e-8), rescaled to u's Frobenius norm; per row block with split_sizes
-    (normuon.py:16-55)."""
-    if split_sizes is not None:
-        parts = [
-            _normuon_normalize(ub, vb, muon_beta2)
-            for ub, vb in zip(
-                u.split(list(split_sizes), dim=-2), v.split(list(split_sizes), dim=-2), strict=True
-            )
-        ]
-        return torch.cat([p[0] for p in parts], dim=-2), torch.cat([p[1] for p in parts], dim=-2)
-    u = u.to(v.dtype)
-    norm_u = u.norm(p=2, dim=(-2, -1), keepdim=True)
-    v_new = torch.lerp(v, (u * u).mean(dim=-1, keepdim=True), 1 - muon_beta2)
-    u = u / (v_new.sqrt() + 1e-8)
-    norm_u_new = u.norm(p=2, dim=(-2, -1), keepdim=True).clamp(min=1e-8)
-    return u * (norm_u / norm_u_new), v_new
+from .muon import _Contig, _offloaded, fused_orth_available, is_quantized, momentum_seam, schedule
 
 
 def _normuon_step(params, grads, bufs, variances, lr_ratios, *, lr, weight_decay, cautious_wd,
                   momentum, nesterov, maximize, ns_steps, orthogonalization_strategy,
                   split_sizes, muon_beta2, batched):
+    if not params[0].is_cuda:
+        # host-resident tensors (the per-parameter driver's default for them): run on
+        # device copies and copy every result back
+        return _offloaded(_normuon_step, params, grads, bufs, variances, lr_ratios, lr=lr,
+                          weight_decay=weight_decay, cautious_wd=cautious_wd,
+                          momentum=momentum, nesterov=nesterov, maximize=maximize,
+                          ns_steps=ns_steps,
+                          orthogonalization_strategy=orthogonalization_strategy,
+                          split_sizes=split_sizes, muon_beta2=muon_beta2, batched=batched)
     lrs = _ops.adjusted_lrs(lr_ratios, lr)
     coeffs, prescale = schedule(orthogonalization_strategy, ns_steps)
     quantized = is_quantized(bufs[0])

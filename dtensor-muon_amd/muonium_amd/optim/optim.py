@@ -78,8 +78,10 @@ def _concurrent_slots(buckets, algorithm: MuonAlgorithm, batch_size: int | None)
     A bucket whose Gram products (upper-triangle 256-row tiles x matrices) launch fewer
     workgroups than the device has compute units leaves most of it idle (the GPT-2 set:
     72 workgroups per product on 256 CUs); such buckets run concurrently, one stream per
-    workspace shape, since buckets of one padded shape share the library's workspace.
-    Large buckets stay on the current stream. Built-in algorithms only."""
+    padded workspace shape, so each side stream holds at most one workspace per shape
+    (workspaces are cached per stream: a side stream never touches the buffer of the
+    current stream or of another side stream). Large buckets stay on the current
+    stream. Built-in algorithms only."""
     if not type(algorithm).__module__.startswith("muonium_amd."):
         return {}
     from muonium_amd import _ops

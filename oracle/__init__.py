@@ -18,9 +18,12 @@ Pinning status (what fixes each function independently of its own formula):
   expansion with overridden coefficients, transpose symmetry, zero/rank-1 inputs,
   orthogonal fixed point, scale invariance, batched == unbatched) and the fp64 run of
   the same iteration.
-* ``muon_ref.muon_update`` / ``muon_foreach_update`` / ``normuon_*`` /
-  ``split_*``: the closed-form known answers of the reference tests
-  (test_optim.py:392-584, test_algorithms.py:174-393).
+* ``muon_ref.muon_update`` / ``split_*``: the closed-form known answers of the
+  reference tests (test_optim.py:392-584, test_algorithms.py:315-393).
+* ``muon_ref.normuon_normalize`` / ``normuon_update``: invariants of the method
+  (Frobenius norm preserved, equal row norms from a zero variance, the EMA's fixed
+  point, the same per split_sizes row block) and the known answers of
+  test_algorithms.py:174-259.
 * ``quant_ref``: the quantized-state arithmetic lives in torchao 0.17.0, which is not
   present here; the restatement follows torchao's published algorithm and is pinned
   by brute-force nearest-code search, map structure, round-trip error bounds and

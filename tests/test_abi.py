@@ -97,6 +97,8 @@ def test_result_location_follows_orientation():
     [
         (lambda L: L.muon_gram(None, None, 9, 1, 4, 4, None), 2),
         (lambda L: L.muon_gram(None, None, 1, -1, 4, 4, None), 1),
+        # K == 0 never reads x; y must hold whole elements (an odd address is refused)
+        (lambda L: L.muon_gram(None, 1, 1, 1, 4, 0, None), 3),
         (lambda L: L.muon_prepass(1, None, None, 1, 0, 0, 4, 4, 0.9, 1, 0, 0, None, 1, 1, None), 1),
         (lambda L: L.muon_prepass(1, None, None, 1, 0, 1, 4, 4, 0.9, 1, 0, 0, None, 1, 1, None), 5),
         (lambda L: L.muon_orth_run(None, 1, 1, 2, 4, 4, None, 1, 1.0, 1e-7, None), 5),

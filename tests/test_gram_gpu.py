@@ -97,3 +97,18 @@ def test_gram_zero_rows_give_zero_rows_and_columns():
     assert torch.count_nonzero(y[2]) == 0
     assert torch.count_nonzero(y[:, 3]) == 0
     assert torch.count_nonzero(y[:, :, 3]) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gram_abi_empty_contraction_writes_zeros(dtype):
+    """muon_gram with K == 0 through the C ABI: y is all zeros (x is never read, so a
+    null x is fine), whatever y held before."""
+    from muonium_amd import _lib
+
+    lib = _lib.load()
+    _lib.ensure_device(torch.device("cuda"))
+    y = torch.full((3, 17, 17), float("nan"), dtype=dtype, device="cuda")
+    rc = lib.muon_gram(None, y.data_ptr(), _lib.dtype_code(dtype), 3, 17, 0,
+                       _lib.stream(y.device))
+    assert rc == 0, _lib.last_error()
+    assert torch.equal(y.cpu(), torch.zeros(3, 17, 17, dtype=dtype))

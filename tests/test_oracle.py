@@ -214,16 +214,40 @@ def test_split_orthogonalize_known_answer():
     assert scales == pytest.approx((1.0 / full, 1.0 / full))
 
 
-def test_normuon_known_transcription():
-    torch.manual_seed(0)
-    u = torch.randn(4, 3)
-    v = torch.zeros(4, 1)
-    un, vn = R.normuon_normalize(u, v, 0.9)
-    v_exp = 0.1 * (u * u).mean(dim=-1, keepdim=True)
-    u_exp = u / (v_exp.sqrt() + 1e-8)
-    u_exp = u_exp * (u.norm() / u_exp.norm())
-    torch.testing.assert_close(vn, v_exp)
-    torch.testing.assert_close(un, u_exp)
+def test_normuon_invariants():
+    """NorMuon's normalization pinned by what the method fixes, not by its formula:
+    the Frobenius norm of u is preserved; from v = 0 every row ends with the same norm
+    (the division by sqrt of the row mean square equalizes them), i.e. ||u||_F /
+    sqrt(rows); v' = (1 - beta2) * mean_j u_ij^2 from v = 0; a v that already equals the
+    row mean squares is a fixed point of the EMA and then leaves u's direction
+    row-scaled only; with split_sizes the same holds per row block."""
+    gen = torch.Generator().manual_seed(0)
+    # rows with very different scales, so equal row norms are not an accident
+    u = torch.randn(6, 5, generator=gen, dtype=torch.float64) * torch.tensor(
+        [[0.1], [0.3], [1.0], [3.0], [10.0], [100.0]], dtype=torch.float64)
+    rows, cols = u.shape
+    un, vn = R.normuon_normalize(u, torch.zeros(rows, 1, dtype=torch.float64), 0.9)
+    torch.testing.assert_close(un.norm(), u.norm(), rtol=1e-12, atol=0)
+    torch.testing.assert_close(un.norm(dim=1), torch.full((rows,), u.norm().item() / rows**0.5,
+                                                          dtype=torch.float64), rtol=1e-5, atol=0)
+    ms = torch.tensor([[(u[i] ** 2).sum().item() / cols] for i in range(rows)], dtype=torch.float64)
+    torch.testing.assert_close(vn, 0.1 * ms, rtol=1e-12, atol=0)
+    # fixed point of the EMA: v' = v; u is only row-scaled, by 1 / (sqrt(v_i) + 1e-8)
+    un2, vn2 = R.normuon_normalize(u, ms.clone(), 0.5)
+    torch.testing.assert_close(vn2, ms, rtol=1e-12, atol=0)
+    ratio = un2 / u
+    torch.testing.assert_close(ratio, ratio[:, :1].expand_as(ratio), rtol=1e-10, atol=0)
+    # per row block with split_sizes
+    ub, vb = R.normuon_normalize(u, torch.zeros(rows, 1, dtype=torch.float64), 0.9,
+                                 split_sizes=(2, 4))
+    for lo, hi in ((0, 2), (2, 6)):
+        blk = u[lo:hi]
+        torch.testing.assert_close(ub[lo:hi].norm(), blk.norm(), rtol=1e-12, atol=0)
+        torch.testing.assert_close(
+            ub[lo:hi].norm(dim=1),
+            torch.full((hi - lo,), blk.norm().item() / (hi - lo) ** 0.5, dtype=torch.float64),
+            rtol=1e-5, atol=0)
+    torch.testing.assert_close(vb, vn, rtol=1e-12, atol=0)
 
 
 # ---- quantizers -----------------------------------------------------------------------------

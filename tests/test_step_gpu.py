@@ -521,3 +521,67 @@ def test_small_buckets_on_side_streams_match_sequential_buckets():
     (pa, ba), (pb, bb) = runs
     for x, y in zip(pa + ba, pb + bb):
         assert torch.equal(x, y)
+
+
+def test_side_stream_bucket_sharing_padded_extents_with_large_bucket():
+    """A small bucket on a side stream and a large bucket on the caller's stream whose
+    matrices pad to the same workspace extents (96 x 288 -> 256 x 512) run at the same
+    time: each stream has its own workspace, so three steps give bit for bit the
+    parameters and momentum of one bucket per step call."""
+    from muonium_amd.optim import optim as optim_mod
+
+    # large: 4 x (64, 96, 288) = 256 matrices (fills the device, stays on the caller's
+    # stream, listed first so it allocates first); small: (96, 288) x 2 and (96, 96) x 2
+    shapes = [(64, 96, 288)] * 4 + [(96, 288)] * 2 + [(96, 96)] * 2
+    gen = torch.Generator().manual_seed(47)
+    p0 = [torch.randn(s, generator=gen).bfloat16() for s in shapes]
+    gs = [[torch.randn(s, generator=gen).bfloat16() for s in shapes] for _ in range(3)]
+    runs = []
+    for split_groups in (False, True):
+        params = [nn.Parameter(p.clone().to(DEV)) for p in p0]
+        groups = [{"params": [p]} for p in params] if split_groups else [{"params": params}]
+        opt = Muon(groups, lr=0.05, wd=0.1, momentum=0.9, foreach=True)
+        optim_mod._side_streams.clear()
+        for step in range(3):
+            for p, g in zip(params, gs[step]):
+                p.grad = g.to(DEV)
+            opt.step()
+            assert len(optim_mod._side_streams) == (0 if split_groups else 2)
+        torch.cuda.synchronize()
+        runs.append(([p.detach().clone() for p in params],
+                     [opt.state[p]["momentum_buffer"].clone() for p in params]))
+    (pa, ba), (pb, bb) = runs
+    for x, y in zip(pa + ba, pb + bb):
+        assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("algo", ["muon", "normuon"])
+def test_host_params_per_parameter_driver_matches_device_run(algo):
+    """Host-resident params default to the per-parameter driver (foreach=False); each
+    step runs on device copies and copies the results back: params, grads and state
+    equal the device-resident run exactly and stay on the host (the reference steps
+    host-resident muon / normuon groups, test_algorithms.py:140)."""
+    gen = torch.Generator().manual_seed(5)
+    shapes = [(64, 48), (32, 96), (3, 16, 24)]
+    init = [torch.randn(s, generator=gen) for s in shapes]
+    host = [nn.Parameter(t.clone()) for t in init]
+    dev = [nn.Parameter(t.clone().to(DEV)) for t in init]
+    kw = dict(lr=0.05, wd=0.1, momentum=0.9)
+    opt_h = Muon([{"params": host, "algorithm": algo}], **kw)
+    opt_d = Muon([{"params": dev, "algorithm": algo, "foreach": False}], **kw)
+    assert opt_h.param_groups[0]["foreach"] is False
+    for _ in range(2):
+        gs = [torch.randn(s, generator=gen) for s in shapes]
+        for h, d, g in zip(host, dev, gs):
+            h.grad = g.clone()
+            d.grad = g.clone().to(DEV)
+        opt_h.step()
+        opt_d.step()
+    torch.cuda.synchronize()
+    for h, d in zip(host, dev):
+        assert h.device.type == "cpu"
+        assert torch.equal(h.detach(), d.detach().cpu())
+        assert torch.equal(h.grad, d.grad.cpu())
+        for key, val in opt_d.state[d].items():
+            assert opt_h.state[h][key].device.type == "cpu", key
+            assert torch.equal(opt_h.state[h][key], val.cpu()), key
