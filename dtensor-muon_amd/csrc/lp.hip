@@ -204,6 +204,10 @@ struct LpTileArgs {
   int tiles_c, tiles_used;  // column tiles (cols / 256), tiles with data or padding
   float momentum;
   int nesterov, maximize;
+  // deferred scales (blocks larger than 256 values): block / 256 and the absmax of every
+  // 256 values of a row, per matrix of this launch (rows x cols / 256 each)
+  uint32_t block256;
+  uint32_t* amax;
 };
 
 constexpr int LPT_ROWS = 64, LPT_COLS = 256, LPT_PITCH = LPT_COLS + 8;
@@ -368,17 +372,100 @@ MUON_DEVICE uint32_t group_max_u32(uint32_t v, int lanes) {
 typedef __attribute__((ext_vector_type(2))) __bf16 bf2v;
 typedef __attribute__((ext_vector_type(4))) short lp_i16x4;
 
-template <int GDT, int QF, bool TALL>
+// New momentum of 8 consecutive values: m = g * gs + (dequant(code) * old_scale) * mu, in
+// fp32 with one rounding per operation (the fma rounds once; g * gs is exact). Also the
+// unsigned max of |m| as bit patterns. Shared by every LP kernel so a value recomputed
+// by a second pass has the same bits as in the first.
+template <int QF>
+MUON_DEVICE void lp_momentum8(const float (&g)[8], const typename LpCodes<QF>::T& cw, float osc,
+                              float mom, float gs, const float* q, float (&m)[8], uint32_t& ab) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    float v;
+    if constexpr (QF == MUON_Q_FP8) {
+      // hardware e4m3 conversion straight from byte k of the loaded code word
+      const int wd = (int)(k < 4 ? cw.x : cw.y);
+      switch (k & 3) {  // the byte selector must be a constant; k is unrolled
+        case 0: v = __builtin_amdgcn_cvt_f32_fp8(wd, 0); break;
+        case 1: v = __builtin_amdgcn_cvt_f32_fp8(wd, 1); break;
+        case 2: v = __builtin_amdgcn_cvt_f32_fp8(wd, 2); break;
+        default: v = __builtin_amdgcn_cvt_f32_fp8(wd, 3); break;
+      }
+      v = v * osc;
+    } else {
+      v = code_value<QF>(LpCodes<QF>::get(cw, k), q) * osc;
+    }
+    v = v * mom;
+    m[k] = __builtin_fmaf(g[k], gs, v);
+    ab = max(ab, abs_bits(m[k]));
+  }
+}
+
+// Codes of 8 values m / sc: for fp8 the packed code bytes (c8), for the map formats the
+// 8 code indices (cq), through the threshold tables in LDS.
+template <int QF>
+MUON_DEVICE void lp_codes8(const float (&m)[8], float sc, bool sparse_map, const uint32_t* qthr,
+                           const uint8_t* qtab, int (&cq)[8], uint2& c8) {
+#pragma clang fp contract(off)
+  float ys[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) ys[k] = m[k] / sc;
+  if constexpr (QF == MUON_Q_FP8) {
+    // v_cvt_pk_fp8_f32 writes two codes into the low or high half of the word
+    uint32_t w0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ys[0], ys[1], 0, false);
+    w0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ys[2], ys[3], (int)w0, true);
+    uint32_t w1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ys[4], ys[5], 0, false);
+    w1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ys[6], ys[7], (int)w1, true);
+    if (!(sc <= 3.40282347e38f)) {
+      // NaN or infinite scale: NaN quotients code as the positive NaN 0x7f
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if (ys[k] != ys[k]) {
+          uint32_t& w = k < 4 ? w0 : w1;
+          w = (w & ~(0xffu << (8 * (k & 3)))) | (0x7fu << (8 * (k & 3)));
+        }
+      }
+    }
+    c8 = make_uint2(w0, w1);
+  } else {
+    bool more = false;
+    if (sparse_map) {
+      // no key bucket holds more than two thresholds: the third compare is never true
+#pragma unroll
+      for (int k = 0; k < 8; ++k) cq[k] = quant_code_thr<false>(ys[k], qthr, qtab, more);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) cq[k] = quant_code_thr<true>(ys[k], qthr, qtab, more);
+    }
+    // y is NaN only when the scale is NaN or infinite: those blocks take the full
+    // count, which codes NaN as 0
+    if (more || !(sc <= 3.40282347e38f)) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        cq[k] = quant_code_thr_all<QF == MUON_Q_8BIT ? 256 : 16>(ys[k], qthr);
+    }
+  }
+}
+
+// Block index of element e (a multiple of 256 apart from the block start) for a block of
+// block256 * 256 values: a 32-bit division (the launcher checks e / 256 < 2^32).
+MUON_DEVICE int64_t lp_block_of(int64_t e, uint32_t block256) {
+  return (int64_t)((uint32_t)(e >> 8) / block256);
+}
+
+template <int GDT, int QF, bool TALL, bool DEFER>
 __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
 #pragma clang fp contract(off)
   constexpr bool MAP = QF != MUON_Q_FP8;
+  constexpr bool TABLES = MAP && !DEFER;  // code search here (not in a requant pass)
   __shared__ float q[256];
-  __shared__ __align__(16) uint8_t qtab[MAP ? MUON_QTAB_SIZE : 16];
-  __shared__ __align__(16) uint32_t qthr[MAP ? 256 + MUON_QTHR_PAD : 4];
-  // the tall transpose tile: one 32-row half at a time for the map formats (their tables
-  // take 18 KB of LDS, and four workgroups per CU need a quarter of the CU's 160 KB), the
-  // whole 64 rows for fp8
-  constexpr int TROWS = MAP ? LPT_ROWS / 2 : LPT_ROWS;
+  __shared__ __align__(16) uint8_t qtab[TABLES ? MUON_QTAB_SIZE : 16];
+  __shared__ __align__(16) uint32_t qthr[TABLES ? 256 + MUON_QTHR_PAD : 4];
+  // the tall transpose tile: one 32-row half at a time when the code-search tables are
+  // here (they take 18 KB of LDS, and four workgroups per CU need a quarter of the CU's
+  // 160 KB), else the whole 64 rows
+  constexpr int TROWS = TABLES ? LPT_ROWS / 2 : LPT_ROWS;
   __shared__ bf16_t tileT[TALL ? TROWS : 1][TALL ? LPT_PITCH : 1];
   __shared__ float wsum[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -398,7 +485,7 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
   const int chunk = lane & 31;              // 8-value chunk within the row
   const int rsub = wave * 2 + (lane >> 5);  // row within the 8-row pass
   const int64_t c = c0 + chunk * 8;
-  const int block_lanes = 1 << (a.block_shift - 3);
+  const int block_lanes = DEFER ? 32 : 1 << (a.block_shift - 3);
   const float mom = a.momentum;
   constexpr int NP = LPT_ROWS / 8;
 
@@ -417,13 +504,15 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
     const uint4* gt = (const uint4*)a.qtab + tid;
     const uint32_t* gthr = (const uint32_t*)(a.qtab + MUON_QTAB_SIZE);
     tqm = a.qmap[tid < (QF == MUON_Q_8BIT ? 256 : 16) ? tid : 0];
-    tq0 = gt[0];
-    tq1 = gt[256];
-    tq2 = gt[512];
-    tq3 = gt[768];
-    tt0 = gthr[tid];
-    tt1 = gthr[256 + (tid & (MUON_QTHR_PAD - 1))];
-    sparse_map = gthr[MUON_QTHR_FLAG] == 0u;  // the same address for every thread
+    if (TABLES) {
+      tq0 = gt[0];
+      tq1 = gt[256];
+      tq2 = gt[512];
+      tq3 = gt[768];
+      tt0 = gthr[tid];
+      tt1 = gthr[256 + (tid & (MUON_QTHR_PAD - 1))];
+      sparse_map = gthr[MUON_QTHR_FLAG] == 0u;  // the same address for every thread
+    }
     __builtin_amdgcn_sched_barrier(0);
   }
   Raw8<GDT> graw[NP];
@@ -436,16 +525,18 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
     const int64_t e = (mb * a.rows + rr) * a.cols + c;  // element index in the tensor
     graw[p].load(gp, e);
     cw[p] = LpCodes<QF>::load(codes, e);
-    osc[p] = scales[e >> a.block_shift];
+    osc[p] = scales[DEFER ? lp_block_of(e, a.block256) : (e >> a.block_shift)];
   }
   if (MAP) {
     q[tid] = tqm;
-    ((uint4*)qtab)[tid] = tq0;
-    ((uint4*)qtab)[256 + tid] = tq1;
-    ((uint4*)qtab)[512 + tid] = tq2;
-    ((uint4*)qtab)[768 + tid] = tq3;
-    qthr[tid] = tt0;
-    if (tid < MUON_QTHR_PAD) qthr[256 + tid] = tt1;
+    if (TABLES) {
+      ((uint4*)qtab)[tid] = tq0;
+      ((uint4*)qtab)[256 + tid] = tq1;
+      ((uint4*)qtab)[512 + tid] = tq2;
+      ((uint4*)qtab)[768 + tid] = tq3;
+      qthr[tid] = tt0;
+      if (tid < MUON_QTHR_PAD) qthr[256 + tid] = tt1;
+    }
     lds_sync();
   }
 
@@ -464,67 +555,19 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
       const float gs = a.maximize ? -1.0f : 1.0f;  // g * gs is exact: the fma rounds once
       float m[8];
       uint32_t ab = 0;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        float v;
-        if constexpr (QF == MUON_Q_FP8) {
-          // hardware e4m3 conversion straight from byte k of the loaded code word
-          const int wd = (int)(k < 4 ? cw[p].x : cw[p].y);
-          switch (k & 3) {  // the byte selector must be a constant; k is unrolled
-            case 0: v = __builtin_amdgcn_cvt_f32_fp8(wd, 0); break;
-            case 1: v = __builtin_amdgcn_cvt_f32_fp8(wd, 1); break;
-            case 2: v = __builtin_amdgcn_cvt_f32_fp8(wd, 2); break;
-            default: v = __builtin_amdgcn_cvt_f32_fp8(wd, 3); break;
-          }
-          v = v * osc[p];
-        } else {
-          v = code_value<QF>(LpCodes<QF>::get(cw[p], k), q) * osc[p];
-        }
-        v = v * mom;
-        m[k] = __builtin_fmaf(g[k], gs, v);
-        ab = max(ab, abs_bits(m[k]));
-      }
-      // absmax over the block_lanes consecutive lanes of this block (all in one row)
-      const float sc = block_scale<QF>(group_max_u32(ab, block_lanes));
-      float ys[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) ys[k] = m[k] / sc;
+      lp_momentum8<QF>(g, cw[p], osc[p], mom, gs, q, m, ab);
       int cq[8];
       uint2 c8 = {0u, 0u};  // fp8: the 8 code bytes, packed by the conversion itself
-      if constexpr (QF == MUON_Q_FP8) {
-        // v_cvt_pk_fp8_f32 writes two codes into the low or high half of the word
-        uint32_t w0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ys[0], ys[1], 0, false);
-        w0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ys[2], ys[3], (int)w0, true);
-        uint32_t w1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ys[4], ys[5], 0, false);
-        w1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ys[6], ys[7], (int)w1, true);
-        if (!(sc <= 3.40282347e38f)) {
-          // NaN or infinite scale: NaN quotients code as the positive NaN 0x7f
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            if (ys[k] != ys[k]) {
-              uint32_t& w = k < 4 ? w0 : w1;
-              w = (w & ~(0xffu << (8 * (k & 3)))) | (0x7fu << (8 * (k & 3)));
-            }
-          }
-        }
-        c8 = make_uint2(w0, w1);
+      float sc = 0.0f;
+      if constexpr (DEFER) {
+        // the block extends past this tile: leave its absmax over these 256 values (one
+        // row, 32 lanes) for the scale reduction; codes come in the requant pass
+        const uint32_t amax = group_max_u32(ab, 32);
+        if (chunk == 0) a.amax[(mat * a.rows + r) * (a.cols >> 8) + (c0 >> 8)] = amax;
       } else {
-        bool more = false;
-        if (sparse_map) {
-          // no key bucket holds more than two thresholds: the third compare is never true
-#pragma unroll
-          for (int k = 0; k < 8; ++k) cq[k] = quant_code_thr<false>(ys[k], qthr, qtab, more);
-        } else {
-#pragma unroll
-          for (int k = 0; k < 8; ++k) cq[k] = quant_code_thr<true>(ys[k], qthr, qtab, more);
-        }
-        // y is NaN only when the scale is NaN or infinite: those blocks take the full
-        // count, which codes NaN as 0
-        if (more || !(sc <= 3.40282347e38f)) {
-#pragma unroll
-          for (int k = 0; k < 8; ++k)
-            cq[k] = quant_code_thr_all<QF == MUON_Q_8BIT ? 256 : 16>(ys[k], qthr);
-        }
+        // absmax over the block_lanes consecutive lanes of this block (all in one row)
+        sc = block_scale<QF>(group_max_u32(ab, block_lanes));
+        lp_codes8<QF>(m, sc, sparse_map, qthr, qtab, cq, c8);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -539,11 +582,13 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
         ss = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2v, xw[i]),
                                              __builtin_bit_cast(bf2v, xw[i]), ss, false);
       }
-      if constexpr (QF == MUON_Q_FP8)
-        *(uint2*)(codes + e) = c8;
-      else
-        LpCodes<QF>::store(codes, e, cq);
-      if ((chunk & (block_lanes - 1)) == 0) scales[e >> a.block_shift] = sc;
+      if constexpr (!DEFER) {
+        if constexpr (QF == MUON_Q_FP8)
+          *(uint2*)(codes + e) = c8;
+        else
+          LpCodes<QF>::store(codes, e, cq);
+        if ((chunk & (block_lanes - 1)) == 0) scales[e >> a.block_shift] = sc;
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) xw[i] = 0u;
@@ -586,19 +631,159 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
   if (tid == 0) part[blockIdx.x] = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
 }
 
-template <int GDT, int QF>
+template <int GDT, int QF, bool DEFER>
 void launch_lp_tile_t(bool tall, const LpTileArgs& a, dim3 grid, hipStream_t s) {
   if (tall)
-    hipLaunchKernelGGL((lp_prepass_tile_kernel<GDT, QF, true>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((lp_prepass_tile_kernel<GDT, QF, true, DEFER>), grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((lp_prepass_tile_kernel<GDT, QF, false>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((lp_prepass_tile_kernel<GDT, QF, false, DEFER>), grid, dim3(256), 0, s, a);
+}
+
+template <int GDT, bool DEFER>
+void launch_lp_tile_q(int qf, bool tall, const LpTileArgs& a, dim3 grid, hipStream_t s) {
+  if (qf == MUON_Q_8BIT) launch_lp_tile_t<GDT, MUON_Q_8BIT, DEFER>(tall, a, grid, s);
+  else if (qf == MUON_Q_4BIT) launch_lp_tile_t<GDT, MUON_Q_4BIT, DEFER>(tall, a, grid, s);
+  else launch_lp_tile_t<GDT, MUON_Q_FP8, DEFER>(tall, a, grid, s);
+}
+
+// ---- deferred scales: blocks of more than 256 values --------------------------------
+// The tile kernel (DEFER) has left the absmax of every 256 values; this kernel reduces
+// them per block (a group of G lanes per block, G a power of two <= 64), keeps the old
+// scale for the requant pass and stores the new one. Nothing else reads `scales` between
+// the tile kernel and the requant pass.
+struct LpReduceArgs {
+  float* scales[MUON_MAX_TENSORS];
+  const uint32_t* amax;  // [tensor][numel / 256] for the tensors of this launch
+  float* oldsc;          // [tensor][nblocks]
+  int64_t nblocks;       // per tensor
+  int64_t parts;         // partials per block (block / 256)
+  int64_t numel256;      // numel / 256 per tensor
+  int group_shift;       // log2(G)
+  int ntensors;
+};
+
+template <int QF>
+__global__ __launch_bounds__(256) void lp_scale_reduce_kernel(LpReduceArgs a) {
+  const int G = 1 << a.group_shift;
+  const int64_t gid = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> a.group_shift;
+  const int gl = threadIdx.x & (G - 1);
+  const int64_t total = a.nblocks * a.ntensors;
+  const bool active = gid < total;
+  const int64_t t = active ? gid / a.nblocks : 0, b = active ? gid % a.nblocks : 0;
+  uint32_t mx = 0;
+  if (active) {
+    const uint32_t* src = a.amax + t * a.numel256 + b * a.parts;
+    for (int64_t i = gl; i < a.parts; i += G) mx = max(mx, src[i]);
+  }
+  // groups are aligned within the wave: an xor butterfly over the group's lanes
+  for (int off = G >> 1; off > 0; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, 64));
+  if (active && gl == 0) {
+    float* sc = a.scales[t];
+    a.oldsc[t * a.nblocks + b] = sc[b];
+    sc[b] = block_scale<QF>(mx);
+  }
+}
+
+// Requantization of blocks whose scale was reduced across tiles: recompute the new
+// momentum exactly as the tile kernel did (the same inputs, lp_momentum8) and code it
+// with the new scale. Flat over each tensor's values, 8 per lane, 8 passes of 2048 per
+// workgroup with every load issued before the first is used.
+struct LpRequantArgs {
+  void* grads[MUON_MAX_TENSORS];
+  void* codes[MUON_MAX_TENSORS];
+  float* scales[MUON_MAX_TENSORS];  // new scales
+  const float* oldsc;               // [tensor][nblocks]
+  const float* qmap;
+  const uint8_t* qtab;              // bucket table, then thresholds
+  int64_t numel, nblocks;           // per tensor
+  uint32_t block256;
+  float momentum;
+  int maximize;
+};
+
+constexpr int LPR_PASSES = 8;
+
+template <int GDT, int QF>
+__global__ __launch_bounds__(256) void lp_requant_kernel(LpRequantArgs a) {
+#pragma clang fp contract(off)
+  constexpr bool MAP = QF != MUON_Q_FP8;
+  __shared__ float q[256];
+  __shared__ __align__(16) uint8_t qtab[MAP ? MUON_QTAB_SIZE : 16];
+  __shared__ __align__(16) uint32_t qthr[MAP ? 256 + MUON_QTHR_PAD : 4];
+  const int tid = threadIdx.x;
+  const int t = blockIdx.y;
+  uint4 tq0 = {}, tq1 = {}, tq2 = {}, tq3 = {};
+  float tqm = 0.0f;
+  uint32_t tt0 = 0, tt1 = 0;
+  bool sparse_map = false;
+  if (MAP) {
+    const uint4* gt = (const uint4*)a.qtab + tid;
+    const uint32_t* gthr = (const uint32_t*)(a.qtab + MUON_QTAB_SIZE);
+    tqm = a.qmap[tid < (QF == MUON_Q_8BIT ? 256 : 16) ? tid : 0];
+    tq0 = gt[0];
+    tq1 = gt[256];
+    tq2 = gt[512];
+    tq3 = gt[768];
+    tt0 = gthr[tid];
+    tt1 = gthr[256 + (tid & (MUON_QTHR_PAD - 1))];
+    sparse_map = gthr[MUON_QTHR_FLAG] == 0u;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const void* gp = a.grads[t];
+  uint8_t* codes = (uint8_t*)a.codes[t];
+  const float* nsc = a.scales[t];
+  const float* osc_t = a.oldsc + (int64_t)t * a.nblocks;
+  const int64_t base = (int64_t)blockIdx.x * LPR_PASSES * 2048 + tid * 8;
+  Raw8<GDT> graw[LPR_PASSES];
+  typename LpCodes<QF>::T cw[LPR_PASSES];
+  float osc[LPR_PASSES], sc[LPR_PASSES];
+#pragma unroll
+  for (int p = 0; p < LPR_PASSES; ++p) {
+    const int64_t e0 = base + p * 2048;
+    const int64_t e = e0 < a.numel ? e0 : a.numel - 8;  // clamped, not used
+    const int64_t b = lp_block_of(e, a.block256);
+    graw[p].load(gp, e);
+    cw[p] = LpCodes<QF>::load(codes, e);
+    osc[p] = osc_t[b];
+    sc[p] = nsc[b];
+  }
+  if (MAP) {
+    q[tid] = tqm;
+    ((uint4*)qtab)[tid] = tq0;
+    ((uint4*)qtab)[256 + tid] = tq1;
+    ((uint4*)qtab)[512 + tid] = tq2;
+    ((uint4*)qtab)[768 + tid] = tq3;
+    qthr[tid] = tt0;
+    if (tid < MUON_QTHR_PAD) qthr[256 + tid] = tt1;
+    lds_sync();
+  }
+  const float gs = a.maximize ? -1.0f : 1.0f;
+#pragma unroll
+  for (int p = 0; p < LPR_PASSES; ++p) {
+    const int64_t e = base + p * 2048;
+    if (e >= a.numel) continue;
+    float g[8], m[8];
+    graw[p].unpack(g);
+    uint32_t ab = 0;
+    lp_momentum8<QF>(g, cw[p], osc[p], a.momentum, gs, q, m, ab);
+    int cq[8];
+    uint2 c8 = {0u, 0u};
+    lp_codes8<QF>(m, sc[p], sparse_map, qthr, qtab, cq, c8);
+    if constexpr (QF == MUON_Q_FP8)
+      *(uint2*)(codes + e) = c8;
+    else
+      LpCodes<QF>::store(codes, e, cq);
+  }
 }
 
 template <int GDT>
-void launch_lp_tile_q(int qf, bool tall, const LpTileArgs& a, dim3 grid, hipStream_t s) {
-  if (qf == MUON_Q_8BIT) launch_lp_tile_t<GDT, MUON_Q_8BIT>(tall, a, grid, s);
-  else if (qf == MUON_Q_4BIT) launch_lp_tile_t<GDT, MUON_Q_4BIT>(tall, a, grid, s);
-  else launch_lp_tile_t<GDT, MUON_Q_FP8>(tall, a, grid, s);
+void launch_lp_requant_q(int qf, const LpRequantArgs& a, dim3 grid, hipStream_t s) {
+  if (qf == MUON_Q_8BIT)
+    hipLaunchKernelGGL((lp_requant_kernel<GDT, MUON_Q_8BIT>), grid, dim3(256), 0, s, a);
+  else if (qf == MUON_Q_4BIT)
+    hipLaunchKernelGGL((lp_requant_kernel<GDT, MUON_Q_4BIT>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((lp_requant_kernel<GDT, MUON_Q_FP8>), grid, dim3(256), 0, s, a);
 }
 
 template <int QF>
@@ -717,13 +902,17 @@ int muon_launch_lp_prepass_tiled(int ntensors, void* const* grads, int gdt, void
                                  int64_t mat0, hipStream_t s) {
   int shift = 0;
   while ((1LL << shift) < block) ++shift;
-  if (cols % LPT_COLS || (1LL << shift) != block || block < 8 || block > LPT_COLS) return MUON_ERR_SHAPE;
-  const int64_t ges = gdt == MUON_DT_F32 ? 4 : 2;
+  // blocks of at most 256 values (a power of two) lie within one tile row: one pass;
+  // larger blocks (multiples of 256, up to the whole tensor) defer their scale to a
+  // reduction over the tiles' absmax partials and a requant pass
+  const int64_t numel = nb * rows * cols;
+  const bool fused = (1LL << shift) == block && block >= 8 && block <= LPT_COLS;
+  const bool defer = !fused && block % 256 == 0 && (numel >> 8) < (1LL << 32);
+  if (cols % LPT_COLS || !(fused || defer)) return MUON_ERR_SHAPE;
   for (int i = 0; i < ntensors; ++i) {
     if (((uintptr_t)grads[i] & 15) || ((uintptr_t)codes[i] & 7) || ((uintptr_t)scales[i] & 3))
       return MUON_ERR_SHAPE;
   }
-  (void)ges;
   LpTileArgs a;
   for (int i = 0; i < ntensors; ++i) {
     a.grads[i] = grads[i];
@@ -749,6 +938,15 @@ int muon_launch_lp_prepass_tiled(int ntensors, void* const* grads, int gdt, void
   a.momentum = momentum;
   a.nesterov = nesterov;
   a.maximize = maximize;
+  // deferred scales: absmax partials of every matrix (rows * cols / 256 each), then the
+  // old scales of every tensor, in the X1 iterate buffer, which nothing reads before the
+  // first product of the iteration writes it
+  const int64_t mat_parts = rows * cols / 256;
+  const int64_t nblocks = numel / block;
+  uint32_t* amax_all = (uint32_t*)((char*)ws + L.off_x1);
+  float* oldsc_all = (float*)((char*)amax_all + round_up(L.batch * mat_parts * 4, 256));
+  a.block256 = (uint32_t)(block / 256);
+  a.amax = amax_all + mat0 * mat_parts;
   if (qf != MUON_Q_FP8 && mat0 == 0) {
     // thresholds and bucket table of this map, rebuilt per call (a few microseconds)
     uint8_t* tab = (uint8_t*)ws + L.off_qtab;
@@ -760,16 +958,69 @@ int muon_launch_lp_prepass_tiled(int ntensors, void* const* grads, int gdt, void
     hipLaunchKernelGGL(build_qtab_kernel, dim3(MUON_QTAB_SIZE / 256), dim3(256), 0, s,
                        (const uint32_t*)thr, qf == MUON_Q_8BIT ? 256 : 16, tab);
   }
+  if (gdt != MUON_DT_F32 && gdt != MUON_DT_BF16 && gdt != MUON_DT_F16) {
+    muon_set_error("lp_prepass: unsupported grad dtype %d", gdt);
+    return MUON_ERR_DTYPE;
+  }
   dim3 grid((unsigned)L.parts, (unsigned)(ntensors * nb));
   switch (gdt) {
-    case MUON_DT_F32: launch_lp_tile_q<MUON_DT_F32>(qf, L.tall, a, grid, s); break;
-    case MUON_DT_BF16: launch_lp_tile_q<MUON_DT_BF16>(qf, L.tall, a, grid, s); break;
-    case MUON_DT_F16: launch_lp_tile_q<MUON_DT_F16>(qf, L.tall, a, grid, s); break;
+    case MUON_DT_F32:
+      defer ? launch_lp_tile_q<MUON_DT_F32, true>(qf, L.tall, a, grid, s)
+            : launch_lp_tile_q<MUON_DT_F32, false>(qf, L.tall, a, grid, s);
+      break;
+    case MUON_DT_BF16:
+      defer ? launch_lp_tile_q<MUON_DT_BF16, true>(qf, L.tall, a, grid, s)
+            : launch_lp_tile_q<MUON_DT_BF16, false>(qf, L.tall, a, grid, s);
+      break;
     default:
-      muon_set_error("lp_prepass: unsupported grad dtype %d", gdt);
-      return MUON_ERR_DTYPE;
+      defer ? launch_lp_tile_q<MUON_DT_F16, true>(qf, L.tall, a, grid, s)
+            : launch_lp_tile_q<MUON_DT_F16, false>(qf, L.tall, a, grid, s);
+      break;
   }
   MUON_CHECK_LAUNCH("lp_prepass_tiled");
+  if (!defer) return MUON_OK;
+
+  const int64_t t_first = mat0 / nb;  // tensor index of this launch's first tensor
+  LpReduceArgs r;
+  for (int i = 0; i < ntensors; ++i) r.scales[i] = (float*)scales[i];
+  r.amax = a.amax;
+  r.oldsc = oldsc_all + t_first * nblocks;
+  r.nblocks = nblocks;
+  r.parts = block / 256;
+  r.numel256 = numel / 256;
+  int gshift = 0;
+  while ((1LL << gshift) < r.parts && gshift < 6) ++gshift;
+  r.group_shift = gshift;
+  r.ntensors = ntensors;
+  const int64_t rthreads = nblocks * ntensors << gshift;
+  dim3 rgrid((unsigned)((rthreads + 255) / 256));
+  if (qf == MUON_Q_FP8)
+    hipLaunchKernelGGL(lp_scale_reduce_kernel<MUON_Q_FP8>, rgrid, dim3(256), 0, s, r);
+  else
+    hipLaunchKernelGGL(lp_scale_reduce_kernel<MUON_Q_8BIT>, rgrid, dim3(256), 0, s, r);
+  MUON_CHECK_LAUNCH("lp_scale_reduce");
+
+  LpRequantArgs q;
+  for (int i = 0; i < ntensors; ++i) {
+    q.grads[i] = grads[i];
+    q.codes[i] = codes[i];
+    q.scales[i] = (float*)scales[i];
+  }
+  q.oldsc = r.oldsc;
+  q.qmap = qmap;
+  q.qtab = a.qtab;
+  q.numel = numel;
+  q.nblocks = nblocks;
+  q.block256 = a.block256;
+  q.momentum = momentum;
+  q.maximize = maximize;
+  dim3 qgrid((unsigned)((numel + LPR_PASSES * 2048 - 1) / (LPR_PASSES * 2048)), (unsigned)ntensors);
+  switch (gdt) {
+    case MUON_DT_F32: launch_lp_requant_q<MUON_DT_F32>(qf, q, qgrid, s); break;
+    case MUON_DT_BF16: launch_lp_requant_q<MUON_DT_BF16>(qf, q, qgrid, s); break;
+    default: launch_lp_requant_q<MUON_DT_F16>(qf, q, qgrid, s); break;
+  }
+  MUON_CHECK_LAUNCH("lp_requant");
   return MUON_OK;
 }
 

@@ -194,3 +194,9 @@ class OptimStateFp8(QuantizedState):
     @classmethod
     def zeros(cls, shape, block_size: int = 256, device=None):  # type: ignore[override]
         return super().zeros(shape, True, block_size, device)
+
+
+# A MuonLP checkpoint holds these objects as optimizer state. Their pickled form is the
+# class plus a dict of plain tensors and scalars, which torch.load's default
+# weights_only unpickler accepts once the classes are allow-listed.
+torch.serialization.add_safe_globals([OptimState8bit, OptimState4bit, OptimStateFp8])

@@ -29,6 +29,7 @@ from muonium_amd.utils.offload import pipeline_supported, run_offloaded
 
 from .algorithms import BufferSpec, MuonAlgorithm, get_algorithm
 from .algorithms.base import ADAM_ALGORITHMS
+from .lp_state import QuantizedState
 
 
 def _group_muon_tensors(
@@ -310,6 +311,11 @@ class Muon(torch.optim.Optimizer):
                     p_state = self.state.get(p, [])
                     if len(p_state) != 0 and not torch.is_tensor(p_state["step"]):
                         p_state["step"] = torch.tensor(float(p_state["step"]))
+                    # load_state_dict moves tensor state to the param's device; quantized
+                    # momentum (not a tensor) is moved here, as torchao's subclasses are
+                    for key, val in (p_state.items() if len(p_state) != 0 else ()):
+                        if isinstance(val, QuantizedState) and val.device != p.device:
+                            p_state[key] = val.to(p.device)
             else:
                 group.setdefault("amsgrad", False)
                 group.setdefault("maximize", False)

@@ -42,7 +42,7 @@ class MuonLP(Muon):
         fused_adam: bool | None = None,
         foreach: bool | None = False,
         batch_size: int | None = None,
-        block_size: int = 2048,
+        block_size: int | None = 2048,
         bf16_stochastic_round: bool = False,
     ):
         super().__init__(
@@ -74,9 +74,14 @@ class MuonLP(Muon):
 
     def _new_buffer(self, p: Tensor, signed: bool):
         """Quantized zeros when eligible (optim_lp.py:81-102, bitsandbytes' 4096
-        threshold), else plain zeros in the param's dtype."""
-        if p.numel() >= 4096 and p.numel() % self.block_size == 0:
-            out = self._subclass_zeros(p, signed, self.block_size)
+        threshold), else plain zeros in the param's dtype.
+
+        ``block_size=None`` (an addition to the reference's API, whose blocks all have one
+        size per optimizer) gives every quantized buffer a single block, i.e. one scale
+        per tensor; the eligibility threshold is unchanged."""
+        block = p.numel() if self.block_size is None else self.block_size
+        if p.numel() >= 4096 and p.numel() % block == 0:
+            out = self._subclass_zeros(p, signed, block)
         else:
             out = torch.zeros_like(p)
         return out.to(p.device)

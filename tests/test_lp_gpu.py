@@ -148,6 +148,34 @@ def test_lp_tiled_prepass_outputs_exact(fmt, cls, block, shape, gdtype):
     for tall matrices, zero padding included) and the norm partials. Called through
     the C ABI: codes and scales bit-exact against the quantizer oracle, X0 equal to
     bf16(g') in the wide layout, the partials summing to sum(x^2)."""
+    _check_tiled_prepass(fmt, cls, block, shape, gdtype)
+
+
+# blocks of more than 256 values: the reference's default 2048 (optim_lp.py:49), other
+# multiples of 256, and one block per tensor (an fp8 per-tensor scale)
+DEFERRED = [("8bit", OptimState8bit, 2048), ("4bit", OptimState4bit, 2048),
+            ("fp8", OptimStateFp8, 2048), ("8bit", OptimState8bit, 512),
+            ("4bit", OptimState4bit, 768), ("fp8", OptimStateFp8, "numel"),
+            ("8bit", OptimState8bit, "numel")]
+DEFERRED_SHAPES = [(512, 256), (256, 768), (2048, 256), (2, 256, 512), (4, 96, 512)]
+
+
+@pytest.mark.parametrize("fmt,cls,block", DEFERRED)
+@pytest.mark.parametrize("shape", DEFERRED_SHAPES)
+@pytest.mark.parametrize("gdtype", [torch.float32, torch.bfloat16])
+def test_lp_deferred_scale_prepass_outputs_exact(fmt, cls, block, shape, gdtype):
+    """Blocks larger than a tile row (multiples of 256, up to the whole tensor) take the
+    tiled pass with the scale deferred: absmax partials per 256 values, a per-block
+    reduction, and a requant pass that recomputes the same momentum. Codes, scales, X0
+    and the norm partials exactly as for the one-pass blocks, wide and tall."""
+    numel = math.prod(shape)
+    block = numel if block == "numel" else block
+    if numel % block:
+        pytest.skip(f"{numel} values do not split into blocks of {block}")
+    _check_tiled_prepass(fmt, cls, block, shape, gdtype)
+
+
+def _check_tiled_prepass(fmt, cls, block, shape, gdtype):
     from muonium_amd import _lib
 
     lib = _lib.load()
@@ -195,7 +223,9 @@ def test_lp_tiled_prepass_outputs_exact(fmt, cls, block, shape, gdtype):
     torch.testing.assert_close(P.sum(dim=1), want, rtol=1e-6, atol=0)
 
 
-@pytest.mark.parametrize("fmt,cls,block", TILED[:3])
+@pytest.mark.parametrize("fmt,cls,block", TILED[:3] + [("8bit", OptimState8bit, 2048),
+                                                      ("fp8", OptimStateFp8, 2048),
+                                                      ("fp8", OptimStateFp8, None)])
 @pytest.mark.parametrize("shape", [(512, 256), (256, 768)])
 def test_lp_tiled_step_matches_oracle(fmt, cls, block, shape):
     """The full MuonLP step on a tiled shape: codes bit-exact; the update within the
@@ -219,11 +249,13 @@ def test_lp_tiled_step_matches_oracle(fmt, cls, block, shape):
         if codes is None:
             codes = np.zeros(st.codes.numel(), np.uint8)
             scales = np.zeros(st.scale.numel(), np.float32)
+        assert st.block_size == (block or math.prod(shape))  # None: one block per tensor
         codes, scales, gq = quant_ref.lp_momentum_step(
-            codes, scales, g.numpy(), block=block, fmt=fmt, qmap=_qmap(fmt), momentum=0.9,
-            nesterov=True, maximize=False,
+            codes, scales, g.numpy(), block=st.block_size, fmt=fmt, qmap=_qmap(fmt),
+            momentum=0.9, nesterov=True, maximize=False,
         )
         assert np.array_equal(st.codes.cpu().numpy(), codes), f"codes differ at step {step}"
+        assert np.array_equal(st.scale.cpu().numpy().view(np.uint32), scales.view(np.uint32))
         U = muon_ref.polar_iteration_bf16(torch.from_numpy(gq).view(shape), coeffs,
                                           prescale=prescale, eps=1e-7)
         adj = muon_ref.lr_ratio(shape) * 0.05
@@ -242,17 +274,22 @@ def _same_scales(got, want):
 
 @pytest.mark.filterwarnings("ignore:invalid value encountered:RuntimeWarning")
 @pytest.mark.parametrize("fmt,cls,block", TILED[:3])
-@pytest.mark.parametrize("path", ["quantize", "general", "tiled-wide", "tiled-tall"])
+@pytest.mark.parametrize("path", ["quantize", "general", "tiled-wide", "tiled-tall",
+                                  "deferred-wide", "deferred-tall"])
 def test_lp_nan_and_inf_blocks_match_oracle(fmt, cls, block, path):
     """A NaN in a block makes the block's scale NaN and codes every value of it as a NaN
     quotient (0 for the maps, 0x7f for fp8), as torch's amax / clamp do in the reference;
     an infinite value makes the scale infinite (its own quotient NaN, the others 0).
     Covered for the standalone quantizer, the general pre-pass (columns not a multiple
-    of 256) and the tiled pre-pass in both orientations, two steps each."""
+    of 256), the tiled pre-pass in both orientations and its deferred-scale form (blocks
+    of 2048), two steps each."""
     from muonium_amd import _lib
 
     shape = {"quantize": (64, 256), "general": (128, 96), "tiled-wide": (256, 768),
-             "tiled-tall": (512, 256)}[path]
+             "tiled-tall": (512, 256), "deferred-wide": (256, 768),
+             "deferred-tall": (512, 256)}[path]
+    if path.startswith("deferred"):
+        block = 2048  # a block longer than a tile row: the scale is reduced across tiles
     gen = torch.Generator().manual_seed(9)
     g = torch.randn(shape, generator=gen)
     g[0, 5] = float("nan")
@@ -289,7 +326,10 @@ def test_lp_nan_and_inf_blocks_match_oracle(fmt, cls, block, path):
         )
         assert np.array_equal(st.codes.cpu().numpy(), codes), f"codes differ at step {step}"
         _same_scales(st.scale.cpu().numpy(), scales)
-    assert np.isnan(scales).sum() >= 3  # the inf blocks turn NaN at the second step
+    # every block holding a non-finite value has a NaN scale at the second step (an inf
+    # block's own quotient inf / inf is NaN, so its momentum is NaN from then on)
+    bad_blocks = {(r * cols + c) // block for r, c in ((0, 5), (7, 60), (9, 1))}
+    assert np.isnan(scales).sum() == len(bad_blocks)
 
 
 def test_fp8_codes_exact_at_every_rounding_boundary():
@@ -380,3 +420,57 @@ def test_lp_custom_map_codes_exact_and_flag(dense):
     thr = ws[off_qtab + 16384: off_qtab + 16384 + 260 * 4].cpu().view(torch.int32).numpy().view(np.uint32)
     assert thr[259] == (1 if dense else 0)
     assert thr[256] == 0xFFFFFFFF and thr[257] == 0xFFFFFFFF
+
+
+@pytest.mark.parametrize("opt_cls", [Muon8bit, Muon4bit, MuonFp8])
+@pytest.mark.parametrize("map_location", [None, "cpu"])
+def test_lp_checkpoint_round_trip_with_weights_only(opt_cls, map_location):
+    """state_dict -> torch.save -> torch.load(weights_only=True) -> load_state_dict keeps
+    training continuous (test_optim.py:660-686 for Muon, here for the quantized states):
+    two more steps from the loaded checkpoint give bit for bit the params, codes and
+    scales of an uninterrupted run. Loaded onto the CPU (map_location="cpu"), the
+    quantized state moves back to its param's device on load_state_dict."""
+    import io
+
+    gen = torch.Generator().manual_seed(3)
+    # tiled wide, tiled tall, general (cols not a multiple of 256) and dense (numel < 4096).
+    # lr_ratio is 1 or 2 here: load_state_dict casts every state tensor but `step` to the
+    # param's dtype (torch.optim.Optimizer, as in the reference), so a bf16 param's
+    # lr_ratio = sqrt(2) would come back rounded to bf16 and the trajectory would differ
+    shapes = [(128, 256), (1024, 256), (256, 64), (8, 16)]
+    init = [torch.randn(s, generator=gen).bfloat16() for s in shapes]
+    grads = [[torch.randn(s, generator=gen).bfloat16() for s in shapes] for _ in range(4)]
+    kw = dict(lr=0.05, wd=0.1, momentum=0.9, block_size=256)
+
+    def run(params, opt, steps):
+        for k in steps:
+            for p, g in zip(params, grads[k]):
+                p.grad = g.to(DEV)
+            opt.step()
+
+    ref_p = [nn.Parameter(t.clone().to(DEV)) for t in init]
+    ref = opt_cls(ref_p, **kw)
+    run(ref_p, ref, range(4))
+
+    src_p = [nn.Parameter(t.clone().to(DEV)) for t in init]
+    src = opt_cls(src_p, **kw)
+    run(src_p, src, range(2))
+    blob = io.BytesIO()
+    torch.save(src.state_dict(), blob)
+    blob.seek(0)
+    sd = torch.load(blob, weights_only=True, map_location=map_location)
+    dst_p = [nn.Parameter(p.detach().clone()) for p in src_p]
+    dst = opt_cls(dst_p, **kw)
+    dst.load_state_dict(sd)
+    mb = dst.state[dst_p[0]]["momentum_buffer"]
+    assert type(mb).__name__.startswith("OptimState") and mb.device.type == "cuda"
+    run(dst_p, dst, range(2, 4))
+    torch.cuda.synchronize()
+    for a, b in zip(dst_p, ref_p):
+        assert torch.equal(a.detach(), b.detach())
+    for a, b in zip(dst_p, ref_p):
+        sa, sb = dst.state[a]["momentum_buffer"], ref.state[b]["momentum_buffer"]
+        if hasattr(sb, "codes"):
+            assert torch.equal(sa.codes, sb.codes) and torch.equal(sa.scale, sb.scale)
+        else:
+            assert torch.equal(sa, sb)

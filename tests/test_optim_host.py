@@ -254,6 +254,21 @@ def test_lp_buffer_eligibility(opt_cls, state_cls, shape, block, quantized):
     assert torch.count_nonzero(dense) == 0
 
 
+@pytest.mark.parametrize("opt_cls,state_cls", [(Muon8bit, OptimState8bit), (MuonFp8, OptimStateFp8)])
+def test_lp_block_size_none_gives_one_block_per_tensor(opt_cls, state_cls):
+    """block_size=None: every quantized buffer is a single block (one scale per tensor),
+    whatever its size; buffers under 4096 values stay dense in the param's dtype."""
+    ps = [nn.Parameter(torch.randn(*s)) for s in ((64, 96), (128, 64), (3, 64, 32), (32, 32))]
+    opt = opt_cls(ps, block_size=None)
+    for p in ps:
+        buf = opt._new_buffer(p, signed=True)
+        if p.numel() >= 4096:
+            assert isinstance(buf, state_cls)
+            assert buf.block_size == p.numel() and buf.scale.numel() == 1
+        else:
+            assert type(buf) is torch.Tensor and buf.dtype == p.dtype
+
+
 def test_lp_stochastic_round_flag_is_stored():
     assert Muon8bit([nn.Parameter(torch.randn(32, 32))], bf16_stochastic_round=True).bf16_stochastic_round
 
@@ -269,3 +284,27 @@ def test_group_tensors_by_shape_and_move_helpers():
     ts = [a, None]
     assert move_tensors_to_device(ts, torch.device("cpu"), torch.device("cpu")) is ts
     assert move_tensors_to_device([], torch.device("cpu"), torch.device("cuda")) == []
+
+
+@pytest.mark.parametrize("state_cls,args", [(OptimState8bit, (True, 256)),
+                                            (OptimState4bit, (False, 128)),
+                                            (OptimStateFp8, (512,))])
+def test_quantized_state_loads_with_weights_only(state_cls, args):
+    """A quantized momentum state inside an optimizer state dict survives torch.save and
+    torch.load with the default weights_only=True: same class, shape, block size,
+    signedness, codes, scales and map."""
+    import io
+
+    st = state_cls.zeros((32, 64), *args, device="cpu")
+    st.codes.copy_(torch.arange(st.codes.numel(), dtype=torch.int64).remainder(251).to(torch.uint8))
+    st.scale.copy_(torch.linspace(0.5, 2.0, st.scale.numel()))
+    blob = io.BytesIO()
+    torch.save({"state": {0: {"step": torch.tensor(2.0), "momentum_buffer": st}}}, blob)
+    blob.seek(0)
+    got = torch.load(blob, weights_only=True)["state"][0]["momentum_buffer"]
+    assert type(got) is state_cls
+    assert (got.shape, got.block_size, got.signed) == (st.shape, st.block_size, st.signed)
+    assert torch.equal(got.codes, st.codes) and torch.equal(got.scale, st.scale)
+    assert (got.qmap is None) == (st.qmap is None)
+    if st.qmap is not None:
+        assert torch.equal(got.qmap, st.qmap)
