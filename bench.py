@@ -12,8 +12,9 @@ ms_per_step = Muon step time, plus the roofline of the dominant kernel (the B X 
 from hipEvent timing of every launch, per-kernel breakdowns, and the CPU baseline
 (the oracle's per-parameter loop on a bounded sample, on this host's cores).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config llama|gpt2|moe]
-       [--lp 8bit|4bit|fp8] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+       [--config llama|gpt2|moe|moe_flat|plumbing] [--lp 8bit|4bit|fp8 [--block-size N|tensor]]
+       [--no-cpu-baseline] | --reference-suite | --blas-ceiling | --calibrate-copy
 """
 
 from __future__ import annotations
@@ -68,17 +69,34 @@ def orth_flops(shape, steps: int) -> float:
     return nb * steps * (m * (m + 1) * n + m * (m + 1) * m + 2 * m * m * n)
 
 
+def _config_hparams(config: str) -> tuple[str, "torch.dtype"]:
+    """(strategy, param dtype) of a workload: Newton-Schulz for the plumbing check and the
+    MoE set (BASELINE.json configs 1 and 4), Polar Express otherwise; fp32 params for the
+    plumbing check, bf16 otherwise."""
+    import torch
+
+    strategy = "newton_schulz" if config in ("moe", "moe_flat", "plumbing") else "polar_express"
+    return strategy, (torch.float32 if config == "plumbing" else torch.bfloat16)
+
+
 def cpu_baseline(config: str = "llama", min_seconds: float = 10.0) -> dict:
-    """The reference's per-parameter loop restated on the CPU (oracle.muon_ref), on a
-    bounded sample: steps of ONE matrix of each distinct shape of the workload (bf16
-    Polar Express 5, cautious wd, Nesterov), whole passes over the shapes until at
-    least min_seconds (10-30 s of CPU work on the bench host). Reported
-    as the sample's orthogonalization TFLOP/s, plus the full-step time extrapolated
-    by weighting each shape's time with its count in the workload."""
+    """The reference's per-parameter loop restated on the CPU (oracle.muon_ref: the
+    foreach=False driver, MuonBaseline.update, the eager bf16 loop of the workload's
+    strategy), with the workload's param dtype, cautious wd 0.1 and Nesterov 0.95.
+
+    Small workloads (plumbing, GPT-2: at most 64 matrices) are stepped whole: one warm-up
+    step, then steps until min_seconds (at least 3), median step time. Larger ones are
+    sampled: one matrix of each distinct shape, whole passes over the shapes until
+    min_seconds (10-30 s of CPU work on the bench host), and the full step extrapolated
+    from each shape's median time times its count. Reported as orthogonalization TFLOP/s
+    of the measured steps (their symmetric-minimal FLOPs over their summed time)."""
+    import statistics
+
     import torch
 
     from oracle import muon_ref
 
+    strategy, pdtype = _config_hparams(config)
     threads = len(os.sched_getaffinity(0))
     threads = min(threads, int(os.environ.get("OMP_NUM_THREADS", threads)))
     torch.set_num_threads(threads)
@@ -88,14 +106,47 @@ def cpu_baseline(config: str = "llama", min_seconds: float = 10.0) -> dict:
     for s in shapes:  # a stacked (experts, rows, cols) tensor counts as its matrices
         key = tuple(s[-2:])
         counts[key] = counts.get(key, 0) + math.prod(s[:-2])
-    warm = torch.randn(256, 512, generator=gen).bfloat16()
-    muon_ref.MuonRef([warm], lr=1e-3, wd=0.1, strategy="polar_express").step([warm.clone()])
+    hp = dict(lr=1e-3, wd=0.1, use_cautious_wd=True, momentum=0.95, nesterov=True,
+              strategy=strategy)
+
+    def grad_like(shape):
+        z = torch.randn(*shape[:-1], 1, generator=gen)
+        return (torch.randn(shape, generator=gen) * torch.exp(z)).to(pdtype)
+
+    try:
+        cpu = open("/proc/cpuinfo").read().split("model name")[1].split("\n")[0].strip(" :\t")
+    except Exception:
+        cpu = "unknown"
+    direct = sum(counts.values()) <= 64
+    if direct:
+        params = [torch.randn(s, generator=gen).to(pdtype) for s in shapes]
+        grads = [grad_like(s) for s in shapes]
+        ref = muon_ref.MuonRef(params, **hp)
+        ref.step(grads)  # warm-up (state allocation, first-call costs)
+        times = []
+        while len(times) < 3 or (sum(times) < min_seconds and len(times) < 20000):
+            t0 = time.perf_counter()
+            ref.step(grads)
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        flops = sum(orth_flops(s, 5) for s in shapes)
+        return {
+            "value": round(flops / med / 1e12, 6),
+            "unit": "TFLOP/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": (f"oracle per-parameter Muon step (eager bf16 {strategy} 5, cautious wd, "
+                       f"Nesterov, {str(pdtype).replace('torch.', '')} params) over the whole "
+                       f"set of {len(shapes)} tensors: median of {len(times)} steps after one "
+                       f"warm-up ({sum(times):.1f} s); CPU: {cpu}"),
+            "ms_per_step": round(med * 1e3, 3),
+        }
+    warm = torch.randn(256, 512, generator=gen).to(pdtype)
+    muon_ref.MuonRef([warm], **hp).step([warm.clone()])
     cases = []
     for shape in counts:
-        p = torch.randn(shape, generator=gen).bfloat16()
-        z = torch.randn(*shape[:-1], 1, generator=gen)
-        g = (torch.randn(shape, generator=gen) * torch.exp(z)).bfloat16()
-        cases.append((shape, muon_ref.MuonRef([p], lr=1e-3, wd=0.1, strategy="polar_express"), g))
+        p = torch.randn(shape, generator=gen).to(pdtype)
+        cases.append((shape, muon_ref.MuonRef([p], **hp), grad_like(shape)))
     # Whole passes over the distinct shapes until at least min_seconds of CPU work.
     per_shape = {shape: [] for shape in counts}
     total_s, total_flops, passes = 0.0, 0.0, 0
@@ -110,23 +161,120 @@ def cpu_baseline(config: str = "llama", min_seconds: float = 10.0) -> dict:
         passes += 1
     full_s, parts = 0.0, []
     for shape, count in counts.items():
-        mean = sum(per_shape[shape]) / len(per_shape[shape])
-        full_s += mean * count
-        parts.append(f"{'x'.join(map(str, shape))}: {mean * 1e3:.0f} ms")
-    try:
-        cpu = open("/proc/cpuinfo").read().split("model name")[1].split("\n")[0].strip(" :\t")
-    except Exception:
-        cpu = "unknown"
+        med = statistics.median(per_shape[shape])
+        full_s += med * count
+        parts.append(f"{'x'.join(map(str, shape))}: {med * 1e3:.0f} ms")
     return {
         "value": round(total_flops / total_s / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle per-parameter Muon step (bf16 Polar Express 5, cautious wd, "
-                   f"Nesterov) on one bf16 matrix of each distinct shape, {passes} passes "
-                   f"({'; '.join(parts)} mean per step; {total_s:.1f} s); CPU: {cpu}"),
+        "sample": (f"oracle per-parameter Muon step (eager bf16 {strategy} 5, cautious wd, "
+                   f"Nesterov, {str(pdtype).replace('torch.', '')} params) on one matrix of each "
+                   f"distinct shape, {passes} passes ({'; '.join(parts)} median per step; "
+                   f"{total_s:.1f} s); CPU: {cpu}"),
         "extrapolated_ms_per_step": round(full_s * 1e3, 1),
     }
+
+
+def _median_ms(fn, reps: int = 50, warmup: int = 5, flush=None) -> float:
+    """Median of `reps` timings of fn() with hipEvents on the current stream, the way the
+    reference's harness times (triton.testing.do_bench, return_mode="median"): the
+    caches are flushed by a 512 MB fill before every timed call (larger than the MI355X's
+    256 MB last-level cache)."""
+    import statistics
+
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(reps):
+        if flush is not None:
+            flush.zero_()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        e1.synchronize()
+        samples.append(e0.elapsed_time(e1))
+    return statistics.median(samples)
+
+
+def reference_suite(dev) -> dict:
+    """The reference's own published single-device benchmarks (benchmark/RESULTS.md:18-37),
+    on this GPU and this library, timed as the reference times them (median, caches
+    flushed):
+
+    * Gram of a (32, 2048, 1024) bf16 batch (bench_kernels.py:22-72): muonium_amd's
+      `gram` next to hipBLASLt's dense x @ x^T (x^T made contiguous beforehand);
+    * Newton-Schulz and Polar Express loops, 5 steps on (32, 2048, 1024) bf16
+      (bench_kernels.py:75-132): `ns_loop` / `pe_loop`;
+    * one optimizer.step() on the _QUICK set (bench_optim.py:28-33, 137-179): 16 fp32
+      matrices, 4 each of 512x512, 512x1536, 512x2048, 2048x512, use_cautious_wd=False,
+      lr 1e-3, wd 0.1, momentum 0.95, Nesterov, 5 steps; the grads are refilled inside the
+      timed call as the reference's _step_fn does; per-parameter and foreach drivers,
+      both strategies.
+
+    The reference's numbers are from an NVIDIA RTX PRO 6000 Blackwell Max-Q (CUDA 13.0,
+    PyTorch 2.12.1), not from an MI355X; they are reported beside ours, not divided."""
+    import torch
+
+    from muonium_amd import Muon
+    from muonium_amd.kernels.gram import gram
+    from muonium_amd.orthogonalize.newton_schulz import ns_loop
+    from muonium_amd.orthogonalize.polar_express import pe_loop
+
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(32, 2048, 1024, device=dev, generator=gen).bfloat16()
+    xt = x.mT.contiguous()
+    t_ours = _median_ms(lambda: gram(x), flush=flush)
+    t_blas = _median_ms(lambda: torch.bmm(x, xt), flush=flush)
+    sym = 32 * 2048 * 2049 * 1024  # upper triangle, symmetric-minimal
+    out["gram_32x2048x1024_bf16"] = {
+        "ms": round(t_ours, 4), "tflops_symmetric_minimal": round(sym / t_ours / 1e9, 1),
+        "hipblaslt_dense_ms": round(t_blas, 4),
+        "reference_ms": {"triton_gram": 0.6077, "torch_x_xT": 1.1234},
+    }
+    loop_flops = 32 * 5 * (1024 * 1025 * 2048 + 1024 * 1025 * 1024 + 2 * 1024 * 1024 * 2048)
+    for name, fn, ref_ms in (("ns_loop", ns_loop, {"eager": 12.7727, "compiled": 10.1110,
+                                                   "triton": 9.3620}),
+                             ("pe_loop", pe_loop, {"eager": 12.7811, "compiled": 10.1018,
+                                                   "triton": 9.3657})):
+        t = _median_ms(lambda: fn(x, 5), flush=flush)
+        out[f"{name}_5steps_32x2048x1024_bf16"] = {
+            "ms": round(t, 4), "tflops_symmetric_minimal": round(loop_flops / t / 1e9, 1),
+            "reference_ms": ref_ms,
+        }
+    del x, xt
+    shapes = [(512, 512)] * 4 + [(512, 1536)] * 4 + [(512, 2048)] * 4 + [(2048, 512)] * 4
+    ref_step = {("newton_schulz", False): 9.3614, ("polar_express", False): 9.5561,
+                ("newton_schulz", True): 2.4483, ("polar_express", True): 2.6481}
+    for (strategy, foreach), ref_ms in ref_step.items():
+        g1 = torch.Generator(device=dev).manual_seed(1)
+        g0 = torch.Generator(device=dev).manual_seed(0)
+        params = [torch.nn.Parameter(torch.randn(*s, device=dev, generator=g1)) for s in shapes]
+        grads = [torch.randn(*s, device=dev, generator=g0) for s in shapes]
+        opt = Muon(params, foreach=foreach, lr=1e-3, wd=0.1, momentum=0.95, nesterov=True,
+                   ns_steps=5, use_cautious_wd=False, orthogonalization_strategy=strategy)
+
+        def step():
+            for p, g in zip(params, grads):
+                p.grad = g.clone()
+            opt.step()
+
+        t = _median_ms(step, flush=flush)
+        key = f"quick_step_{'foreach' if foreach else 'per_param'}_{strategy}"
+        out[key] = {"ms": round(t, 4), "reference_ms": ref_ms}
+        del opt, params, grads
+    torch.cuda.empty_cache()
+    return {"reference_suite": "benchmark/RESULTS.md:18-37 workloads on MI355X",
+            "reference_hardware": "NVIDIA RTX PRO 6000 Blackwell Max-Q, CUDA 13.0, PyTorch 2.12.1",
+            "results": out}
 
 
 def blas_ceiling(config: str, dev, reps: int = 3) -> dict:
@@ -201,7 +349,9 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="llama", choices=sorted(CONFIGS))
     ap.add_argument("--lp", default=None, choices=["8bit", "4bit", "fp8"])
-    ap.add_argument("--block-size", type=int, default=None)
+    ap.add_argument("--block-size", default=None,
+                    help="MuonLP block size (default 256, 4-bit 128), or 'tensor' for one "
+                         "scale per tensor")
     ap.add_argument("--strategy", default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -209,6 +359,9 @@ def main() -> None:
     ap.add_argument("--blas-ceiling", action="store_true",
                     help="only time the iteration's three products per bucket with torch.bmm "
                          "(hipBLASLt) as a library reference")
+    ap.add_argument("--reference-suite", action="store_true",
+                    help="only run the reference's own published single-device benchmarks "
+                         "(Gram, NS/PE loops, the 16-matrix step) and print their times")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -237,11 +390,13 @@ def main() -> None:
     if args.blas_ceiling:
         print(json.dumps(blas_ceiling(args.config, dev)), flush=True)
         return
+    if args.reference_suite:
+        print(json.dumps(reference_suite(dev)), flush=True)
+        return
     shapes = _shapes(args.config)
-    strategy = args.strategy or ("newton_schulz" if args.config in ("moe", "moe_flat", "plumbing")
-                                 else "polar_express")
+    strategy, pdtype = _config_hparams(args.config)
+    strategy = args.strategy or strategy
     flatten = args.config == "moe_flat"
-    pdtype = torch.float32 if args.config == "plumbing" else torch.bfloat16
     print(f"[bench] config={args.config} tensors={len(shapes)} strategy={strategy} "
           f"lp={args.lp}", file=sys.stderr, flush=True)
 
@@ -263,7 +418,10 @@ def main() -> None:
     groups = [{"params": params, "flatten": flatten}]  # flatten is a group key
     if args.lp:
         cls = {"8bit": Muon8bit, "4bit": Muon4bit, "fp8": MuonFp8}[args.lp]
-        block = args.block_size or {"8bit": 256, "4bit": 128, "fp8": 256}[args.lp]
+        if args.block_size == "tensor":
+            block = None  # one scale per tensor
+        else:
+            block = int(args.block_size or {"8bit": 256, "4bit": 128, "fp8": 256}[args.lp])
         opt = cls(groups, foreach=True, block_size=block, **kw)
     else:
         opt = Muon(groups, foreach=args.config != "plumbing", **kw)
@@ -278,17 +436,21 @@ def main() -> None:
     _lib.timing_enable(True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record()
+    # one event between consecutive steps (no synchronization inside the timed region):
+    # the mean over the K steps is ms_per_step, their median is reported beside it
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    evs[0].record()
     for i in range(args.steps):
         opt.step()
-    ev1.record()
+        evs[i + 1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     kern = _lib.timing_read()
     _lib.timing_enable(False)
-    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    ms_per_step = evs[0].elapsed_time(evs[-1]) / args.steps
+    step_ms = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps))
+    median_ms = step_ms[len(step_ms) // 2] if len(step_ms) % 2 else \
+        0.5 * (step_ms[len(step_ms) // 2 - 1] + step_ms[len(step_ms) // 2])
     print(f"[bench] {args.steps} steps: {ms_per_step:.2f} ms/step (wall {wall:.2f}s)",
           file=sys.stderr, flush=True)
 
@@ -308,7 +470,14 @@ def main() -> None:
             entry.update(tflops=round(tf, 1), frac=round(tf / PEAK_BF16_TFLOPS, 4))
         elif k in ("prepass", "postpass", "lp_prepass"):
             gbs = work / (ms * 1e-3) / 1e9
-            entry.update(gbs=round(gbs, 1), frac=round(gbs / PEAK_HBM_GBS, 4))
+            entry.update(gbs=round(gbs, 1), frac=round(gbs / PEAK_HBM_GBS, 4),
+                         bytes_per_elem=round(work / (numel * args.steps), 3))
+            if k == "prepass" and work > 12.5 * numel * args.steps:
+                # the pre-pass also writes the Nesterov g' back into the gradients (2 B per
+                # bf16 value, the foreach driver's in-place update); without that write it
+                # moves the survey's 12 B per value (g 2 + m 4 in, m 4 + X 2 out)
+                gbs12 = 12.0 * numel * args.steps / (ms * 1e-3) / 1e9
+                entry.update(gbs_12B=round(gbs12, 1), frac_12B=round(gbs12 / PEAK_HBM_GBS, 4))
         kernels[k] = entry
 
     gms, gn, gwork = kern["gemm_bx"]
@@ -335,14 +504,18 @@ def main() -> None:
         }
     else:
         achieved = (gwork / max(gn, 1)) / (avg_ms * 1e-3) / 1e12
-        traffic, traffic_src = _measured_traffic("gemm_bf16_nn4_kernel", args.config, args.lp)
+        # the optimizer iterates in bf16 whatever the params' dtype (zeropower casts to
+        # bf16, orthogonalize.py:101-102), so fp32 params (plumbing) run this kernel too
+        kname = "gemm_bf16_nn4_kernel"
+        peak = PEAK_BF16_TFLOPS
+        traffic, traffic_src = _measured_traffic(kname, args.config, args.lp)
         roofline = {
             "bound": "mfma",
-            "kernel": "gemm_bf16_nn4_kernel (X' = a X + B X)",
+            "kernel": f"{kname} (X' = a X + B X)",
             "achieved": round(achieved, 1),
-            "peak": PEAK_BF16_TFLOPS,
+            "peak": peak,
             "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "frac": round(achieved / peak, 4),
             "traffic": traffic,
             "traffic_source": traffic_src,
             "avg_launch_ms": round(avg_ms, 4),
@@ -350,6 +523,9 @@ def main() -> None:
         }
     upd_ms = sum(kern[k][0] for k in ("prepass", "postpass", "lp_prepass")) / args.steps
     upd_bytes = sum(kern[k][2] for k in ("prepass", "postpass", "lp_prepass")) / args.steps
+    # the survey's convention for the fp32-momentum passes: 18 B per bf16 value
+    # (pre 12 + post 6), without the pre-pass's write-back of g' into the gradients
+    upd_bytes18 = 18.0 * numel if (not args.lp and pdtype == torch.bfloat16) else None
 
     cpu = None
     # the oracle's per-parameter loop restates the per-matrix problem; it is not run for
@@ -367,17 +543,19 @@ def main() -> None:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 3),
+        "median_ms_per_step": round(median_ms, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp32" if pdtype == torch.float32 else "bf16",
         "data": "synthetic (seeded N(0,1) gradients with per-row log-normal scales; random-init bf16 params)",
         "config": {
-            "workload": label + (f"; MuonLP {args.lp}" if args.lp else ""),
+            "workload": label + (f"; MuonLP {args.lp}, block {block or 'per tensor'}"
+                                 if args.lp else ""),
             "params": numel,
             "strategy": strategy,
             "ns_steps": 5,
-            "foreach": True,
+            "foreach": args.config != "plumbing",
             "momentum_dtype": (args.lp or "fp32"),
             "orth_tflop_per_step": round(flops_step / 1e12, 3),
         },
@@ -385,6 +563,9 @@ def main() -> None:
         "orth_kernel_tflops": round(flops_step / (orth_ms * 1e-3) / 1e12, 1) if orth_ms else None,
         "update_kernel_ms_per_step": round(upd_ms, 3),
         "update_kernel_gbs": round(upd_bytes / (upd_ms * 1e-3) / 1e9, 1) if upd_ms else None,
+        "update_kernel_bytes_per_elem": round(upd_bytes / numel, 3),
+        "update_kernel_gbs_18B": (round(upd_bytes18 / (upd_ms * 1e-3) / 1e9, 1)
+                                  if upd_ms and upd_bytes18 else None),
         "kernels": kernels,
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -213,6 +213,13 @@ int muon_gram(const void* x, void* y, int dtype, int64_t batch, int64_t M, int64
   if (K == 0)  // an empty contraction: y = 0 (x is never read)
     return muon_launch_zero(y, batch * M * M * (dtype == MUON_DT_F32 ? 4 : 2),
                             (hipStream_t)stream);
+  if (dtype == MUON_DT_BF16 && M % PAD == 0 && K % 64 == 0 && !((uintptr_t)x & 15) &&
+      !((uintptr_t)y & 15))
+    // whole 256-row tiles and 64-wide K-tiles: the iteration's SYRK reads the caller's
+    // operands in place
+    return muon_launch_gemm(dtype, MODE_SYRK, false, batch, M, M, K, x, K, M * K, x, K, M * K,
+                            nullptr, 0, 0, y, M, M * M, nullptr, 0, 0, M, M, 1.0f, 0.0f,
+                            nullptr, 0, (hipStream_t)stream);
   return muon_launch_gemm(dtype, MODE_SYRK, true, batch, M, M, K, x, K,
                           M * K, x, K, M * K, nullptr, 0, 0, y, M, M * M, nullptr, 0, 0, M, M,
                           1.0f, 0.0f, nullptr, 0, (hipStream_t)stream);

@@ -106,32 +106,43 @@ def test_full_size_step_bit_exact_given_u(shape):
     assert torch.equal(got, ref_p), f"{(got.float() - ref_p.float()).abs().max().item():.3e}"
 
 
-def test_full_size_lp_prepass_codes_bit_exact():
+@pytest.mark.parametrize("fmt,block", [("8bit", 256), ("8bit", 2048), ("fp8", None)],
+                         ids=["8bit-b256", "8bit-b2048", "fp8-per-tensor"])
+def test_full_size_lp_prepass_codes_bit_exact(fmt, block):
+    """Config 5's quantized momentum on a gate-sized (14336 x 4096) tensor: 8-bit at the
+    bench's block 256 and at the reference's default block 2048 (deferred scales), and
+    fp8 with one scale for the whole tensor."""
     from muonium_amd import _lib
+    from muonium_amd.optim.lp_state import OptimStateFp8
 
     lib = _lib.load()
     dev = torch.device(DEV)
     _lib.ensure_device(dev)
-    rows, cols, block = 14336, 4096, 256
+    rows, cols = 14336, 4096
+    block = block or rows * cols
     gen = torch.Generator().manual_seed(23)
     g = (torch.randn(rows, cols, generator=gen)
          * torch.exp(torch.randn(rows, 1, generator=gen))).bfloat16()
-    st = OptimState8bit.zeros((rows, cols), True, block, DEV)
+    if fmt == "fp8":
+        st = OptimStateFp8.zeros((rows, cols), block, DEV)
+    else:
+        st = OptimState8bit.zeros((rows, cols), True, block, DEV)
     ws = torch.empty(lib.muon_orth_workspace_bytes(_lib.DT_BF16, 1, rows, cols), dtype=torch.uint8,
                      device=dev)
     gd = g.to(dev)
     codes = np.zeros(st.codes.numel(), np.uint8)
     scales = np.zeros(st.scale.numel(), np.float32)
-    qmap = quant_ref.qmap_8bit(True)
+    qmap = quant_ref.qmap_8bit(True) if fmt == "8bit" else None
     for step in range(2):
         rc = lib.muon_lp_prepass(1, _lib.ptr_array([gd]), _lib.DT_BF16, _lib.ptr_array([st.codes]),
-                                 _lib.ptr_array([st.scale]), st.qmap.data_ptr(), st.qformat, block,
+                                 _lib.ptr_array([st.scale]),
+                                 st.qmap.data_ptr() if st.qmap is not None else None, st.qformat, block,
                                  1, rows, cols, 0.95, 1, 0, ws.data_ptr(), _lib.DT_BF16, 1,
                                  _lib.stream(dev))
         assert rc == 0, _lib.last_error()
         torch.cuda.synchronize()
         codes, scales, _ = quant_ref.lp_momentum_step(
-            codes, scales, g.float().numpy(), block=block, fmt="8bit", qmap=qmap, momentum=0.95,
+            codes, scales, g.float().numpy(), block=block, fmt=fmt, qmap=qmap, momentum=0.95,
             nesterov=True, maximize=False)
         assert np.array_equal(st.codes.cpu().numpy(), codes), f"codes differ at step {step}"
         assert np.array_equal(st.scale.cpu().numpy().view(np.uint32), scales.view(np.uint32))

@@ -24,6 +24,9 @@ SHAPES = [
     (4, 1, 1),
     (4, 64, 1024),
     (2, 520, 300),
+    # whole 256-row tiles, K a multiple of 64: the SYRK reads the caller's tensors in place
+    (3, 512, 320),
+    (2, 2048, 1024),
 ]
 
 
@@ -44,9 +47,10 @@ def test_gram_matches_oracle(shape, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_gram_output_is_exactly_symmetric(dtype):
+@pytest.mark.parametrize("shape", [(4, 300, 70), (2, 512, 320)])
+def test_gram_output_is_exactly_symmetric(dtype, shape):
     gen = torch.Generator().manual_seed(42)
-    x = torch.randn(4, 300, 70, generator=gen).to(dtype).cuda()
+    x = torch.randn(*shape, generator=gen).to(dtype).cuda()
     y = gram(x)
     assert torch.equal(y, y.mT)
 
