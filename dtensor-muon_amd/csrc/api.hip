@@ -169,6 +169,41 @@ OrthLayout muon_orth_layout(int dtype, int64_t batch, int64_t rows, int64_t cols
   return L;
 }
 
+// ---- static scratch of the allocation-free entry point -------------------------------
+// One array per GPU (each device holds its own copy of a __device__ variable), held until
+// the process ends. Host code must not use the array's name as a device address: its
+// address on each device comes from hipGetSymbolAddress, looked up once per device with
+// that device current (muon_amd_init, else the entry point's first call on the device).
+static __device__ __align__(256) unsigned char scratch[MUON_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Address of the current device's scratch array (looked up on first use per device).
+int current_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    muon_set_error("scratch: no usable current HIP device (%d)", dev);
+    return MUON_ERR_DEVICE;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      muon_set_error("scratch: hipGetSymbolAddress failed on device %d: %s", dev,
+                     hipGetErrorString(e));
+      return MUON_ERR_DEVICE;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MUON_OK;
+}
+}  // namespace
+
 static bool iter_dtype_ok(int dt) { return dt == MUON_DT_BF16 || dt == MUON_DT_F32; }
 static bool io_dtype_ok(int dt) {
   return dt == MUON_DT_BF16 || dt == MUON_DT_F32 || dt == MUON_DT_F16;
@@ -196,7 +231,8 @@ int muon_amd_init(void) {
                    prop.gcnArchName);
     return MUON_ERR_DEVICE;
   }
-  return MUON_OK;
+  void* sp = nullptr;
+  return current_scratch(&sp);  // this device's static scratch address, once
 }
 
 int muon_gram(const void* x, void* y, int dtype, int64_t batch, int64_t M, int64_t K,
@@ -469,6 +505,64 @@ int muon_postpass(int ntensors, void* const* params, int p_dtype, const void* u,
   return MUON_OK;
 }
 
+// NorMuon post-pass on an update U at ubase (pitch / matrix stride in elements; trans: a
+// tall result in the workspace's wide layout), with the per-row statistics in ss (one
+// float per stored row, ss_mst floats per matrix, at least chunk x nb matrices, reused by
+// each chunk of MUON_MAX_TENSORS tensors in stream order). Every ss value the kernels
+// read is written first, so ss needs no clearing.
+static int normuon_postpass_on(int ntensors, void* const* params, int p_dtype,
+                               void* const* variances, int v_dtype, const char* ubase, int udt,
+                               int64_t pitch, int64_t mst, int trans, float* ss, int64_t ss_mst,
+                               int64_t nb, int64_t rows, int64_t cols, const int64_t* starts,
+                               int nb_split, const float* adjusted_lrs, float wd, int cautious,
+                               double beta2, hipStream_t s) {
+  const int es = udt == MUON_DT_F32 ? 4 : 2;
+  const int pes = p_dtype == MUON_DT_F32 ? 4 : 2;
+  const float w = (float)(1.0 - beta2);
+  Timed timed(MUON_K_POSTPASS, (2.0 * es + 2.0 * pes) * (double)ntensors * nb * rows * cols, s);
+  for (int t0 = 0; t0 < ntensors; t0 += MUON_MAX_TENSORS) {
+    const int cnt = std::min(MUON_MAX_TENSORS, ntensors - t0);
+    const char* uc = ubase + (int64_t)t0 * nb * mst * es;
+    int rc = muon_launch_normuon_stats(cnt, variances + t0, v_dtype, uc, udt, pitch, mst, trans,
+                                       nb, rows, cols, ss, ss_mst, starts, nb_split, w, s);
+    if (rc != MUON_OK) return rc;
+    rc = muon_launch_postpass(cnt, params + t0, adjusted_lrs + t0, p_dtype, uc, udt, pitch, mst,
+                              trans, ss, ss_mst, nullptr, nb, rows, cols, wd, cautious, s);
+    if (rc != MUON_OK) return rc;
+  }
+  return MUON_OK;
+}
+
+// Row-block offsets of a NorMuon call: the whole matrix, or split_sizes summing to rows.
+static int normuon_row_blocks(const char* who, const int64_t* split_sizes, int nsplits,
+                              int64_t rows, int64_t* starts, int* nb_split) {
+  *nb_split = 1;
+  starts[0] = 0;
+  starts[1] = rows;
+  if (!split_sizes || nsplits <= 0) return MUON_OK;
+  if (nsplits > MUON_MAX_SPLITS) {
+    muon_set_error("%s: %d row blocks exceed the maximum %d", who, nsplits, MUON_MAX_SPLITS);
+    return MUON_ERR_ARG;
+  }
+  int64_t acc = 0;
+  for (int i = 0; i < nsplits; ++i) {
+    if (split_sizes[i] <= 0) {
+      muon_set_error("%s: row block %d has size %lld", who, i, (long long)split_sizes[i]);
+      return MUON_ERR_SHAPE;
+    }
+    starts[i] = acc;
+    acc += split_sizes[i];
+  }
+  if (acc != rows) {
+    muon_set_error("%s: row blocks sum to %lld, not %lld rows", who, (long long)acc,
+                   (long long)rows);
+    return MUON_ERR_SHAPE;
+  }
+  starts[nsplits] = rows;
+  *nb_split = nsplits;
+  return MUON_OK;
+}
+
 int muon_normuon_postpass(int ntensors, void* const* params, int p_dtype,
                           void* const* variances, int v_dtype, const void* u, int u_dtype,
                           void* ws, int ws_dtype, int64_t ws_batch, int steps, int64_t nb,
@@ -489,35 +583,10 @@ int muon_normuon_postpass(int ntensors, void* const* params, int p_dtype,
                    (long long)ntensors * nb);
     return MUON_ERR_ARG;
   }
-  // row blocks: the whole matrix, or split_sizes summing to rows
   int64_t starts[MUON_MAX_SPLITS + 1];
-  int nb_split = 1;
-  starts[0] = 0;
-  starts[1] = rows;
-  if (split_sizes && nsplits > 0) {
-    if (nsplits > MUON_MAX_SPLITS) {
-      muon_set_error("normuon_postpass: %d row blocks exceed the maximum %d", nsplits,
-                     MUON_MAX_SPLITS);
-      return MUON_ERR_ARG;
-    }
-    int64_t acc = 0;
-    for (int i = 0; i < nsplits; ++i) {
-      if (split_sizes[i] <= 0) {
-        muon_set_error("normuon_postpass: row block %d has size %lld", i,
-                       (long long)split_sizes[i]);
-        return MUON_ERR_SHAPE;
-      }
-      starts[i] = acc;
-      acc += split_sizes[i];
-    }
-    if (acc != rows) {
-      muon_set_error("normuon_postpass: row blocks sum to %lld, not %lld rows", (long long)acc,
-                     (long long)rows);
-      return MUON_ERR_SHAPE;
-    }
-    starts[nsplits] = rows;
-    nb_split = nsplits;
-  }
+  int nb_split;
+  int rc = normuon_row_blocks("normuon_postpass", split_sizes, nsplits, rows, starts, &nb_split);
+  if (rc != MUON_OK) return rc;
   OrthLayout L = muon_orth_layout(ws_dtype, ws_batch, rows, cols);
   const char* ubase;
   int udt, trans = 0;
@@ -533,30 +602,57 @@ int muon_normuon_postpass(int ntensors, void* const* params, int p_dtype,
     mst = rows * cols;
   } else {
     int64_t off;
-    int rc = muon_orth_result(ws_dtype, ws_batch, rows, cols, steps, &off, &pitch, &mst, &trans);
+    rc = muon_orth_result(ws_dtype, ws_batch, rows, cols, steps, &off, &pitch, &mst, &trans);
     if (rc != MUON_OK) return rc;
     ubase = (const char*)ws + off;
     udt = ws_dtype;
   }
-  const int es = udt == MUON_DT_F32 ? 4 : 2;
-  const int pes = p_dtype == MUON_DT_F32 ? 4 : 2;
-  hipStream_t s = (hipStream_t)stream;
-  float* ss = (float*)((char*)ws + L.off_rows);
-  const int64_t ss_mst = L.n_pad;  // stored rows <= n <= n_pad
-  const float w = (float)(1.0 - beta2);
-  Timed timed(MUON_K_POSTPASS, (2.0 * es + 2.0 * pes) * (double)ntensors * nb * rows * cols, s);
-  for (int t0 = 0; t0 < ntensors; t0 += MUON_MAX_TENSORS) {
-    const int cnt = std::min(MUON_MAX_TENSORS, ntensors - t0);
-    const char* uc = ubase + (int64_t)t0 * nb * mst * es;
-    float* ssc = ss + (int64_t)t0 * nb * ss_mst;
-    int rc = muon_launch_normuon_stats(cnt, variances + t0, v_dtype, uc, udt, pitch, mst, trans,
-                                       nb, rows, cols, ssc, ss_mst, starts, nb_split, w, s);
-    if (rc != MUON_OK) return rc;
-    rc = muon_launch_postpass(cnt, params + t0, adjusted_lrs + t0, p_dtype, uc, udt, pitch, mst,
-                              trans, ssc, ss_mst, nullptr, nb, rows, cols, wd, cautious, s);
-    if (rc != MUON_OK) return rc;
+  float* ss = (float*)((char*)ws + L.off_rows);  // stored rows <= n <= n_pad per matrix
+  return normuon_postpass_on(ntensors, params, p_dtype, variances, v_dtype, ubase, udt, pitch,
+                             mst, trans, ss, L.n_pad, nb, rows, cols, starts, nb_split,
+                             adjusted_lrs, wd, cautious, beta2, (hipStream_t)stream);
+}
+
+int muon_normuon_postpass_noalloc(int ntensors, void* const* params, int p_dtype,
+                                  void* const* variances, int v_dtype, const void* u,
+                                  int u_dtype, int64_t nb, int64_t rows, int64_t cols,
+                                  const int64_t* split_sizes, int nsplits,
+                                  const float* adjusted_lrs, float wd, int cautious,
+                                  double beta2, void* stream) {
+  if (!io_dtype_ok(p_dtype) || !io_dtype_ok(v_dtype) || !io_dtype_ok(u_dtype)) {
+    muon_set_error("normuon_postpass_noalloc: unsupported dtype (param %d, variance %d, u %d)",
+                   p_dtype, v_dtype, u_dtype);
+    return MUON_ERR_DTYPE;
   }
-  return MUON_OK;
+  if (ntensors < 0 || nb <= 0 || rows <= 0 || cols <= 0) {
+    muon_set_error("normuon_postpass_noalloc: bad extents");
+    return MUON_ERR_SHAPE;
+  }
+  if (!u) {
+    muon_set_error("normuon_postpass_noalloc: the update u is required");
+    return MUON_ERR_ARG;
+  }
+  // one float per stored row of each matrix of a chunk of MUON_MAX_TENSORS tensors
+  const int64_t need = (int64_t)std::min(ntensors, MUON_MAX_TENSORS) * nb * rows * 4;
+  if (need > MUON_NOALLOC_SCRATCH_BYTES) {
+    muon_set_error("normuon_postpass_noalloc: %lld bytes of row statistics exceed the %d-byte "
+                   "scratch (at most %d tensors per chunk x nb x rows x 4 B)",
+                   (long long)need, MUON_NOALLOC_SCRATCH_BYTES, MUON_MAX_TENSORS);
+    return MUON_ERR_SHAPE;
+  }
+  int64_t starts[MUON_MAX_SPLITS + 1];
+  int nb_split;
+  int rc = normuon_row_blocks("normuon_postpass_noalloc", split_sizes, nsplits, rows, starts,
+                              &nb_split);
+  if (rc != MUON_OK) return rc;
+  if (ntensors == 0) return MUON_OK;
+  void* sp = nullptr;
+  rc = current_scratch(&sp);
+  if (rc != MUON_OK) return rc;
+  return normuon_postpass_on(ntensors, params, p_dtype, variances, v_dtype, (const char*)u,
+                             u_dtype, cols, rows * cols, 0, (float*)sp, rows, nb, rows, cols,
+                             starts, nb_split, adjusted_lrs, wd, cautious, beta2,
+                             (hipStream_t)stream);
 }
 
 int muon_lp_prepass(int ntensors, void* const* grads, int g_dtype, void* const* codes,

@@ -160,6 +160,25 @@ int muon_normuon_postpass(int ntensors, void* const* params, int p_dtype,
                           const float* adjusted_lrs, float wd, int cautious, double beta2,
                           void* stream);
 
+/* ---- Allocation-free NorMuon post-pass ------------------------------------------------
+ * No counterpart in the reference: for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving or training loops, harnesses that forbid
+ * hipMalloc). Same arithmetic and results as muon_normuon_postpass with an explicit update
+ * u (required here) and no workspace: the per-row statistics live in a static device array
+ * of MUON_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends. A call needs
+ * min(ntensors, MUON_MAX_TENSORS) * nb * rows * 4 bytes of it and is refused with
+ * MUON_ERR_SHAPE beyond (rows up to 131072 for 32 single-matrix tensors). Nothing is
+ * allocated and nothing needs clearing between calls (every value read is written first
+ * by the same call). All calls on one GPU share its array: calls that overlap in time on
+ * one GPU (on different streams) race and must be serialized by the caller. */
+#define MUON_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+int muon_normuon_postpass_noalloc(int ntensors, void* const* params, int p_dtype,
+                                  void* const* variances, int v_dtype, const void* u,
+                                  int u_dtype, int64_t nb, int64_t rows, int64_t cols,
+                                  const int64_t* split_sizes, int nsplits,
+                                  const float* adjusted_lrs, float wd, int cautious,
+                                  double beta2, void* stream);
+
 /* ---- Quantized momentum (MuonLP) -------------------------------------------------
  * State of one tensor of `numel` values: codes (uint8; numel bytes for 8-bit and
  * fp8, numel/2 for 4-bit with element 2i in the high nibble) and one fp32 scale per
