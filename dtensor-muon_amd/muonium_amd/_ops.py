@@ -12,7 +12,7 @@ import ctypes
 import threading
 
 import numpy as np
-from typing import Sequence
+from typing import Optional, Sequence
 
 import torch
 from torch import Tensor
@@ -107,16 +107,39 @@ def coeffs_for(strategy: str, steps: int) -> tuple[list[tuple[float, float, floa
     raise ValueError(f"Unknown orthogonalization strategy: {strategy}")
 
 
-def _flat_coeffs(coeffs: Sequence[tuple[float, float, float]]):
-    return _lib.f64_array([c for abc in coeffs for c in abc])
+def _flat_coeffs(coeffs: Sequence[float]):
+    return _lib.f64_array(list(coeffs))
+
+
+def _flatten_coeffs(coeffs) -> list[float]:
+    """(a, b, c) triples -> [a0, b0, c0, a1, ...] (plain floats, as the ops take them)."""
+    return [float(c) for abc in coeffs for c in abc]
+
+
+def adjusted_lrs(lr_ratios: Sequence[Tensor], lr: Tensor | float) -> list[float]:
+    """lr_ratio * lr as the fp32 product of two 0-dim fp32 tensors (muon.py:71,115)."""
+    lr32 = np.float32(float(lr))
+    return [float(np.float32(float(r)) * lr32) for r in lr_ratios]
+
+
+def _as_tensor(lr) -> Tensor:
+    return lr if isinstance(lr, Tensor) else torch.tensor(float(lr))
+
+
+def _compiling() -> bool:
+    return torch.compiler.is_compiling()
 
 
 # ---------------------------------------------------------------------------------
-# gram
+# Device operations. Each runs its implementation (`_*_impl`) directly in eager mode.
+# While an outer torch.compile traces the step (optim.py:616-623: the reference then
+# runs its raw update inside the caller's graph), the same implementation is reached
+# through a torch.library custom op of namespace "muonium_amd", whose fake (meta)
+# implementation lets the tracer put the library call into the graph instead of
+# breaking it: the ops declare which tensor lists they write (mutates_args).
 
 
-def gram_(x: Tensor, y: Tensor) -> None:
-    """y = x x^T over the last two dims; x (B, M, K) and y (B, M, M) contiguous."""
+def _gram_impl(x: Tensor, y: Tensor) -> None:
     lib = _lib.load()
     _lib.ensure_device(x.device)
     B, M, K = matrix_view(x)
@@ -127,22 +150,16 @@ def gram_(x: Tensor, y: Tensor) -> None:
     )
 
 
-# ---------------------------------------------------------------------------------
-# orthogonalization of a list of same-shape tensors (zeropower / loop functions)
+def gram_(x: Tensor, y: Tensor) -> None:
+    """y = x x^T over the last two dims; x (B, M, K) and y (B, M, M) contiguous."""
+    if _compiling():
+        torch.ops.muonium_amd.gram_(x, y)
+    else:
+        _gram_impl(x, y)
 
 
-def orthogonalize(
-    tensors: Sequence[Tensor],
-    coeffs: Sequence[tuple[float, float, float]],
-    *,
-    prescale: float,
-    eps: float,
-    iter_dtype: torch.dtype,
-    out_dtype: torch.dtype,
-) -> Tensor:
-    """Run the polynomial iteration on every matrix of ``tensors`` (same shape, any
-    float dtype, cast to ``iter_dtype`` on the fly) and return the stacked result
-    of shape (len(tensors), *shape) in ``out_dtype``."""
+def _orthogonalize_impl(tensors: list[Tensor], coeffs: list[float], prescale: float, eps: float,
+                        iter_dtype: torch.dtype, out_dtype: torch.dtype) -> Tensor:
     lib = _lib.load()
     t0 = tensors[0]
     device = t0.device
@@ -156,7 +173,7 @@ def orthogonalize(
     ws, cap = workspace(device, iter_dtype, count * nb, rows, cols)
     wdt = _lib.dtype_code(iter_dtype)
     s = _lib.stream(device)
-    steps = len(coeffs)
+    steps = len(coeffs) // 3
     grads = _lib.ptr_array(tensors)
     _lib.check(
         lib.muon_prepass(count, grads, None, _lib.dtype_code(t0.dtype), 0, nb, rows, cols, 0.0,
@@ -176,21 +193,31 @@ def orthogonalize(
     return out
 
 
+def orthogonalize(
+    tensors: Sequence[Tensor],
+    coeffs: Sequence[tuple[float, float, float]],
+    *,
+    prescale: float,
+    eps: float,
+    iter_dtype: torch.dtype,
+    out_dtype: torch.dtype,
+) -> Tensor:
+    """Run the polynomial iteration on every matrix of ``tensors`` (same shape, any
+    float dtype, cast to ``iter_dtype`` on the fly) and return the stacked result
+    of shape (len(tensors), *shape) in ``out_dtype``."""
+    args = (list(tensors), _flatten_coeffs(coeffs), float(prescale), float(eps), iter_dtype,
+            out_dtype)
+    if _compiling():
+        return torch.ops.muonium_amd.orthogonalize(*args)
+    return _orthogonalize_impl(*args)
+
+
 # ---------------------------------------------------------------------------------
 # the Muon step pieces
 
 
-def adjusted_lrs(lr_ratios: Sequence[Tensor], lr: Tensor | float) -> list[float]:
-    """lr_ratio * lr as the fp32 product of two 0-dim fp32 tensors (muon.py:71,115)."""
-    lr32 = np.float32(float(lr))
-    return [float(np.float32(float(r)) * lr32) for r in lr_ratios]
-
-
-def momentum_only(
-    grads: Sequence[Tensor], bufs: Sequence[Tensor], *, momentum: float, nesterov: bool,
-    maximize: bool, write_back_grad: bool,
-) -> None:
-    """buf' = buf*mu + g (and, with write_back_grad, grad <- g + mu*buf') in place."""
+def _momentum_impl(grads: list[Tensor], bufs: list[Tensor], momentum: float, nesterov: bool,
+                   maximize: bool, write_back_grad: bool) -> None:
     lib = _lib.load()
     g0 = grads[0]
     _lib.ensure_device(g0.device)
@@ -205,23 +232,30 @@ def momentum_only(
     )
 
 
-def postpass(
-    params: Sequence[Tensor], us: Sequence[Tensor] | Tensor, lrs: Sequence[float], *,
-    weight_decay: float, cautious_wd: bool, shape=None,
+def momentum_only(
+    grads: Sequence[Tensor], bufs: Sequence[Tensor], *, momentum: float, nesterov: bool,
+    maximize: bool, write_back_grad: bool,
 ) -> None:
-    """p <- p - lr_t * (u + wd * p * [u*p > 0]) elementwise.
+    """buf' = buf*mu + g (and, with write_back_grad, grad <- g + mu*buf') in place."""
+    args = (list(grads), list(bufs), float(momentum), bool(nesterov), bool(maximize),
+            bool(write_back_grad))
+    if _compiling():
+        torch.ops.muonium_amd.momentum_only(*args)
+    else:
+        _momentum_impl(*args)
 
-    ``us`` is either one contiguous stacked tensor or a list of tensors with the
-    elements of each param in the same order; ``shape`` (default: the params') gives
-    the (…, rows, cols) matrix view."""
+
+def _postpass_impl(params: list[Tensor], us: list[Tensor], lr_ratios: list[Tensor], lr: Tensor,
+                   weight_decay: float, cautious_wd: bool, shape: list[int]) -> None:
     lib = _lib.load()
     p0 = params[0]
     _lib.ensure_device(p0.device)
     _check_cuda_contig(params, "params")
-    nb, rows, cols = matrix_view(p0 if shape is None else shape)
+    lrs = adjusted_lrs(lr_ratios, lr)
+    nb, rows, cols = matrix_view(shape)
     s = _lib.stream(p0.device)
-    if isinstance(us, Tensor):
-        chunks = [(list(range(len(params))), us)]
+    if len(us) == 1 and len(params) > 1:
+        chunks = [(list(range(len(params))), us[0])]  # one stacked tensor for every param
     else:
         chunks = [([i], u) for i, u in enumerate(us)]
     for idx, u in chunks:
@@ -236,37 +270,41 @@ def postpass(
         )
 
 
-def fused_step(
-    params: Sequence[Tensor],
-    grads: Sequence[Tensor],
-    bufs: Sequence[Tensor],
-    lrs: Sequence[float],
-    *,
-    momentum: float,
-    nesterov: bool,
-    maximize: bool,
-    write_back_grad: bool,
-    weight_decay: float,
-    cautious_wd: bool,
-    coeffs: Sequence[tuple[float, float, float]],
-    prescale: float,
-    eps: float = 1e-7,
-    u_scales: Sequence[float] | None = None,
+def postpass(
+    params: Sequence[Tensor], us: Sequence[Tensor] | Tensor, lr_ratios: Sequence[Tensor], lr, *,
+    weight_decay: float, cautious_wd: bool, shape=None,
 ) -> None:
-    """One Muon step over a same-shape bucket: momentum pre-pass into the batched bf16
-    workspace, the iteration, and the weight-decay/apply post-pass reading the
-    result straight from the workspace. ``u_scales`` (one per tensor) rescales each
-    update first, rounded to bf16: the split_sizes row-block correction."""
+    """p <- p - lr_ratio * lr * (u + wd * p * [u*p > 0]) elementwise.
+
+    ``us`` is either one contiguous stacked tensor or a list of tensors with the
+    elements of each param in the same order; ``shape`` (default: the params') gives
+    the (..., rows, cols) matrix view."""
+    us = [us] if isinstance(us, Tensor) else list(us)
+    shape = list(params[0].shape if shape is None else shape)
+    args = (list(params), us, list(lr_ratios), _as_tensor(lr), float(weight_decay),
+            bool(cautious_wd), shape)
+    if _compiling():
+        torch.ops.muonium_amd.postpass(*args)
+    else:
+        _postpass_impl(*args)
+
+
+def _fused_step_impl(params: list[Tensor], grads: list[Tensor], bufs: list[Tensor],
+                     lr_ratios: list[Tensor], lr: Tensor, momentum: float, nesterov: bool,
+                     maximize: bool, write_back_grad: bool, weight_decay: float,
+                     cautious_wd: bool, coeffs: list[float], prescale: float, eps: float,
+                     u_scales: Optional[list[float]]) -> None:
     lib = _lib.load()
     g0 = grads[0]
     device = g0.device
     _lib.ensure_device(device)
     _check_cuda_contig(list(params) + list(grads) + list(bufs), "Muon step tensors")
+    lrs = adjusted_lrs(lr_ratios, lr)
     nb, rows, cols = matrix_view(g0)
     count = len(grads)
     ws, cap = workspace(device, torch.bfloat16, count * nb, rows, cols)
     s = _lib.stream(device)
-    steps = len(coeffs)
+    steps = len(coeffs) // 3
     _lib.check(
         lib.muon_prepass(count, _lib.ptr_array(grads), _lib.ptr_array(bufs),
                          _lib.dtype_code(g0.dtype), _lib.dtype_code(bufs[0].dtype), nb, rows, cols,
@@ -289,18 +327,12 @@ def fused_step(
     )
 
 
-def _splits(split_sizes):
-    if split_sizes is None:
-        return None, 0
-    return _lib.i64_array(list(split_sizes)), len(split_sizes)
-
-
-def fused_normuon_step(
+def fused_step(
     params: Sequence[Tensor],
     grads: Sequence[Tensor],
     bufs: Sequence[Tensor],
-    variances: Sequence[Tensor],
-    lrs: Sequence[float],
+    lr_ratios: Sequence[Tensor],
+    lr,
     *,
     momentum: float,
     nesterov: bool,
@@ -310,22 +342,46 @@ def fused_normuon_step(
     cautious_wd: bool,
     coeffs: Sequence[tuple[float, float, float]],
     prescale: float,
-    beta2: float,
     eps: float = 1e-7,
+    u_scales: Sequence[float] | None = None,
 ) -> None:
-    """fused_step for the "normuon" algorithm: the post-pass normalizes U per stored row
-    (second-moment EMA into ``variances``, Frobenius rescale) before the apply."""
+    """One Muon step over a same-shape bucket: momentum pre-pass into the batched bf16
+    workspace, the iteration, and the weight-decay/apply post-pass reading the
+    result straight from the workspace. ``u_scales`` (one per tensor) rescales each
+    update first, rounded to bf16: the split_sizes row-block correction."""
+    args = (list(params), list(grads), list(bufs), list(lr_ratios), _as_tensor(lr),
+            float(momentum), bool(nesterov), bool(maximize), bool(write_back_grad),
+            float(weight_decay), bool(cautious_wd), _flatten_coeffs(coeffs), float(prescale),
+            float(eps), None if u_scales is None else [float(v) for v in u_scales])
+    if _compiling():
+        torch.ops.muonium_amd.fused_step(*args)
+    else:
+        _fused_step_impl(*args)
+
+
+def _splits(split_sizes):
+    if split_sizes is None:
+        return None, 0
+    return _lib.i64_array(list(split_sizes)), len(split_sizes)
+
+
+def _fused_normuon_impl(params: list[Tensor], grads: list[Tensor], bufs: list[Tensor],
+                        variances: list[Tensor], lr_ratios: list[Tensor], lr: Tensor,
+                        momentum: float, nesterov: bool, maximize: bool, write_back_grad: bool,
+                        weight_decay: float, cautious_wd: bool, coeffs: list[float],
+                        prescale: float, beta2: float, eps: float) -> None:
     lib = _lib.load()
     g0 = grads[0]
     device = g0.device
     _lib.ensure_device(device)
     _check_cuda_contig(list(params) + list(grads) + list(bufs) + list(variances),
                        "NorMuon step tensors")
+    lrs = adjusted_lrs(lr_ratios, lr)
     nb, rows, cols = matrix_view(g0)
     count = len(grads)
     ws, cap = workspace(device, torch.bfloat16, count * nb, rows, cols)
     s = _lib.stream(device)
-    steps = len(coeffs)
+    steps = len(coeffs) // 3
     _lib.check(
         lib.muon_prepass(count, _lib.ptr_array(grads), _lib.ptr_array(bufs),
                          _lib.dtype_code(g0.dtype), _lib.dtype_code(bufs[0].dtype), nb, rows, cols,
@@ -349,68 +405,102 @@ def fused_normuon_step(
     )
 
 
-def normuon_postpass(
-    params: Sequence[Tensor], us: Sequence[Tensor], variances: Sequence[Tensor],
-    lrs: Sequence[float], *, weight_decay: float, cautious_wd: bool, beta2: float,
-    split_sizes=None, shape=None,
+def fused_normuon_step(
+    params: Sequence[Tensor],
+    grads: Sequence[Tensor],
+    bufs: Sequence[Tensor],
+    variances: Sequence[Tensor],
+    lr_ratios: Sequence[Tensor],
+    lr,
+    *,
+    momentum: float,
+    nesterov: bool,
+    maximize: bool,
+    write_back_grad: bool,
+    weight_decay: float,
+    cautious_wd: bool,
+    coeffs: Sequence[tuple[float, float, float]],
+    prescale: float,
+    beta2: float,
+    eps: float = 1e-7,
 ) -> None:
-    """NorMuon's normalization and apply for explicit updates ``us`` (one tensor per
-    param, the elements in the param's order), per row block with ``split_sizes``."""
+    """fused_step for the "normuon" algorithm: the post-pass normalizes U per stored row
+    (second-moment EMA into ``variances``, Frobenius rescale) before the apply."""
+    args = (list(params), list(grads), list(bufs), list(variances), list(lr_ratios),
+            _as_tensor(lr), float(momentum), bool(nesterov), bool(maximize),
+            bool(write_back_grad), float(weight_decay), bool(cautious_wd),
+            _flatten_coeffs(coeffs), float(prescale), float(beta2), float(eps))
+    if _compiling():
+        torch.ops.muonium_amd.fused_normuon_step(*args)
+    else:
+        _fused_normuon_impl(*args)
+
+
+def _normuon_postpass_impl(params: list[Tensor], us: list[Tensor], variances: list[Tensor],
+                           lr_ratios: list[Tensor], lr: Tensor, weight_decay: float,
+                           cautious_wd: bool, beta2: float, split_sizes: Optional[list[int]],
+                           shape: list[int]) -> None:
     lib = _lib.load()
     p0 = params[0]
     _lib.ensure_device(p0.device)
     _check_cuda_contig(list(params) + list(variances), "NorMuon tensors")
-    nb, rows, cols = matrix_view(p0 if shape is None else shape)
+    lrs = adjusted_lrs(lr_ratios, lr)
+    nb, rows, cols = matrix_view(shape)
     ws, cap = workspace(p0.device, torch.bfloat16, nb, rows, cols)
     sp, nsp = _splits(split_sizes)
     s = _lib.stream(p0.device)
-    for p, u, v, lr in zip(params, us, variances, lrs):
+    for p, u, v, lr_t in zip(params, us, variances, lrs):
         u = u.contiguous()
         _lib.check(
             lib.muon_normuon_postpass(
                 1, _lib.ptr_array([p]), _lib.dtype_code(p.dtype), _lib.ptr_array([v]),
                 _lib.dtype_code(v.dtype), u.data_ptr(), _lib.dtype_code(u.dtype), ws.data_ptr(),
-                _lib.DT_BF16, cap, 0, nb, rows, cols, sp, nsp, _lib.f32_array([lr]),
+                _lib.DT_BF16, cap, 0, nb, rows, cols, sp, nsp, _lib.f32_array([lr_t]),
                 float(weight_decay), int(cautious_wd), float(beta2), s,
             ),
             "muon_normuon_postpass",
         )
 
 
-def fused_lp_step(
-    params: Sequence[Tensor],
-    grads: Sequence[Tensor],
-    states: Sequence,  # QuantizedState objects
-    lrs: Sequence[float],
-    *,
-    momentum: float,
-    nesterov: bool,
-    maximize: bool,
-    weight_decay: float,
-    cautious_wd: bool,
-    coeffs: Sequence[tuple[float, float, float]],
-    prescale: float,
-    eps: float = 1e-7,
+def normuon_postpass(
+    params: Sequence[Tensor], us: Sequence[Tensor], variances: Sequence[Tensor],
+    lr_ratios: Sequence[Tensor], lr, *, weight_decay: float, cautious_wd: bool, beta2: float,
+    split_sizes=None, shape=None,
 ) -> None:
-    """fused_step with quantized momentum: dequant -> momentum -> requant pre-pass."""
+    """NorMuon's normalization and apply for explicit updates ``us`` (one tensor per
+    param, the elements in the param's order), per row block with ``split_sizes``."""
+    shape = list(params[0].shape if shape is None else shape)
+    args = (list(params), list(us), list(variances), list(lr_ratios), _as_tensor(lr),
+            float(weight_decay), bool(cautious_wd), float(beta2),
+            None if split_sizes is None else [int(v) for v in split_sizes], shape)
+    if _compiling():
+        torch.ops.muonium_amd.normuon_postpass(*args)
+    else:
+        _normuon_postpass_impl(*args)
+
+
+def _fused_lp_impl(params: list[Tensor], grads: list[Tensor], codes: list[Tensor],
+                   scales: list[Tensor], qmap: Optional[Tensor], qformat: int, block: int,
+                   lr_ratios: list[Tensor], lr: Tensor, momentum: float, nesterov: bool,
+                   maximize: bool, weight_decay: float, cautious_wd: bool, coeffs: list[float],
+                   prescale: float, eps: float) -> None:
     lib = _lib.load()
     g0 = grads[0]
     device = g0.device
     _lib.ensure_device(device)
     _check_cuda_contig(list(params) + list(grads), "MuonLP step tensors")
-    st0 = states[0]
+    lrs = adjusted_lrs(lr_ratios, lr)
     nb, rows, cols = matrix_view(g0)
     count = len(grads)
     ws, cap = workspace(device, torch.bfloat16, count * nb, rows, cols)
     s = _lib.stream(device)
-    steps = len(coeffs)
+    steps = len(coeffs) // 3
     _lib.check(
         lib.muon_lp_prepass(
-            count, _lib.ptr_array(grads), _lib.dtype_code(g0.dtype),
-            _lib.ptr_array([st.codes for st in states]), _lib.ptr_array([st.scale for st in states]),
-            st0.qmap.data_ptr() if st0.qmap is not None else None, st0.qformat, st0.block_size,
-            nb, rows, cols, momentum, int(nesterov), int(maximize), ws.data_ptr(), _lib.DT_BF16,
-            cap, s,
+            count, _lib.ptr_array(grads), _lib.dtype_code(g0.dtype), _lib.ptr_array(codes),
+            _lib.ptr_array(scales), qmap.data_ptr() if qmap is not None else None, qformat,
+            block, nb, rows, cols, momentum, int(nesterov), int(maximize), ws.data_ptr(),
+            _lib.DT_BF16, cap, s,
         ),
         "muon_lp_prepass",
     )
@@ -427,8 +517,36 @@ def fused_lp_step(
     )
 
 
-def lp_quantize(src: Tensor, codes: Tensor, scale: Tensor, qmap: Tensor | None, qformat: int,
-                block: int) -> None:
+def fused_lp_step(
+    params: Sequence[Tensor],
+    grads: Sequence[Tensor],
+    states: Sequence,  # QuantizedState objects
+    lr_ratios: Sequence[Tensor],
+    lr,
+    *,
+    momentum: float,
+    nesterov: bool,
+    maximize: bool,
+    weight_decay: float,
+    cautious_wd: bool,
+    coeffs: Sequence[tuple[float, float, float]],
+    prescale: float,
+    eps: float = 1e-7,
+) -> None:
+    """fused_step with quantized momentum: dequant -> momentum -> requant pre-pass."""
+    st0 = states[0]
+    args = (list(params), list(grads), [st.codes for st in states], [st.scale for st in states],
+            st0.qmap, int(st0.qformat), int(st0.block_size), list(lr_ratios), _as_tensor(lr),
+            float(momentum), bool(nesterov), bool(maximize), float(weight_decay),
+            bool(cautious_wd), _flatten_coeffs(coeffs), float(prescale), float(eps))
+    if _compiling():
+        torch.ops.muonium_amd.fused_lp_step(*args)
+    else:
+        _fused_lp_impl(*args)
+
+
+def _lp_quantize_impl(src: Tensor, codes: Tensor, scale: Tensor, qmap: Optional[Tensor],
+                      qformat: int, block: int) -> None:
     lib = _lib.load()
     _lib.ensure_device(src.device)
     src = src.contiguous().float()
@@ -440,8 +558,17 @@ def lp_quantize(src: Tensor, codes: Tensor, scale: Tensor, qmap: Tensor | None, 
     )
 
 
-def lp_dequantize(codes: Tensor, scale: Tensor, qmap: Tensor | None, qformat: int, block: int,
-                  numel: int, out: Tensor) -> None:
+def lp_quantize(src: Tensor, codes: Tensor, scale: Tensor, qmap: Tensor | None, qformat: int,
+                block: int) -> None:
+    args = (src, codes, scale, qmap, int(qformat), int(block))
+    if _compiling():
+        torch.ops.muonium_amd.lp_quantize(*args)
+    else:
+        _lp_quantize_impl(*args)
+
+
+def _lp_dequantize_impl(codes: Tensor, scale: Tensor, qmap: Optional[Tensor], qformat: int,
+                        block: int, numel: int, out: Tensor) -> None:
     lib = _lib.load()
     _lib.ensure_device(codes.device)
     _lib.check(
@@ -450,3 +577,38 @@ def lp_dequantize(codes: Tensor, scale: Tensor, qmap: Tensor | None, qformat: in
                                block, out.data_ptr(), _lib.stream(codes.device)),
         "muon_lp_dequantize",
     )
+
+
+def lp_dequantize(codes: Tensor, scale: Tensor, qmap: Tensor | None, qformat: int, block: int,
+                  numel: int, out: Tensor) -> None:
+    args = (codes, scale, qmap, int(qformat), int(block), int(numel), out)
+    if _compiling():
+        torch.ops.muonium_amd.lp_dequantize(*args)
+    else:
+        _lp_dequantize_impl(*args)
+
+
+# ---------------------------------------------------------------------------------
+# torch.library registration: the ops above, their written arguments and fake impls
+
+
+def _register_ops() -> None:
+    def op(name, impl, mutates, fake=None):
+        o = torch.library.custom_op(f"muonium_amd::{name}", impl, mutates_args=mutates)
+        o.register_fake(fake or (lambda *args, **kwargs: None))
+
+    op("gram_", _gram_impl, ("y",))
+    op("orthogonalize", _orthogonalize_impl, (),
+       lambda tensors, coeffs, prescale, eps, iter_dtype, out_dtype: tensors[0].new_empty(
+           (len(tensors), *tensors[0].shape), dtype=out_dtype))
+    op("momentum_only", _momentum_impl, ("grads", "bufs"))
+    op("postpass", _postpass_impl, ("params",))
+    op("fused_step", _fused_step_impl, ("params", "grads", "bufs"))
+    op("fused_normuon_step", _fused_normuon_impl, ("params", "grads", "bufs", "variances"))
+    op("normuon_postpass", _normuon_postpass_impl, ("params", "variances"))
+    op("fused_lp_step", _fused_lp_impl, ("params", "grads", "codes", "scales"))
+    op("lp_quantize", _lp_quantize_impl, ("codes", "scale"))
+    op("lp_dequantize", _lp_dequantize_impl, ("out",))
+
+
+_register_ops()

@@ -95,7 +95,6 @@ def muon_step(
                           nesterov=nesterov, maximize=maximize, ns_steps=ns_steps,
                           orthogonalization_strategy=orthogonalization_strategy,
                           split_sizes=split_sizes, batched=batched)
-    lrs = _ops.adjusted_lrs(lr_ratios, lr)
     coeffs, prescale = schedule(orthogonalization_strategy, ns_steps)
     quantized = is_quantized(bufs[0])
     P = _Contig(params)
@@ -105,7 +104,8 @@ def muon_step(
     if split_sizes is not None and not quantized and G.work[0].dim() == 2 and \
             fused_orth_available(None, batched):
         _fused_split_step(
-            pview, G.work, B.work, lrs, split_sizes, momentum=momentum, nesterov=nesterov,
+            pview, G.work, B.work, lr_ratios, lr, split_sizes, momentum=momentum,
+            nesterov=nesterov,
             maximize=maximize, write_back_grad=batched and nesterov and not maximize,
             weight_decay=weight_decay, cautious_wd=cautious_wd, coeffs=coeffs,
             prescale=prescale,
@@ -113,13 +113,13 @@ def muon_step(
     elif fused_orth_available(split_sizes, batched):
         if quantized:
             _ops.fused_lp_step(
-                pview, G.work, bufs, lrs, momentum=momentum, nesterov=nesterov,
+                pview, G.work, bufs, lr_ratios, lr, momentum=momentum, nesterov=nesterov,
                 maximize=maximize, weight_decay=weight_decay, cautious_wd=cautious_wd,
                 coeffs=coeffs, prescale=prescale,
             )
         else:
             _ops.fused_step(
-                pview, G.work, B.work, lrs, momentum=momentum, nesterov=nesterov,
+                pview, G.work, B.work, lr_ratios, lr, momentum=momentum, nesterov=nesterov,
                 maximize=maximize, write_back_grad=batched and nesterov and not maximize,
                 weight_decay=weight_decay, cautious_wd=cautious_wd, coeffs=coeffs,
                 prescale=prescale,
@@ -134,7 +134,7 @@ def muon_step(
             us = [orthogonalize_single(gq[0], ns_steps=ns_steps,
                                        strategy=orthogonalization_strategy,
                                        split_sizes=split_sizes)]
-        _ops.postpass(pview, [u.reshape(g.shape) for u, g in zip(us, G.work)], lrs,
+        _ops.postpass(pview, [u.reshape(g.shape) for u, g in zip(us, G.work)], lr_ratios, lr,
                       weight_decay=weight_decay, cautious_wd=cautious_wd, shape=G.work[0].shape)
     P.writeback()
     if batched and nesterov and not maximize:
@@ -143,7 +143,7 @@ def muon_step(
         B.writeback()
 
 
-def _fused_split_step(params, grads, bufs, lrs, split_sizes, **kw) -> None:
+def _fused_split_step(params, grads, bufs, lr_ratios, lr, split_sizes, **kw) -> None:
     """The fused step for 2D tensors split into row blocks (base.py:56-99): every block is a
     contiguous row slice, i.e. a matrix of its own, so equal-height blocks of all tensors run
     through one prepass / iteration / post-pass sequence, each block's update rescaled by
@@ -158,16 +158,16 @@ def _fused_split_step(params, grads, bufs, lrs, split_sizes, **kw) -> None:
     for j, h in enumerate(split_sizes):
         by_height.setdefault(h, []).append(j)
     for h, blocks in by_height.items():
-        ps, gs, bs, block_lrs, block_scales = [], [], [], [], []
-        for p, g, b, lr in zip(params, grads, bufs, lrs):
+        ps, gs, bs, block_ratios, block_scales = [], [], [], [], []
+        for p, g, b, ratio in zip(params, grads, bufs, lr_ratios):
             for j in blocks:
                 o = offsets[j]
                 ps.append(p[o:o + h])
                 gs.append(g[o:o + h])
                 bs.append(b[o:o + h])
-                block_lrs.append(lr)
+                block_ratios.append(ratio)
                 block_scales.append(scales[j])
-        _ops.fused_step(ps, gs, bs, block_lrs, u_scales=block_scales, **kw)
+        _ops.fused_step(ps, gs, bs, block_ratios, lr, u_scales=block_scales, **kw)
 
 
 def _offloaded(fn, params, grads, *state_lists, **kw):

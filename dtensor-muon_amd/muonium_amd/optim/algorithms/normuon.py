@@ -35,7 +35,6 @@ def _normuon_step(params, grads, bufs, variances, lr_ratios, *, lr, weight_decay
                           ns_steps=ns_steps,
                           orthogonalization_strategy=orthogonalization_strategy,
                           split_sizes=split_sizes, muon_beta2=muon_beta2, batched=batched)
-    lrs = _ops.adjusted_lrs(lr_ratios, lr)
     coeffs, prescale = schedule(orthogonalization_strategy, ns_steps)
     quantized = is_quantized(bufs[0])
     P, G, V = _Contig(params), _Contig(grads), _Contig(variances)
@@ -43,7 +42,7 @@ def _normuon_step(params, grads, bufs, variances, lr_ratios, *, lr, weight_decay
     pview = [p.view(g.shape) for p, g in zip(P.work, G.work)]
     if not quantized and fused_orth_available(split_sizes, batched):
         _ops.fused_normuon_step(
-            pview, G.work, B.work, V.work, lrs, momentum=momentum, nesterov=nesterov,
+            pview, G.work, B.work, V.work, lr_ratios, lr, momentum=momentum, nesterov=nesterov,
             maximize=maximize, write_back_grad=batched and nesterov and not maximize,
             weight_decay=weight_decay, cautious_wd=cautious_wd, coeffs=coeffs,
             prescale=prescale, beta2=muon_beta2,
@@ -59,7 +58,7 @@ def _normuon_step(params, grads, bufs, variances, lr_ratios, *, lr, weight_decay
                                        strategy=orthogonalization_strategy,
                                        split_sizes=split_sizes)]
         _ops.normuon_postpass(pview, [u.reshape(g.shape) for u, g in zip(us, G.work)], V.work,
-                              lrs, weight_decay=weight_decay, cautious_wd=cautious_wd,
+                              lr_ratios, lr, weight_decay=weight_decay, cautious_wd=cautious_wd,
                               beta2=muon_beta2, split_sizes=split_sizes, shape=G.work[0].shape)
     P.writeback()
     if batched and nesterov and not maximize:

@@ -83,8 +83,8 @@ def _concurrent_slots(buckets, algorithm: MuonAlgorithm, batch_size: int | None)
     (workspaces are cached per stream: a side stream never touches the buffer of the
     current stream or of another side stream). Large buckets stay on the current
     stream. Built-in algorithms only."""
-    if not type(algorithm).__module__.startswith("muonium_amd."):
-        return {}
+    if not type(algorithm).__module__.startswith("muonium_amd.") or torch.compiler.is_compiling():
+        return {}  # (under an outer torch.compile the buckets run in the traced order)
     from muonium_amd import _ops
 
     cus: dict[torch.device, int] = {}
@@ -481,7 +481,8 @@ class Muon(torch.optim.Optimizer):
                  [dev_lr[i] for i in sel])
                 for sel in batches
             ]
-            if torch.cuda.is_available() and all(pipeline_supported(b) for b in host):
+            if (torch.cuda.is_available() and not torch.compiler.is_compiling()
+                    and all(pipeline_supported(b) for b in host)):
                 # pinned-memory round trip, copies overlapped with the updates
                 run_offloaded(
                     host,

@@ -113,3 +113,34 @@ def test_argument_errors_return_codes_without_launching(call, code):
     lib = _lib.load()
     assert call(lib) == code
     assert _lib.last_error() != ""
+
+
+def test_library_calls_are_registered_torch_ops_with_fake_impls():
+    """Every library call of the package is a torch.library custom op (namespace
+    muonium_amd) that declares the tensors it writes, and its fake implementation runs
+    on fake tensors without a device: what lets an outer torch.compile trace step()."""
+    import torch
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    import muonium_amd  # noqa: F401  (registers the ops)
+
+    writes = {
+        "gram_": ["y"], "orthogonalize": [], "momentum_only": ["grads", "bufs"],
+        "postpass": ["params"], "fused_step": ["params", "grads", "bufs"],
+        "fused_normuon_step": ["params", "grads", "bufs", "variances"],
+        "normuon_postpass": ["params", "variances"],
+        "fused_lp_step": ["params", "grads", "codes", "scales"],
+        "lp_quantize": ["codes", "scale"], "lp_dequantize": ["out"],
+    }
+    for name, mutated in writes.items():
+        schema = getattr(torch.ops.muonium_amd, name).default._schema
+        got = [a.name for a in schema.arguments if a.alias_info is not None and a.alias_info.is_write]
+        assert got == mutated, (name, got)
+    with FakeTensorMode():
+        x = torch.empty(3, 64, 32, device="cuda")
+        u = torch.ops.muonium_amd.orthogonalize([x, x], [3.4445, -4.775, 2.0315], 1.0, 1e-7,
+                                                torch.bfloat16, torch.bfloat16)
+        assert u.shape == (2, 3, 64, 32) and u.dtype == torch.bfloat16
+        assert torch.ops.muonium_amd.fused_step(
+            [x], [x], [x], [torch.empty(())], torch.empty(()), 0.9, True, False, True, 0.1,
+            True, [3.4445, -4.775, 2.0315], 1.0, 1e-7, None) is None
