@@ -131,9 +131,8 @@ def muon_step(
             us = orthogonalize_batch(gq, ns_steps=ns_steps, strategy=orthogonalization_strategy,
                                      split_sizes=split_sizes)
         else:
-            us = [orthogonalize_single(gq[0], ns_steps=ns_steps,
-                                       strategy=orthogonalization_strategy,
-                                       split_sizes=split_sizes)]
+            us = [orthogonalize_single(g, ns_steps=ns_steps, strategy=orthogonalization_strategy,
+                                       split_sizes=split_sizes) for g in gq]
         _ops.postpass(pview, [u.reshape(g.shape) for u, g in zip(us, G.work)], lr_ratios, lr,
                       weight_decay=weight_decay, cautious_wd=cautious_wd, shape=G.work[0].shape)
     P.writeback()
@@ -219,11 +218,36 @@ def momentum_seam(grads, bufs, *, momentum, nesterov, maximize, batched) -> list
     return gq
 
 
+def batches_per_tensor(algorithm, cls, split_sizes) -> bool:
+    """True when the per-parameter driver may group same-shape tensors of ``algorithm``
+    into one `update_same_shape` call: the built-in `update` is in place (not replaced
+    on the instance) and its step runs entirely in the fused kernels (this library's
+    orthogonalizer, no row blocks)."""
+    return (type(algorithm) is cls and "update" not in vars(algorithm)
+            and fused_orth_available(split_sizes, batched=False))
+
+
 @register_muon_algorithm
 class MuonBaseline(MuonAlgorithm):
     """The original Muon update: momentum, orthogonalize, shape-scaled apply."""
 
     name = "muon"
+
+    def batches_per_tensor(self, split_sizes) -> bool:
+        return batches_per_tensor(self, MuonBaseline, split_sizes)
+
+    def update_same_shape(self, params, grads, state, lr_ratios, *, lr, weight_decay,
+                          cautious_wd, momentum, nesterov, maximize, ns_steps,
+                          orthogonalization_strategy, split_sizes, **opts) -> None:
+        """`update` for several same-shape tensors at once, per-tensor semantics
+        (muon.py:21-77 for each): the gradients are left as they are."""
+        muon_step(
+            params, grads, state["momentum_buffer"], lr_ratios, lr=lr,
+            weight_decay=weight_decay, cautious_wd=cautious_wd, momentum=momentum,
+            nesterov=nesterov, maximize=maximize, ns_steps=ns_steps,
+            orthogonalization_strategy=orthogonalization_strategy, split_sizes=split_sizes,
+            batched=False,
+        )
 
     def update(
         self,

@@ -20,7 +20,15 @@ from .base import (
     orthogonalize_single,
     register_muon_algorithm,
 )
-from .muon import _Contig, _offloaded, fused_orth_available, is_quantized, momentum_seam, schedule
+from .muon import (
+    _Contig,
+    _offloaded,
+    batches_per_tensor,
+    fused_orth_available,
+    is_quantized,
+    momentum_seam,
+    schedule,
+)
 
 
 def _normuon_step(params, grads, bufs, variances, lr_ratios, *, lr, weight_decay, cautious_wd,
@@ -54,9 +62,8 @@ def _normuon_step(params, grads, bufs, variances, lr_ratios, *, lr, weight_decay
             us = orthogonalize_batch(gq, ns_steps=ns_steps, strategy=orthogonalization_strategy,
                                      split_sizes=split_sizes)
         else:
-            us = [orthogonalize_single(gq[0], ns_steps=ns_steps,
-                                       strategy=orthogonalization_strategy,
-                                       split_sizes=split_sizes)]
+            us = [orthogonalize_single(g, ns_steps=ns_steps, strategy=orthogonalization_strategy,
+                                       split_sizes=split_sizes) for g in gq]
         _ops.normuon_postpass(pview, [u.reshape(g.shape) for u, g in zip(us, G.work)], V.work,
                               lr_ratios, lr, weight_decay=weight_decay, cautious_wd=cautious_wd,
                               beta2=muon_beta2, split_sizes=split_sizes, shape=G.work[0].shape)
@@ -78,6 +85,22 @@ class NorMuon(MuonAlgorithm):
         "momentum_buffer": BufferSpec(like="grad", signed=True),
         "variance_neuron": BufferSpec(like="grad_rows", signed=False),
     }
+
+    def batches_per_tensor(self, split_sizes) -> bool:
+        return batches_per_tensor(self, NorMuon, split_sizes)
+
+    def update_same_shape(self, params, grads, state, lr_ratios, *, lr, weight_decay,
+                          cautious_wd, momentum, nesterov, maximize, ns_steps,
+                          orthogonalization_strategy, split_sizes, muon_beta2=0.95,
+                          **opts) -> None:
+        """`update` for several same-shape tensors at once, per-tensor semantics."""
+        _normuon_step(
+            params, grads, state["momentum_buffer"], state["variance_neuron"], lr_ratios,
+            lr=lr, weight_decay=weight_decay, cautious_wd=cautious_wd, momentum=momentum,
+            nesterov=nesterov, maximize=maximize, ns_steps=ns_steps,
+            orthogonalization_strategy=orthogonalization_strategy, split_sizes=split_sizes,
+            muon_beta2=muon_beta2, batched=False,
+        )
 
     def update(
         self,

@@ -59,6 +59,28 @@ def _group_muon_tensors(
     return buckets
 
 
+def _per_tensor_runs(algorithm: MuonAlgorithm, params, grads, state, split_sizes):
+    """Index lists for the per-parameter driver: singletons (one `update` call each, the
+    reference's loop, optim.py:511-531), except that same-shape device tensors of a
+    built-in algorithm whose per-tensor update runs entirely in this library's fused
+    kernels are grouped and handed to `update_same_shape` in one launch sequence. Each
+    tensor keeps the per-tensor semantics (its gradient is not rewritten) and gets bit
+    for bit the result of its own `update` call: the kernels treat every matrix of a
+    batch independently. Groups keep first-seen order; the updates are independent."""
+    if not getattr(algorithm, "batches_per_tensor", lambda s: False)(split_sizes) or \
+            torch.compiler.is_compiling():
+        return [[i] for i in range(len(params))]
+    keyed: dict[tuple, list[int]] = {}
+    for i, (p, g) in enumerate(zip(params, grads)):
+        if not p.is_cuda:
+            keyed[("single", i)] = [i]
+            continue
+        bufs = tuple((type(b[i]), b[i].dtype, getattr(b[i], "block_size", None),
+                      getattr(b[i], "signed", None)) for b in state.values())
+        keyed.setdefault((p.device, p.dtype, tuple(g.shape), g.dtype, bufs), []).append(i)
+    return list(keyed.values())
+
+
 _MAX_SIDE_STREAMS = 4  # GPU_MAX_HW_QUEUES is 4 by default: one hardware queue each
 _side_streams: dict[tuple[int, int], torch.cuda.Stream] = {}
 
@@ -444,8 +466,16 @@ class Muon(torch.optim.Optimizer):
             **opts,
         )
         if not foreach:
-            for i, (param, grad, lr_ratio) in enumerate(zip(params, grads, lr_ratios, strict=True)):
-                algorithm.update(param, grad, {k: b[i] for k, b in state.items()}, lr_ratio, **hp)
+            for idx in _per_tensor_runs(algorithm, params, grads, state, split_sizes):
+                if len(idx) == 1:
+                    i = idx[0]
+                    algorithm.update(params[i], grads[i], {k: b[i] for k, b in state.items()},
+                                     lr_ratios[i], **hp)
+                else:
+                    algorithm.update_same_shape(
+                        [params[i] for i in idx], [grads[i] for i in idx],
+                        {k: [b[i] for i in idx] for k, b in state.items()},
+                        [lr_ratios[i] for i in idx], **hp)
             return
 
         buckets = _group_muon_tensors(params, grads, state, lr_ratios)

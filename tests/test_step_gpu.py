@@ -585,3 +585,63 @@ def test_host_params_per_parameter_driver_matches_device_run(algo):
         for key, val in opt_d.state[d].items():
             assert opt_h.state[h][key].device.type == "cpu", key
             assert torch.equal(opt_h.state[h][key], val.cpu()), key
+
+
+@pytest.mark.parametrize("kind", ["muon-fp32", "muon-bf16", "normuon", "muon8bit"])
+def test_per_parameter_driver_groups_same_shapes_bit_exact(kind):
+    """foreach=False runs same-shape device tensors of a built-in algorithm as one fused
+    launch sequence with per-tensor semantics: params and state equal, bit for bit, one
+    `update` call per tensor (forced here by wrapping `update` on the instance, which
+    turns the grouping off), and the gradients are left untouched."""
+    from muonium_amd.optim import Muon8bit
+    from muonium_amd.optim.algorithms import get_algorithm
+
+    dtype = torch.bfloat16 if kind == "muon-bf16" else torch.float32
+    shapes = [(96, 64), (64, 160), (96, 64), (2, 64, 160), (64, 160), (96, 64)]
+    gen = torch.Generator().manual_seed(13)
+    init = [torch.randn(s, generator=gen).to(dtype) for s in shapes]
+    grads = [[torch.randn(s, generator=gen).to(dtype) for s in shapes] for _ in range(2)]
+
+    def run(split_calls):
+        ps = [nn.Parameter(t.clone().to(DEV)) for t in init]
+        kw = dict(lr=0.02, wd=0.1, momentum=0.9, foreach=False)
+        if kind == "muon8bit":
+            opt = Muon8bit(ps, block_size=64, **kw)
+        else:
+            opt = Muon([{"params": ps, "algorithm": "normuon" if kind == "normuon" else "muon"}],
+                       **kw)
+        algo = get_algorithm(opt.param_groups[0]["algorithm"])
+        calls = []
+        if split_calls:
+            orig = type(algo).update
+
+            def one(*args, **kwargs):
+                calls.append(1)
+                return orig(algo, *args, **kwargs)
+
+            algo.update = one
+        try:
+            for gs in grads:
+                for p, g in zip(ps, gs):
+                    p.grad = g.clone().to(DEV)
+                opt.step()
+                for p, g in zip(ps, gs):
+                    assert torch.equal(p.grad.cpu(), g)  # per-tensor semantics
+        finally:
+            if split_calls:
+                del algo.update
+        torch.cuda.synchronize()
+        if split_calls:
+            assert len(calls) == 2 * len(shapes)
+        return ps, opt
+
+    pa, oa = run(False)
+    pb, ob = run(True)
+    for a, b in zip(pa, pb):
+        assert torch.equal(a.detach(), b.detach())
+        for key, vb in ob.state[b].items():
+            va = oa.state[a][key]
+            if hasattr(vb, "codes"):
+                assert torch.equal(va.codes, vb.codes) and torch.equal(va.scale, vb.scale)
+            else:
+                assert torch.equal(va, vb), key
