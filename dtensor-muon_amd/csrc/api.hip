@@ -38,7 +38,8 @@ int muon_launch_postpass(int ntensors, void* const* params, const float* adj, in
 int muon_launch_normuon_stats(int ntensors, void* const* vars, int vdt, const void* u, int udt,
                               int64_t u_pitch, int64_t u_mstride, int u_trans, int64_t nb,
                               int64_t rows, int64_t cols, float* ss, int64_t ss_mstride,
-                              const int64_t* split_start, int nsplits, float w, hipStream_t s);
+                              const int64_t* split_start, int nsplits, const float* uscale,
+                              float w, hipStream_t s);
 int muon_launch_extract(const void* src, int wdt, int64_t pitch, int64_t mstride, int trans,
                         void* dst, int odt, int64_t rows, int64_t cols, int64_t batch,
                         hipStream_t s);
@@ -211,7 +212,7 @@ static bool io_dtype_ok(int dt) {
 
 extern "C" {
 
-int muon_amd_abi_version(void) { return 3; }
+int muon_amd_abi_version(void) { return 4; }
 
 const char* muon_amd_last_error(void) { return g_err; }
 
@@ -514,8 +515,8 @@ static int normuon_postpass_on(int ntensors, void* const* params, int p_dtype,
                                void* const* variances, int v_dtype, const char* ubase, int udt,
                                int64_t pitch, int64_t mst, int trans, float* ss, int64_t ss_mst,
                                int64_t nb, int64_t rows, int64_t cols, const int64_t* starts,
-                               int nb_split, const float* adjusted_lrs, float wd, int cautious,
-                               double beta2, hipStream_t s) {
+                               int nb_split, const float* adjusted_lrs, const float* u_scales,
+                               float wd, int cautious, double beta2, hipStream_t s) {
   const int es = udt == MUON_DT_F32 ? 4 : 2;
   const int pes = p_dtype == MUON_DT_F32 ? 4 : 2;
   const float w = (float)(1.0 - beta2);
@@ -523,11 +524,12 @@ static int normuon_postpass_on(int ntensors, void* const* params, int p_dtype,
   for (int t0 = 0; t0 < ntensors; t0 += MUON_MAX_TENSORS) {
     const int cnt = std::min(MUON_MAX_TENSORS, ntensors - t0);
     const char* uc = ubase + (int64_t)t0 * nb * mst * es;
+    const float* usc = u_scales ? u_scales + t0 : nullptr;
     int rc = muon_launch_normuon_stats(cnt, variances + t0, v_dtype, uc, udt, pitch, mst, trans,
-                                       nb, rows, cols, ss, ss_mst, starts, nb_split, w, s);
+                                       nb, rows, cols, ss, ss_mst, starts, nb_split, usc, w, s);
     if (rc != MUON_OK) return rc;
     rc = muon_launch_postpass(cnt, params + t0, adjusted_lrs + t0, p_dtype, uc, udt, pitch, mst,
-                              trans, ss, ss_mst, nullptr, nb, rows, cols, wd, cautious, s);
+                              trans, ss, ss_mst, usc, nb, rows, cols, wd, cautious, s);
     if (rc != MUON_OK) return rc;
   }
   return MUON_OK;
@@ -567,8 +569,8 @@ int muon_normuon_postpass(int ntensors, void* const* params, int p_dtype,
                           void* const* variances, int v_dtype, const void* u, int u_dtype,
                           void* ws, int ws_dtype, int64_t ws_batch, int steps, int64_t nb,
                           int64_t rows, int64_t cols, const int64_t* split_sizes, int nsplits,
-                          const float* adjusted_lrs, float wd, int cautious, double beta2,
-                          void* stream) {
+                          const float* adjusted_lrs, const float* u_scales, float wd,
+                          int cautious, double beta2, void* stream) {
   if (!io_dtype_ok(p_dtype) || !io_dtype_ok(v_dtype)) {
     muon_set_error("normuon_postpass: unsupported param/variance dtype (%d, %d)", p_dtype,
                    v_dtype);
@@ -610,15 +612,15 @@ int muon_normuon_postpass(int ntensors, void* const* params, int p_dtype,
   float* ss = (float*)((char*)ws + L.off_rows);  // stored rows <= n <= n_pad per matrix
   return normuon_postpass_on(ntensors, params, p_dtype, variances, v_dtype, ubase, udt, pitch,
                              mst, trans, ss, L.n_pad, nb, rows, cols, starts, nb_split,
-                             adjusted_lrs, wd, cautious, beta2, (hipStream_t)stream);
+                             adjusted_lrs, u_scales, wd, cautious, beta2, (hipStream_t)stream);
 }
 
 int muon_normuon_postpass_noalloc(int ntensors, void* const* params, int p_dtype,
                                   void* const* variances, int v_dtype, const void* u,
                                   int u_dtype, int64_t nb, int64_t rows, int64_t cols,
                                   const int64_t* split_sizes, int nsplits,
-                                  const float* adjusted_lrs, float wd, int cautious,
-                                  double beta2, void* stream) {
+                                  const float* adjusted_lrs, const float* u_scales, float wd,
+                                  int cautious, double beta2, void* stream) {
   if (!io_dtype_ok(p_dtype) || !io_dtype_ok(v_dtype) || !io_dtype_ok(u_dtype)) {
     muon_set_error("normuon_postpass_noalloc: unsupported dtype (param %d, variance %d, u %d)",
                    p_dtype, v_dtype, u_dtype);
@@ -651,7 +653,7 @@ int muon_normuon_postpass_noalloc(int ntensors, void* const* params, int p_dtype
   if (rc != MUON_OK) return rc;
   return normuon_postpass_on(ntensors, params, p_dtype, variances, v_dtype, (const char*)u,
                              u_dtype, cols, rows * cols, 0, (float*)sp, rows, nb, rows, cols,
-                             starts, nb_split, adjusted_lrs, wd, cautious, beta2,
+                             starts, nb_split, adjusted_lrs, u_scales, wd, cautious, beta2,
                              (hipStream_t)stream);
 }
 

@@ -410,8 +410,10 @@ MUON_DEVICE float apply_elem(float p, float u, float wd, int cautious, float adj
 // workspace after the iteration); the 64 x 64 block u[c0 .. c0+63][r0 .. r0+63] is read
 // with coalesced 16-byte loads and transposed through LDS. Its extents are padded to a
 // multiple of 64, so the block is in bounds.
-// ROWSCALE (NorMuon): u is first multiplied by its row's scale and the result is an fp32
-// tensor, so the apply runs in fp32 whatever U's storage dtype (normuon.py:44-55, 125-134).
+// With uscale, u is first replaced by round(u * uscale[t]) in U's dtype (a split_sizes row
+// block's `u * scales[i]`, base.py:98). ROWSCALE (NorMuon): u is then multiplied by its
+// row's scale and the result is an fp32 tensor, so the apply runs in fp32 whatever U's
+// storage dtype (normuon.py:44-55, 125-134).
 template <int PDT, int UDT, int VEC, bool TRANS, bool ROWSCALE>
 __global__ __launch_bounds__(256) void postpass_kernel(PostArgs a) {
 #pragma clang fp contract(off)
@@ -456,14 +458,14 @@ __global__ __launch_bounds__(256) void postpass_kernel(PostArgs a) {
       } else {
         Vec8<UDT>::load(a.u, ui, u);
       }
+      if (a.has_uscale) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) u[e] = Elem<UDT>::round(u[e] * a.uscale[t]);
+      }
       if constexpr (ROWSCALE) {
         const float rs = a.rscale[(int64_t)mat * a.rs_mstride + r];
 #pragma unroll
         for (int e = 0; e < 8; ++e) u[e] = u[e] * rs;
-      }
-      if (a.has_uscale) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) u[e] = Elem<UDT>::round(u[e] * a.uscale[t]);
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e)
@@ -478,8 +480,8 @@ __global__ __launch_bounds__(256) void postpass_kernel(PostArgs a) {
         const int64_t ui = (int64_t)mat * a.u_mstride + r * a.u_pitch + c;
         const float p = Elem<PDT>::load(pp, pi);
         float u = TRANS ? ut[r - r0][cl + e] : Elem<UDT>::load(a.u, ui);
-        if (ROWSCALE) u = u * a.rscale[(int64_t)mat * a.rs_mstride + r];
         if (a.has_uscale) u = Elem<UDT>::round(u * a.uscale[t]);
+        if (ROWSCALE) u = u * a.rscale[(int64_t)mat * a.rs_mstride + r];
         Elem<PDT>::store(pp, pi,
                          apply_elem<PDT, ROWSCALE ? MUON_DT_F32 : UDT>(p, u, a.wd, a.cautious, adj));
       }
@@ -548,14 +550,14 @@ __global__ __launch_bounds__(256) void postpass_slab_kernel(PostArgs a) {
     } else {
       ur[p].unpack(u);
     }
+    if (a.has_uscale) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) u[e] = Elem<UDT>::round(u[e] * a.uscale[t]);
+    }
     if constexpr (ROWSCALE) {
       const float rs = a.rscale[(int64_t)mat * a.rs_mstride + r];
 #pragma unroll
       for (int e = 0; e < 8; ++e) u[e] = u[e] * rs;
-    }
-    if (a.has_uscale) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) u[e] = Elem<UDT>::round(u[e] * a.uscale[t]);
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e)
@@ -576,6 +578,9 @@ struct RowSsArgs {
   int64_t u_pitch, u_mstride, rows, cols;
   float* ss;      // matrix 0 of this launch, pitch ss_mstride
   int64_t ss_mstride;
+  int64_t nb;     // matrices per tensor
+  float uscale[MUON_MAX_TENSORS];  // per tensor: U <- round_UDT(U * uscale) when has_uscale
+  int has_uscale;
 };
 
 template <int UDT, int VEC, bool TRANS>
@@ -586,12 +591,14 @@ __global__ __launch_bounds__(256) void row_sumsq_kernel(RowSsArgs a) {
   const int64_t r0 = (int64_t)blockIdx.x * 64;
   const int64_t base = (int64_t)mat * a.u_mstride;
   float* ss = a.ss + (int64_t)mat * a.ss_mstride;
+  const float us = a.uscale[mat / a.nb];
   if constexpr (TRANS) {
     const int64_t r = r0 + lane;
     float s = 0.0f;
     if (r < a.rows)
       for (int64_t c = wave; c < a.cols; c += 4) {
-        const float v = Elem<UDT>::load(a.u, base + c * a.u_pitch + r);
+        float v = Elem<UDT>::load(a.u, base + c * a.u_pitch + r);
+        if (a.has_uscale) v = Elem<UDT>::round(v * us);
         s += v * v;
       }
     part[wave][lane] = s;
@@ -606,12 +613,17 @@ __global__ __launch_bounds__(256) void row_sumsq_kernel(RowSsArgs a) {
         for (int64_t c = (int64_t)lane * 8; c < a.cols; c += 512) {
           float v[8];
           Vec8<UDT>::load(a.u, base + r * a.u_pitch + c, v);
+          if (a.has_uscale) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = Elem<UDT>::round(v[e] * us);
+          }
 #pragma unroll
           for (int e = 0; e < 8; ++e) s += v[e] * v[e];
         }
       } else {
         for (int64_t c = lane; c < a.cols; c += 64) {
-          const float v = Elem<UDT>::load(a.u, base + r * a.u_pitch + c);
+          float v = Elem<UDT>::load(a.u, base + r * a.u_pitch + c);
+          if (a.has_uscale) v = Elem<UDT>::round(v * us);
           s += v * v;
         }
       }
@@ -1042,13 +1054,18 @@ int muon_launch_extract(const void* src, int wdt, int64_t pitch, int64_t mstride
 
 // NorMuon row statistics and finalize for nmat matrices of rows x cols starting at u
 // (pitch / matrix stride in elements, transposed as the post-pass reads it), scratch ss
-// (pitch ss_mstride per matrix); splits: nsplits + 1 row offsets.
+// (pitch ss_mstride per matrix); splits: nsplits + 1 row offsets; uscale (per tensor,
+// nullable): the statistics are those of round(U * uscale[t]), as the post-pass applies.
 int muon_launch_normuon_stats(int ntensors, void* const* vars, int vdt, const void* u, int udt,
                               int64_t u_pitch, int64_t u_mstride, int u_trans, int64_t nb,
                               int64_t rows, int64_t cols, float* ss, int64_t ss_mstride,
-                              const int64_t* split_start, int nsplits, float w, hipStream_t s) {
+                              const int64_t* split_start, int nsplits, const float* uscale,
+                              float w, hipStream_t s) {
   const int64_t nmat = (int64_t)ntensors * nb;
   RowSsArgs ra;
+  ra.nb = nb;
+  ra.has_uscale = uscale != nullptr;
+  for (int i = 0; i < ntensors; ++i) ra.uscale[i] = uscale ? uscale[i] : 1.0f;
   ra.u = u;
   ra.u_pitch = u_pitch;
   ra.u_mstride = u_mstride;

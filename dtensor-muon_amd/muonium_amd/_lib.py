@@ -59,14 +59,14 @@ _SIGNATURES = {
     "muon_normuon_postpass": (
         _c_int,
         [_c_int, _pp, _c_int, _pp, _c_int, _vp, _c_int, _vp, _c_int, _c_i64, _c_int, _c_i64,
-         _c_i64, _c_i64, ctypes.POINTER(_c_i64), _c_int, ctypes.POINTER(_c_f32), _c_f32, _c_int,
-         ctypes.c_double, _vp],
+         _c_i64, _c_i64, ctypes.POINTER(_c_i64), _c_int, ctypes.POINTER(_c_f32),
+         ctypes.POINTER(_c_f32), _c_f32, _c_int, ctypes.c_double, _vp],
     ),
     "muon_normuon_postpass_noalloc": (
         _c_int,
         [_c_int, _pp, _c_int, _pp, _c_int, _vp, _c_int, _c_i64, _c_i64, _c_i64,
-         ctypes.POINTER(_c_i64), _c_int, ctypes.POINTER(_c_f32), _c_f32, _c_int, ctypes.c_double,
-         _vp],
+         ctypes.POINTER(_c_i64), _c_int, ctypes.POINTER(_c_f32), ctypes.POINTER(_c_f32), _c_f32,
+         _c_int, ctypes.c_double, _vp],
     ),
     "muon_lp_quantize": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp]),
     "muon_lp_dequantize": (_c_int, [_vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _vp]),

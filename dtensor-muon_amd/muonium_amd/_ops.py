@@ -369,7 +369,8 @@ def _fused_normuon_impl(params: list[Tensor], grads: list[Tensor], bufs: list[Te
                         variances: list[Tensor], lr_ratios: list[Tensor], lr: Tensor,
                         momentum: float, nesterov: bool, maximize: bool, write_back_grad: bool,
                         weight_decay: float, cautious_wd: bool, coeffs: list[float],
-                        prescale: float, beta2: float, eps: float) -> None:
+                        prescale: float, beta2: float, eps: float,
+                        u_scales: Optional[list[float]]) -> None:
     lib = _lib.load()
     g0 = grads[0]
     device = g0.device
@@ -399,7 +400,8 @@ def _fused_normuon_impl(params: list[Tensor], grads: list[Tensor], bufs: list[Te
             count, _lib.ptr_array(params), _lib.dtype_code(params[0].dtype),
             _lib.ptr_array(variances), _lib.dtype_code(variances[0].dtype), None, 0,
             ws.data_ptr(), _lib.DT_BF16, cap, steps, nb, rows, cols, None, 0,
-            _lib.f32_array(lrs), float(weight_decay), int(cautious_wd), float(beta2), s,
+            _lib.f32_array(lrs), None if u_scales is None else _lib.f32_array(u_scales),
+            float(weight_decay), int(cautious_wd), float(beta2), s,
         ),
         "muon_normuon_postpass",
     )
@@ -423,13 +425,17 @@ def fused_normuon_step(
     prescale: float,
     beta2: float,
     eps: float = 1e-7,
+    u_scales: Sequence[float] | None = None,
 ) -> None:
     """fused_step for the "normuon" algorithm: the post-pass normalizes U per stored row
-    (second-moment EMA into ``variances``, Frobenius rescale) before the apply."""
+    (second-moment EMA into ``variances``, Frobenius rescale) before the apply.
+    ``u_scales`` (one per tensor) rescales each U first, rounded to bf16: the split_sizes
+    row-block correction, applied before the normalization as the reference does."""
     args = (list(params), list(grads), list(bufs), list(variances), list(lr_ratios),
             _as_tensor(lr), float(momentum), bool(nesterov), bool(maximize),
             bool(write_back_grad), float(weight_decay), bool(cautious_wd),
-            _flatten_coeffs(coeffs), float(prescale), float(beta2), float(eps))
+            _flatten_coeffs(coeffs), float(prescale), float(beta2), float(eps),
+            None if u_scales is None else [float(v) for v in u_scales])
     if _compiling():
         torch.ops.muonium_amd.fused_normuon_step(*args)
     else:
@@ -455,7 +461,7 @@ def _normuon_postpass_impl(params: list[Tensor], us: list[Tensor], variances: li
             lib.muon_normuon_postpass(
                 1, _lib.ptr_array([p]), _lib.dtype_code(p.dtype), _lib.ptr_array([v]),
                 _lib.dtype_code(v.dtype), u.data_ptr(), _lib.dtype_code(u.dtype), ws.data_ptr(),
-                _lib.DT_BF16, cap, 0, nb, rows, cols, sp, nsp, _lib.f32_array([lr_t]),
+                _lib.DT_BF16, cap, 0, nb, rows, cols, sp, nsp, _lib.f32_array([lr_t]), None,
                 float(weight_decay), int(cautious_wd), float(beta2), s,
             ),
             "muon_normuon_postpass",

@@ -19,6 +19,7 @@ from .base import (
     orthogonalize_batch,
     orthogonalize_single,
     register_muon_algorithm,
+    split_lr_scales,
 )
 from .muon import (
     _Contig,
@@ -48,7 +49,15 @@ def _normuon_step(params, grads, bufs, variances, lr_ratios, *, lr, weight_decay
     P, G, V = _Contig(params), _Contig(grads), _Contig(variances)
     B = None if quantized else _Contig(bufs)
     pview = [p.view(g.shape) for p, g in zip(P.work, G.work)]
-    if not quantized and fused_orth_available(split_sizes, batched):
+    if split_sizes is not None and not quantized and G.work[0].dim() == 2 and \
+            fused_orth_available(None, batched):
+        _fused_normuon_split_step(
+            pview, G.work, B.work, V.work, lr_ratios, lr, split_sizes, momentum=momentum,
+            nesterov=nesterov, maximize=maximize,
+            write_back_grad=batched and nesterov and not maximize, weight_decay=weight_decay,
+            cautious_wd=cautious_wd, coeffs=coeffs, prescale=prescale, beta2=muon_beta2,
+        )
+    elif not quantized and fused_orth_available(split_sizes, batched):
         _ops.fused_normuon_step(
             pview, G.work, B.work, V.work, lr_ratios, lr, momentum=momentum, nesterov=nesterov,
             maximize=maximize, write_back_grad=batched and nesterov and not maximize,
@@ -73,6 +82,37 @@ def _normuon_step(params, grads, bufs, variances, lr_ratios, *, lr, weight_decay
     if B is not None:
         B.writeback()
     V.writeback()
+
+
+def _fused_normuon_split_step(params, grads, bufs, variances, lr_ratios, lr, split_sizes,
+                              **kw) -> None:
+    """The fused NorMuon step for 2D tensors split into row blocks (base.py:56-99 and
+    normuon.py:16-42): every block is a contiguous row slice, a matrix of its own with its
+    own slice of the per-row variance state, so equal-height blocks of all tensors run
+    through one pre-pass / iteration / NorMuon post-pass sequence. Each block's update is
+    rescaled by its split_lr_scales entry (rounded to bf16) before the normalization, as
+    `u * scales[i]` precedes _normuon_normalize in the reference."""
+    rows, cols = grads[0].shape
+    scales = split_lr_scales((rows, cols), tuple(split_sizes))
+    offsets, acc = [], 0
+    for h in split_sizes:
+        offsets.append(acc)
+        acc += h
+    by_height: dict[int, list[int]] = {}
+    for j, h in enumerate(split_sizes):
+        by_height.setdefault(h, []).append(j)
+    for h, blocks in by_height.items():
+        ps, gs, bs, vs, ratios, block_scales = [], [], [], [], [], []
+        for p, g, b, v, ratio in zip(params, grads, bufs, variances, lr_ratios):
+            for j in blocks:
+                o = offsets[j]
+                ps.append(p[o:o + h])
+                gs.append(g[o:o + h])
+                bs.append(b[o:o + h])
+                vs.append(v[o:o + h])
+                ratios.append(ratio)
+                block_scales.append(scales[j])
+        _ops.fused_normuon_step(ps, gs, bs, vs, ratios, lr, u_scales=block_scales, **kw)
 
 
 @register_muon_algorithm

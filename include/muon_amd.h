@@ -53,7 +53,7 @@ extern "C" {
 /* Maximum tensors per multi-tensor launch; larger lists are chunked internally. */
 #define MUON_MAX_TENSORS 32
 
-/* ABI version of this header (bumped on any signature change). */
+/* ABI version of this header (bumped on any signature change): 4. */
 int muon_amd_abi_version(void);
 
 /* Text of the last error reported on the calling thread ("" if none). */
@@ -148,8 +148,11 @@ int muon_postpass(int ntensors, void* const* params, int p_dtype, const void* u,
  *   U'    = U(i, :) / (sqrt(v_i') + 1e-8)
  *   U''   = U' * ||U||_F / max(||U'||_F, 1e-8)        (norms per matrix and row block)
  * and v_i' is stored into the variance state; then cautious weight decay and the apply
- * run on U'' in fp32 exactly as muon_postpass. The workspace (same quadruple as the other
- * calls; required also with an explicit u) holds the per-row scratch.
+ * run on U'' in fp32 exactly as muon_postpass. With u_scales (one per tensor, NULL for
+ * none) U is first replaced by U * u_scales[t] rounded to U's dtype, before the statistics:
+ * the split_sizes row-block rescale `u * scales[i]` of base.py:98, for a row block handed
+ * over as its own tensor. The workspace (same quadruple as the other calls; required also
+ * with an explicit u) holds the per-row scratch.
  * Replaces: muonium/optim/algorithms/normuon.py:16-55 (_normuon_normalize), :118-134
  * (NorMuon.update after the orthogonalization) and :182-203 (foreach_update). */
 #define MUON_MAX_SPLITS 16
@@ -157,8 +160,8 @@ int muon_normuon_postpass(int ntensors, void* const* params, int p_dtype,
                           void* const* variances, int v_dtype, const void* u, int u_dtype,
                           void* ws, int ws_dtype, int64_t ws_batch, int steps, int64_t nb,
                           int64_t rows, int64_t cols, const int64_t* split_sizes, int nsplits,
-                          const float* adjusted_lrs, float wd, int cautious, double beta2,
-                          void* stream);
+                          const float* adjusted_lrs, const float* u_scales, float wd,
+                          int cautious, double beta2, void* stream);
 
 /* ---- Allocation-free NorMuon post-pass ------------------------------------------------
  * No counterpart in the reference: for callers that cannot allocate device memory (code
@@ -176,8 +179,8 @@ int muon_normuon_postpass_noalloc(int ntensors, void* const* params, int p_dtype
                                   void* const* variances, int v_dtype, const void* u,
                                   int u_dtype, int64_t nb, int64_t rows, int64_t cols,
                                   const int64_t* split_sizes, int nsplits,
-                                  const float* adjusted_lrs, float wd, int cautious,
-                                  double beta2, void* stream);
+                                  const float* adjusted_lrs, const float* u_scales, float wd,
+                                  int cautious, double beta2, void* stream);
 
 /* ---- Quantized momentum (MuonLP) -------------------------------------------------
  * State of one tensor of `numel` values: codes (uint8; numel bytes for 8-bit and

@@ -80,14 +80,26 @@ def test_normuon_matches_oracle_buckets(shapes, dtype, foreach):
                                    atol=1e-7)
 
 
-def test_normuon_split_sizes_matches_oracle():
-    # row blocks normalized independently (normuon.py:30-42), through the explicit-U path
-    opt, params, p0, ref_p, ref_v = _run([(96, 32)], torch.float32, True,
-                                         split_sizes=(64, 16, 16))
-    got = params[0].detach().cpu() - p0[0]
-    assert rel_fro(got, ref_p[0] - p0[0]) < 1e-4
-    torch.testing.assert_close(opt.state[params[0]]["variance_neuron"].cpu(), ref_v[0],
-                               rtol=1e-4, atol=1e-7)
+@pytest.mark.parametrize("foreach", [True, False])
+@pytest.mark.parametrize(
+    "shapes,dtype,split",
+    [([(96, 32)], torch.float32, (64, 16, 16)),
+     ([(384, 256)] * 3, torch.bfloat16, (128, 128, 128)),
+     ([(320, 128)] * 2, torch.float32, (64, 256)),
+     ([(520, 96)], torch.bfloat16, (8, 512))],
+    ids=["small-fp32", "equal-blocks-bf16-x3", "mixed-fp32-x2", "tiny-block-bf16"],
+)
+def test_normuon_split_sizes_matches_oracle(shapes, dtype, split, foreach):
+    """Row blocks normalized independently (normuon.py:30-42) after their split_lr_scales
+    rescale: each block runs as its own matrix through the fused pre-pass, iteration and
+    NorMuon post-pass, with its slice of the variance state."""
+    opt, params, p0, ref_p, ref_v = _run(shapes, dtype, foreach, split_sizes=split)
+    tol = 2e-2 if dtype == torch.bfloat16 else 1e-4
+    for p, p_init, rp, rv in zip(params, p0, ref_p, ref_v):
+        got = p.detach().cpu().float() - p_init.float()
+        assert rel_fro(got, rp.float() - p_init.float()) < tol
+        torch.testing.assert_close(opt.state[p]["variance_neuron"].cpu(), rv, rtol=1e-4,
+                                   atol=1e-7)
 
 
 def test_normuon_beta2_weight_is_exact():

@@ -27,7 +27,7 @@ def _case(ntensors, nb, rows, cols, seed):
     return ps, us, vs, lrs
 
 
-def _run(noalloc, ps, us, vs, lrs, nb, rows, cols, splits):
+def _run(noalloc, ps, us, vs, lrs, nb, rows, cols, splits, uscales=None):
     lib = _lib.load()
     dev = torch.device(DEV)
     _lib.ensure_device(dev)
@@ -39,7 +39,8 @@ def _run(noalloc, ps, us, vs, lrs, nb, rows, cols, splits):
     s = _lib.stream(dev)
     args = (len(p), _lib.ptr_array(p), _lib.DT_BF16, _lib.ptr_array(v), _lib.DT_F32,
             u.data_ptr(), _lib.DT_BF16)
-    tail = (nb, rows, cols, sp, nsp, _lib.f32_array(lrs), 0.1, 1, 0.95, s)
+    usc = None if uscales is None else _lib.f32_array(uscales)
+    tail = (nb, rows, cols, sp, nsp, _lib.f32_array(lrs), usc, 0.1, 1, 0.95, s)
     if noalloc:
         rc = lib.muon_normuon_postpass_noalloc(*args, *tail)
     else:
@@ -54,12 +55,13 @@ def _run(noalloc, ps, us, vs, lrs, nb, rows, cols, splits):
 
 def test_noalloc_matches_workspace_entry_point_twice():
     # first call: 40 tensors (two chunks of the multi-tensor launch), 2 matrices each,
-    # with row blocks; second call smaller in every extent
+    # with row blocks and per-tensor update scales; second call smaller in every extent
     for ntensors, nb, rows, cols, splits, seed in ((40, 2, 384, 256, (128, 256), 1),
                                                    (3, 1, 100, 64, None, 2)):
         ps, us, vs, lrs = _case(ntensors, nb, rows, cols, seed)
-        ref_p, ref_v = _run(False, ps, us, vs, lrs, nb, rows, cols, splits)
-        got_p, got_v = _run(True, ps, us, vs, lrs, nb, rows, cols, splits)
+        usc = [0.75 + 0.1 * (i % 4) for i in range(ntensors)] if splits else None
+        ref_p, ref_v = _run(False, ps, us, vs, lrs, nb, rows, cols, splits, usc)
+        got_p, got_v = _run(True, ps, us, vs, lrs, nb, rows, cols, splits, usc)
         for a, b, p0 in zip(got_p, ref_p, ps):
             assert torch.equal(a, b)
             assert not torch.equal(a, p0)  # the step did move the params
@@ -74,6 +76,6 @@ def test_noalloc_refuses_sizes_beyond_the_scratch():
     rc = lib.muon_normuon_postpass_noalloc(1, _lib.ptr_array([None]), _lib.DT_BF16,
                                            _lib.ptr_array([None]), _lib.DT_F32, 16,
                                            _lib.DT_BF16, 1, 5_000_000, 8, None, 0,
-                                           _lib.f32_array([0.01]), 0.1, 1, 0.95, None)
+                                           _lib.f32_array([0.01]), None, 0.1, 1, 0.95, None)
     assert rc == 1  # MUON_ERR_SHAPE
     assert "scratch" in _lib.last_error()
