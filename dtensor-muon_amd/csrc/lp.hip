@@ -204,10 +204,12 @@ struct LpTileArgs {
   int tiles_c, tiles_used;  // column tiles (cols / 256), tiles with data or padding
   float momentum;
   int nesterov, maximize;
-  // deferred scales (blocks larger than 256 values): block / 256 and the absmax of every
-  // 256 values of a row, per matrix of this launch (rows x cols / 256 each)
+  // deferred scales (blocks larger than 256 values): block / 256, blocks per tensor, and
+  // the running absmax (as fp32 bit patterns) of every block of this launch's tensors,
+  // zero before the launch
   uint32_t block256;
-  uint32_t* amax;
+  int64_t nblocks;
+  uint32_t* bmax;
 };
 
 constexpr int LPT_ROWS = 64, LPT_COLS = 256, LPT_PITCH = LPT_COLS + 8;
@@ -468,6 +470,7 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
   constexpr int TROWS = TABLES ? LPT_ROWS / 2 : LPT_ROWS;
   __shared__ bf16_t tileT[TALL ? TROWS : 1][TALL ? LPT_PITCH : 1];
   __shared__ float wsum[4];
+  __shared__ uint32_t wmaxs[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int mat = blockIdx.y;
   float* part = a.partials + (int64_t)mat * a.parts;
@@ -542,6 +545,19 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
 
   bf16_t* x0 = (bf16_t*)a.x0 + (int64_t)mat * a.x_mstride;
   float ss = 0.0f;
+  // DEFER: when every valid row of the tile lies in one block (always, for one block per
+  // tensor) the tile's absmax goes out as one atomic max; else one per row (256 values)
+  int64_t blk0 = 0;
+  bool one_block = false;
+  uint32_t tmax = 0;
+  if constexpr (DEFER) {
+    // (a tile of padding rows only, r0 >= rows, has no block and sends nothing)
+    if (r0 < a.rows) {
+      const int64_t rl = min(r0 + LPT_ROWS - 1, a.rows - 1);
+      blk0 = lp_block_of((mb * a.rows + r0) * a.cols + c0, a.block256);
+      one_block = blk0 == lp_block_of((mb * a.rows + rl) * a.cols + c0, a.block256);
+    }
+  }
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int rl = p * 8 + rsub;
@@ -560,10 +576,13 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
       uint2 c8 = {0u, 0u};  // fp8: the 8 code bytes, packed by the conversion itself
       float sc = 0.0f;
       if constexpr (DEFER) {
-        // the block extends past this tile: leave its absmax over these 256 values (one
-        // row, 32 lanes) for the scale reduction; codes come in the requant pass
+        // the block extends past this tile: its absmax over these 256 values (one row,
+        // 32 lanes) joins the block's running max; codes come in the requant pass
         const uint32_t amax = group_max_u32(ab, 32);
-        if (chunk == 0) a.amax[(mat * a.rows + r) * (a.cols >> 8) + (c0 >> 8)] = amax;
+        if (one_block)
+          tmax = max(tmax, amax);
+        else if (chunk == 0)
+          atomicMax(a.bmax + (int64_t)t * a.nblocks + lp_block_of(e, a.block256), amax);
       } else {
         // absmax over the block_lanes consecutive lanes of this block (all in one row)
         sc = block_scale<QF>(group_max_u32(ab, block_lanes));
@@ -627,8 +646,19 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
   }
   ss = warp_sum(ss);
   if (lane == 0) wsum[wave] = ss;
+  if constexpr (DEFER) {
+    if (one_block) {
+      const uint32_t wm = wave_max_u32(tmax);
+      if (lane == 0) wmaxs[wave] = wm;
+    }
+  }
   __syncthreads();
-  if (tid == 0) part[blockIdx.x] = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+  if (tid == 0) {
+    part[blockIdx.x] = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+    if (DEFER && one_block)
+      atomicMax(a.bmax + (int64_t)t * a.nblocks + blk0,
+                max(max(wmaxs[0], wmaxs[1]), max(wmaxs[2], wmaxs[3])));
+  }
 }
 
 template <int GDT, int QF, bool DEFER>
@@ -647,41 +677,26 @@ void launch_lp_tile_q(int qf, bool tall, const LpTileArgs& a, dim3 grid, hipStre
 }
 
 // ---- deferred scales: blocks of more than 256 values --------------------------------
-// The tile kernel (DEFER) has left the absmax of every 256 values; this kernel reduces
-// them per block (a group of G lanes per block, G a power of two <= 64), keeps the old
-// scale for the requant pass and stores the new one. Nothing else reads `scales` between
-// the tile kernel and the requant pass.
+// The tile kernel (DEFER) has left each block's absmax (unsigned max of the |m| bit
+// patterns, so a NaN wins); this kernel keeps the old scale for the requant pass and
+// stores the new one, one thread per block. Nothing else reads `scales` between the tile
+// kernel and the requant pass.
 struct LpReduceArgs {
   float* scales[MUON_MAX_TENSORS];
-  const uint32_t* amax;  // [tensor][numel / 256] for the tensors of this launch
+  const uint32_t* bmax;  // [tensor][nblocks] for the tensors of this launch
   float* oldsc;          // [tensor][nblocks]
   int64_t nblocks;       // per tensor
-  int64_t parts;         // partials per block (block / 256)
-  int64_t numel256;      // numel / 256 per tensor
-  int group_shift;       // log2(G)
   int ntensors;
 };
 
 template <int QF>
 __global__ __launch_bounds__(256) void lp_scale_reduce_kernel(LpReduceArgs a) {
-  const int G = 1 << a.group_shift;
-  const int64_t gid = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> a.group_shift;
-  const int gl = threadIdx.x & (G - 1);
-  const int64_t total = a.nblocks * a.ntensors;
-  const bool active = gid < total;
-  const int64_t t = active ? gid / a.nblocks : 0, b = active ? gid % a.nblocks : 0;
-  uint32_t mx = 0;
-  if (active) {
-    const uint32_t* src = a.amax + t * a.numel256 + b * a.parts;
-    for (int64_t i = gl; i < a.parts; i += G) mx = max(mx, src[i]);
-  }
-  // groups are aligned within the wave: an xor butterfly over the group's lanes
-  for (int off = G >> 1; off > 0; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, 64));
-  if (active && gl == 0) {
-    float* sc = a.scales[t];
-    a.oldsc[t * a.nblocks + b] = sc[b];
-    sc[b] = block_scale<QF>(mx);
-  }
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= a.nblocks * a.ntensors) return;
+  const int64_t t = gid / a.nblocks, b = gid % a.nblocks;
+  float* sc = a.scales[t];
+  a.oldsc[gid] = sc[b];
+  sc[b] = block_scale<QF>(a.bmax[gid]);
 }
 
 // Requantization of blocks whose scale was reduced across tiles: recompute the new
@@ -838,6 +853,8 @@ void launch_lp_q(int qf, const LpArgs& a, dim3 grid, hipStream_t s) {
 
 }  // namespace
 
+int muon_launch_zero(void* dst, int64_t bytes, hipStream_t s);
+
 int muon_check_lp_format(int qformat, int64_t numel, int64_t block) {
   if (qformat != MUON_Q_8BIT && qformat != MUON_Q_4BIT && qformat != MUON_Q_FP8) {
     muon_set_error("lp: unknown quantization format %d", qformat);
@@ -938,15 +955,21 @@ int muon_launch_lp_prepass_tiled(int ntensors, void* const* grads, int gdt, void
   a.momentum = momentum;
   a.nesterov = nesterov;
   a.maximize = maximize;
-  // deferred scales: absmax partials of every matrix (rows * cols / 256 each), then the
-  // old scales of every tensor, in the X1 iterate buffer, which nothing reads before the
-  // first product of the iteration writes it
-  const int64_t mat_parts = rows * cols / 256;
+  // deferred scales: the blocks' running absmax, then their old scales, for every tensor
+  // of the call, in the X1 iterate buffer, which nothing reads before the first product
+  // of the iteration writes it (at most 8 bytes per 256 values; X1 holds 2 per value)
   const int64_t nblocks = numel / block;
-  uint32_t* amax_all = (uint32_t*)((char*)ws + L.off_x1);
-  float* oldsc_all = (float*)((char*)amax_all + round_up(L.batch * mat_parts * 4, 256));
+  const int64_t t_first = mat0 / nb;  // tensor index of this launch's first tensor
+  const int64_t all_tensors = L.batch / nb;
+  uint32_t* bmax_all = (uint32_t*)((char*)ws + L.off_x1);
+  float* oldsc_all = (float*)((char*)bmax_all + round_up(all_tensors * nblocks * 4, 256));
   a.block256 = (uint32_t)(block / 256);
-  a.amax = amax_all + mat0 * mat_parts;
+  a.nblocks = nblocks;
+  a.bmax = bmax_all + t_first * nblocks;
+  if (defer) {
+    const int zrc = muon_launch_zero(a.bmax, (int64_t)ntensors * nblocks * 4, s);
+    if (zrc != MUON_OK) return zrc;
+  }
   if (qf != MUON_Q_FP8 && mat0 == 0) {
     // thresholds and bucket table of this map, rebuilt per call (a few microseconds)
     uint8_t* tab = (uint8_t*)ws + L.off_qtab;
@@ -980,20 +1003,13 @@ int muon_launch_lp_prepass_tiled(int ntensors, void* const* grads, int gdt, void
   MUON_CHECK_LAUNCH("lp_prepass_tiled");
   if (!defer) return MUON_OK;
 
-  const int64_t t_first = mat0 / nb;  // tensor index of this launch's first tensor
   LpReduceArgs r;
   for (int i = 0; i < ntensors; ++i) r.scales[i] = (float*)scales[i];
-  r.amax = a.amax;
+  r.bmax = a.bmax;
   r.oldsc = oldsc_all + t_first * nblocks;
   r.nblocks = nblocks;
-  r.parts = block / 256;
-  r.numel256 = numel / 256;
-  int gshift = 0;
-  while ((1LL << gshift) < r.parts && gshift < 6) ++gshift;
-  r.group_shift = gshift;
   r.ntensors = ntensors;
-  const int64_t rthreads = nblocks * ntensors << gshift;
-  dim3 rgrid((unsigned)((rthreads + 255) / 256));
+  dim3 rgrid((unsigned)((nblocks * ntensors + 255) / 256));
   if (qf == MUON_Q_FP8)
     hipLaunchKernelGGL(lp_scale_reduce_kernel<MUON_Q_FP8>, rgrid, dim3(256), 0, s, r);
   else
