@@ -359,6 +359,11 @@ def main() -> None:
     ap.add_argument("--blas-ceiling", action="store_true",
                     help="only time the iteration's three products per bucket with torch.bmm "
                          "(hipBLASLt) as a library reference")
+    ap.add_argument("--products", default=None, choices=["q", "kv", "gate", "down"],
+                    help="only run the iteration's products on --count random bf16 matrices of "
+                         "one Llama bucket's shape (one Newton-Schulz step, twice; for "
+                         "profiling the product kernels)")
+    ap.add_argument("--count", type=int, default=32)
     ap.add_argument("--reference-suite", action="store_true",
                     help="only run the reference's own published single-device benchmarks "
                          "(Gram, NS/PE loops, the 16-matrix step) and print their times")
@@ -392,6 +397,19 @@ def main() -> None:
         return
     if args.reference_suite:
         print(json.dumps(reference_suite(dev)), flush=True)
+        return
+    if args.products:
+        from muonium_amd import _ops
+
+        shape = {"q": (4096, 4096), "kv": (1024, 4096), "gate": (14336, 4096),
+                 "down": (4096, 14336)}[args.products]
+        gen = torch.Generator(device=dev).manual_seed(0)
+        xs = [torch.randn(shape, device=dev, generator=gen).bfloat16() for _ in range(args.count)]
+        for _ in range(2):
+            _ops.orthogonalize(xs, [(3.4445, -4.7750, 2.0315)], prescale=1.0, eps=1e-7,
+                               iter_dtype=torch.bfloat16, out_dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        print(json.dumps({"products": args.products, "shape": shape, "count": args.count}))
         return
     shapes = _shapes(args.config)
     strategy, pdtype = _config_hparams(args.config)
