@@ -3,8 +3,11 @@
 bf16 iteration: compared with the oracle restated at the HIP path's bf16 storage
 points (tolerance 1e-2 rel-Frobenius, the bar stated for bf16 iteration), and bounded
 against the fp64 iteration and against the reference's compiled-Triton rounding
-points. fp32 iteration: compared with the oracle's fp32 iteration at 1e-5
-rel-Frobenius. Mirrors tests/orthogonalize/test_{newton_schulz,polar_express,
+points. fp32 iteration: compared with the same iteration in fp64 (the exact result of
+the algorithm) at 1e-5 rel-Frobenius on every shape, and with the oracle's fp32
+iteration on the CPU at 1e-5 where that run is itself within 5e-6 of fp64 (torch's
+CPU fp32 products drift to 2e-5 .. 6e-5 from fp64 on the larger shapes here, further
+than the HIP path does). Mirrors tests/orthogonalize/test_{newton_schulz,polar_express,
 orthogonalize}.py of the reference.
 """
 
@@ -23,8 +26,7 @@ pytestmark = pytest.mark.gpu
 BF16_TOL = 1e-2   # HIP bf16 vs the oracle at the same storage points
 FP64_SLACK = 1.25  # HIP bf16 vs fp64: within 1.25x the fused-bf16 oracle's own distance
 TRITON_TOL = 4e-2  # HIP bf16 vs the reference's pe_loop_triton rounding points (at least)
-FP32_TOL = 1e-5   # HIP fp32 iteration vs the fp64 iteration (non-square inputs)
-FP32_TOL_SQUARE = 3e-5  # square Gaussian inputs: the fp32 iteration itself is ~1.3e-5 off
+FP32_TOL = 1e-5   # HIP fp32 iteration vs the fp64 iteration, and vs the CPU fp32 oracle
 
 SHAPES = [(8, 256, 128), (8, 128, 256), (4, 512, 512), (256, 128), (128, 256), (3, 130, 70),
           (2, 70, 300), (1, 768, 2304)]
@@ -63,16 +65,20 @@ def test_bf16_iteration_matches_oracle(shape, steps, strategy):
 
 
 @pytest.mark.parametrize("strategy", STRATS)
-@pytest.mark.parametrize("shape", [(4, 256, 128), (128, 256), (3, 130, 70), (2, 512, 512)])
-def test_fp32_iteration_matches_oracle(shape, strategy):
-    X = _inputs(shape, seed=1)
+@pytest.mark.parametrize("shape", [(4, 256, 128), (128, 256), (3, 130, 70), (2, 512, 512),
+                                   (300, 300), (1, 1024, 1024), (2, 768, 2304)])
+@pytest.mark.parametrize("seed", [1, 2])
+def test_fp32_iteration_matches_oracle(shape, strategy, seed):
+    X = _inputs(shape, seed=seed)
     coeffs, prescale = muon_ref.strategy_coeffs(strategy, 5)
     fn = pe_loop if strategy == "polar_express" else ns_loop
     got = fn(X.cuda(), 5, eps=1e-7).cpu()
     assert got.dtype == torch.float32
-    ref = muon_ref.polar_iteration(X.double(), coeffs, prescale=prescale, eps=1e-7)
-    tol = FP32_TOL_SQUARE if shape[-1] == shape[-2] else FP32_TOL
-    assert rel_fro(got, ref) <= tol, f"{rel_fro(got, ref):.3e}"
+    exact = muon_ref.polar_iteration(X.double(), coeffs, prescale=prescale, eps=1e-7)
+    assert rel_fro(got, exact) <= FP32_TOL, f"vs fp64 {rel_fro(got, exact):.3e}"
+    cpu32 = muon_ref.polar_iteration(X.float(), coeffs, prescale=prescale, eps=1e-7)
+    if rel_fro(cpu32, exact) <= 5e-6:
+        assert rel_fro(got, cpu32) <= FP32_TOL, f"vs CPU fp32 {rel_fro(got, cpu32):.3e}"
 
 
 @pytest.mark.parametrize("strategy", STRATS)
