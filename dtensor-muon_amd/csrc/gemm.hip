@@ -14,7 +14,11 @@
 //
 // Operands live in workspaces whose extents are padded to the tile size and whose
 // padding is rewritten as zeros by every producer, so the K loop and the stores
-// need no masking (only the standalone gram_ path uses the masked variant).
+// need no masking (only the standalone gram_ path uses the masked variant). The one
+// exception is the last 128 rows and columns of a SYRK output whose valid extent
+// leaves them empty (packed tiles, below): what reads them lands only in output rows
+// that are masked to zeros or not stored.
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <type_traits>
@@ -462,11 +466,33 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
 //   * row-major stores: written element-wise to a row-major LDS tile.
 // Diagonal SYRK tiles store only their upper triangle, mirrored in place, so the
 // output is exactly symmetric.
+//
+// Packed tiles (PK). When the valid extent m leaves the last 128 rows of the padded
+// extent M empty (m <= M - 128), the last tile column holds one 128-wide unit of real
+// output, columns c0 = M - 256 .. M - 129. A launch of 256 x 256 tiles would spend half
+// of every tile of that column on padding, so the PK kernel's full tiles stop one tile
+// column short and packed tiles cover the unit: 512 rows x 128 columns per workgroup
+// (two 256-row sub-tiles of the a panel against one 128-row b panel), 8 wavefronts of
+// 64 x 128 each, the same inner loop. A matrix's packed tiles follow its full tiles in
+// one launch: in a launch of their own they re-read every row panel from HBM (the
+// m = 1408 X X^T packed tiles ran 1.7x as long as a full tile each, memory-bound). The unit's own 128 x 128 diagonal block lies in
+// one packed tile and is stored symmetric as a diagonal tile is; rows and columns from
+// M - 128 on are neither computed into the output nor stored. Readers of the result
+// never reach them: the products contract over K <= M - 128 and mask rows beyond m.
+// Per matrix the packed layout takes T(T-1)/2 + ceil((2T - 1)/4) workgroups instead
+// of T(T+1)/2 (T = M / 256): 18 instead of 21 at m = 1408.
 constexpr int V2_BK = 64, V2_ROWB = V2_BK * 2, V2_TILEB = 256 * V2_ROWB;
 constexpr int V2_STAGEB = 2 * V2_TILEB;
 constexpr int V2_EP_PITCH = 256 + 8;  // staging row pitch (elements)
 constexpr int V2_SMEM = (2 * V2_STAGEB > 256 * V2_EP_PITCH * 2) ? 2 * V2_STAGEB
                                                                    : 256 * V2_EP_PITCH * 2;
+constexpr int V2P_TP = 512 + 8;  // packed: transposed staging, 128 rows of 512
+constexpr int V2P_RP = 128 + 8;  // packed: row-major staging, 512 rows of 128
+constexpr int v2_smem(bool pk) {
+  return !pk ? V2_SMEM
+             : std::max(2 * (512 + 128) * V2_ROWB, std::max(128 * V2P_TP * 2, 512 * V2P_RP * 2));
+}
+static_assert(v2_smem(true) <= 160 * 1024, "packed SYRK tile fits the LDS");
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -532,19 +558,60 @@ MUON_DEVICE void frag_load(bf16x8_mfma (&na)[2], bf16x8_mfma (&nb)[4], uint32_t 
 MUON_DEVICE void mfma_to_valu_wait() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
 MUON_DEVICE void valu_to_mfma_wait() { asm volatile("s_nop 4" ::: "memory"); }
 
-template <int MODE>
+template <int MODE, bool PK>
 __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
-  constexpr int NW = 8, WGN = 2, WM = 64, WN = 128, FM = 2, FN = 4;
-  constexpr int SPW = (V2_TILEB / 1024) / NW;  // 1 KB load slabs per wave per operand
+  // PK: the launch mixes the full tiles of the first T-1 tile columns' triangle with the
+  // packed tiles of the last column; each matrix's packed tiles follow its full tiles in
+  // the tile order, so the workgroups of one XCD share the matrix's row panels in L2
+  constexpr int NW = 8, WM = 64, WN = 128, FM = 2, FN = 4;
   extern __shared__ __align__(16) uint8_t smem[];
 
-  int bidx, tm, tn;
-  map_tile(g, MODE, bidx, tm, tn);
+  int bidx, tm = 0, tn = 0;
+  bool pk = false;  // this workgroup's tile is a packed one
+  // arow0: first output row; packed: rows arow0 .. arow0 + 511 (logical), the second
+  // sub-tile's operand rows read from arow1, which differs from arow0 + 256 only when
+  // that sub-tile lies wholly in the padding (it then re-reads valid rows, unstored)
+  int64_t arow0, arow1, brow0;
+  if constexpr (PK) {
+    int64_t L = blockIdx.x;
+    const int64_t total = (int64_t)gridDim.x;
+    if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
+    bidx = (int)(L / g.tiles_per_batch);
+    int t = (int)(L % g.tiles_per_batch);
+    const int T1 = g.tiles_m - 1;
+    const int ntri = T1 * (T1 + 1) / 2;
+    const int64_t mpad = (int64_t)g.tiles_m * 256;
+    if (t < ntri) {
+      int r = 0;
+      while (t >= T1 - r) {
+        t -= T1 - r;
+        ++r;
+      }
+      tm = r;
+      tn = r + t;
+      arow0 = (int64_t)tm * 256;
+      arow1 = arow0 + 256;
+      brow0 = (int64_t)tn * 256;
+    } else {
+      pk = true;
+      arow0 = (int64_t)(t - ntri) * 512;
+      arow1 = std::min(arow0 + 256, mpad - 256);
+      brow0 = mpad - 256;
+    }
+  } else {
+    map_tile(g, MODE, bidx, tm, tn);
+    arow0 = (int64_t)tm * 256;
+    arow1 = arow0 + 256;
+    brow0 = (int64_t)tn * 256;
+  }
+  // operand panels: full tiles 256 a rows and 256 b rows (waves 4 x 2), packed tiles
+  // 512 a rows and 128 b rows (waves 8 x 1); each wave computes 64 x 128 either way
+  const int arows = pk ? 512 : 256;
+  const int stageb = (pk ? 640 : 512) * V2_ROWB;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WGN, wn = wave % WGN;
+  const int wm = pk ? wave : wave >> 1, wn = pk ? 0 : wave & 1;
   const bf16_t* A = (const bf16_t*)g.a + (int64_t)bidx * g.sa;
   const bf16_t* B = (const bf16_t*)g.b + (int64_t)bidx * g.sb;
-  const int64_t arow0 = (int64_t)tm * 256, brow0 = (int64_t)tn * 256;
   const int lda_b = (int)(g.lda * 2), ldb_b = (int)(g.ldb * 2);
   const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(A + arow0 * g.lda), 0, 0x7fffffff, 0x00020000);
@@ -556,16 +623,27 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
   const int lch = (lane & 7) ^ kswz(r_in);
   const int voa = r_in * lda_b + lch * 16;
   const int vob = r_in * ldb_b + lch * 16;
-  auto issue = [&](int kt, int st) {
-    uint8_t* sa = smem + st * V2_STAGEB;
-    uint8_t* sb = sa + V2_TILEB;
+  // PK: per-lane byte offsets of the a-panel slabs (slabs 4-7, packed tiles only, from
+  // the second sub-tile's rows arow1)
+  int voq[8];
 #pragma unroll
-    for (int q = 0; q < SPW; ++q) {
+  for (int q = 0; q < 8; ++q)
+    voq[q] = voa + (int)((q >= 4 ? arow1 - arow0 + (q - 4) * NW * 8 : q * NW * 8) * lda_b);
+  auto issue = [&](int kt, int st) {
+    uint8_t* sa = smem + st * stageb;
+    uint8_t* sb = sa + arows * V2_ROWB;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
       const int slab = q * NW + wave;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(sa + slab * 1024), 16, voa,
-                                               q * NW * 8 * lda_b + kt * V2_ROWB, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_ptr_t)(sb + slab * 1024), 16, vob,
-                                               q * NW * 8 * ldb_b + kt * V2_ROWB, 0, 0);
+      if (q < 4 || pk) {
+        const int vo = PK ? voq[q] : voa;
+        const int so = PK ? kt * V2_ROWB : q * NW * 8 * lda_b + kt * V2_ROWB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(sa + slab * 1024), 16, vo, so,
+                                                 0, 0);
+      }
+      if (q < 2 || (q < 4 && !pk))
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_ptr_t)(sb + slab * 1024), 16, vob,
+                                                 q * NW * 8 * ldb_b + kt * V2_ROWB, 0, 0);
     }
   };
 
@@ -575,7 +653,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
   int foff[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) foff[ks] = fr * V2_ROWB + (((ks * 2 + fh) ^ kswz(fr)) << 4);
-  const int abase = wm * WM * V2_ROWB, bbase = V2_TILEB + wn * WN * V2_ROWB;
+  const int abase = wm * WM * V2_ROWB, bbase = arows * V2_ROWB + wn * WN * V2_ROWB;
 
   float alpha = g.alpha, beta = g.beta;
   if (g.scale_mode != 0) {
@@ -588,8 +666,9 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
     }
   }
   const float ratio = beta != 0.0f ? beta / alpha : 0.0f;
-  // K-tile whose k range equals this wave's output rows (WM == BK)
-  const int kdiag = ratio != 0.0f ? (int)((arow0 + wm * WM) / V2_BK) : -1;
+  // K-tile whose k range equals this wave's output rows (WM == BK), as read
+  const int64_t wrow = pk && wm >= 4 ? arow1 + (wm - 4) * WM : arow0 + wm * WM;
+  const int kdiag = ratio != 0.0f ? (int)(wrow / V2_BK) : -1;
 
   f32x16 acc[FM][FN];
 #pragma unroll
@@ -601,8 +680,8 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
 
   const int KT = (int)(g.K / V2_BK);
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
-  auto aaddr = [&](int st, int ks) -> uint32_t { return lds0 + st * V2_STAGEB + abase + foff[ks]; };
-  auto baddr = [&](int st, int ks) -> uint32_t { return lds0 + st * V2_STAGEB + bbase + foff[ks]; };
+  auto aaddr = [&](int st, int ks) -> uint32_t { return lds0 + st * stageb + abase + foff[ks]; };
+  auto baddr = [&](int st, int ks) -> uint32_t { return lds0 + st * stageb + bbase + foff[ks]; };
   bf16x8_mfma a0[FM], b0[FN], a1[FM], b1[FN];
   issue(0, 0);
   wait_vmcnt0();
@@ -618,7 +697,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
       // cin(i, j) = b(j, i): row j of the b panel, k offset i - kt*BK (4 consecutive
       // rows i of one accumulator group are 8 contiguous bytes of that row)
       mfma_to_valu_wait();
-      const uint8_t* sb = smem + cs * V2_STAGEB + bbase;
+      const uint8_t* sb = smem + cs * stageb + bbase;
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
@@ -645,6 +724,89 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
 
   // ---- epilogue: stage through LDS, store 16-byte row chunks ----
   bf16_t* T = (bf16_t*)smem;
+  if (PK && pk) {
+    // Packed tile: logical rows arow0 + il (il < 512) against columns c0 + jl (jl <
+    // 128), c0 = brow0. Rows below c0 are off-diagonal (stored, and mirrored into rows
+    // c0 + jl); rows c0 .. c0 + 127 are the unit's diagonal block (upper triangle
+    // stored, mirrored in place); later rows are padding, not stored.
+    const int64_t c0 = brow0;
+    bf16_t* out = (bf16_t*)g.out + (int64_t)bidx * g.so;
+    // the tile as bf16 pairs, converted once: hv[fm][fn][2 rg + h] holds rows
+    // 4 rg + 2 h, +1 of the accumulator's lane column (zeros outside Mv x Nv)
+    const int rem_i = (int)std::max<int64_t>(
+        -1, std::min<int64_t>(g.Mv - (arow0 + wm * WM + fh * 4), 1 << 20));
+    const int rem_j = (int)std::max<int64_t>(-1, std::min<int64_t>(g.Nv - (c0 + fr), 1 << 20));
+    uint32_t hv[FM][FN][8];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const int il0 = fm * 32 + (r >> 2) * 8 + (r & 3);  // this lane's row, less fh*4
+          const bool vj = fn * 32 < rem_j;
+          const float v0 = vj && il0 < rem_i ? alpha * acc[fm][fn][r] : 0.0f;
+          const float v1 = vj && il0 + 1 < rem_i ? alpha * acc[fm][fn][r + 1] : 0.0f;
+          hv[fm][fn][r >> 1] = (uint32_t)f32_to_bf16(v0) | ((uint32_t)f32_to_bf16(v1) << 16);
+        }
+    // mirror: T[jl][il], 4 consecutive il per lane -> one 8-byte write
+    lds_barrier();
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const int jl = fn * 32 + fr;
+          const int il = wm * WM + fm * 32 + rg * 8 + fh * 4;
+          *(uint2*)(T + jl * V2P_TP + il) = make_uint2(hv[fm][fn][2 * rg], hv[fm][fn][2 * rg + 1]);
+        }
+    lds_barrier();
+#pragma unroll 4
+    for (int it = 0; it < 16; ++it) {
+      const int id = it * 512 + tid;
+      const int jl = id >> 6, c = (id & 63) * 8;
+      if (arow0 + c < c0) {  // 8 rows of one off-diagonal unit
+        const uint4 w = *(const uint4*)(T + jl * V2P_TP + c);
+        *(uint4*)(out + (c0 + jl) * g.ldo + arow0 + c) = w;
+      }
+    }
+    // row-major: T[il][jl]
+    lds_barrier();
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int il = wm * WM + fm * 32 + (r >> 2) * 8 + fh * 4 + (r & 3);
+          const int jl = fn * 32 + fr;
+          T[il * V2P_RP + jl] = (bf16_t)(hv[fm][fn][r >> 1] >> (16 * (r & 1)));
+        }
+    lds_barrier();
+    const int dl0 = (int)(c0 - arow0);  // staging row of the diagonal block's first row
+#pragma unroll 4
+    for (int it = 0; it < 16; ++it) {
+      const int id = it * 512 + tid;
+      const int il = id >> 4, c = (id & 15) * 8;
+      const int dr = il - dl0;  // row within the diagonal block (< 0: off-diagonal)
+      if (dr >= 128) continue;  // padding rows
+      uint4 w;
+      if (dr < 0 || c >= dr) {
+        w = *(const uint4*)(T + il * V2P_RP + c);
+      } else {
+        // diagonal block, chunk reaching below the diagonal: those columns come from
+        // the computed (upper) element of the mirror position
+        uint16_t e[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          e[q] = (c + q < dr) ? T[(dl0 + c + q) * V2P_RP + dr] : T[il * V2P_RP + c + q];
+        __builtin_memcpy(&w, e, 16);
+      }
+      *(uint4*)(out + (arow0 + il) * g.ldo + c0 + c) = w;
+    }
+    return;
+  }
   const bool diag = MODE == MODE_SYRK && tm == tn;
   const int row0w = wm * WM, col0w = wn * WN;  // wave origin within the tile
   auto val = [&](int fm, int fn, int r) -> float {
@@ -1200,8 +1362,13 @@ int reserve_bf16_lds() {
       if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, BF_SMEM) !=
           hipSuccess)
         status = -1;
-    if (hipFuncSetAttribute((const void*)gemm_bf16_v2_kernel<MODE_SYRK>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, V2_SMEM) != hipSuccess)
+    if (hipFuncSetAttribute((const void*)gemm_bf16_v2_kernel<MODE_SYRK, false>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, v2_smem(false)) !=
+        hipSuccess)
+      status = -1;
+    if (hipFuncSetAttribute((const void*)gemm_bf16_v2_kernel<MODE_SYRK, true>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, v2_smem(true)) !=
+        hipSuccess)
       status = -1;
     if (hipFuncSetAttribute((const void*)gemm_bf16_nn4_kernel,
                             hipFuncAttributeMaxDynamicSharedMemorySize, N4_SMEM) != hipSuccess)
@@ -1323,7 +1490,20 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
       const int wgs = (int)std::min<int64_t>(blocks, device_cus());
       hipLaunchKernelGGL(gemm_bf16_nn4_kernel, dim3((unsigned)wgs), dim3(256), N4_SMEM, stream, g);
     } else if (!masked && (alpha != 0.0f || beta == 0.0f)) {
-      hipLaunchKernelGGL(gemm_bf16_v2_kernel<MODE_SYRK>, grid, dim3(512), V2_SMEM, stream, g);
+      // the last 128 rows padding only: the last tile column's real unit in packed tiles,
+      // in the same launch as the full tiles
+      const int T = g.tiles_m;
+      if (T >= 2 && Mv <= M - 128 && Nv == Mv) {
+        GemmArgs gp = g;
+        gp.tiles_per_batch = (T - 1) * T / 2 + (2 * T - 1 + 3) / 4;
+        gp.tiles_total = gp.tiles_per_batch * (int)batch;
+        hipLaunchKernelGGL((gemm_bf16_v2_kernel<MODE_SYRK, true>),
+                           dim3((unsigned)(gp.tiles_per_batch * batch)), dim3(512),
+                           v2_smem(true), stream, gp);
+      } else {
+        hipLaunchKernelGGL((gemm_bf16_v2_kernel<MODE_SYRK, false>), grid, dim3(512),
+                           v2_smem(false), stream, g);
+      }
     } else {
       if (masked) LAUNCH_BF(MODE_SYRK, true); else LAUNCH_BF(MODE_SYRK, false);
     }
