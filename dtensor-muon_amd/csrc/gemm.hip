@@ -558,6 +558,42 @@ MUON_DEVICE void frag_load(bf16x8_mfma (&na)[2], bf16x8_mfma (&nb)[4], uint32_t 
 MUON_DEVICE void mfma_to_valu_wait() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
 MUON_DEVICE void valu_to_mfma_wait() { asm volatile("s_nop 4" ::: "memory"); }
 
+typedef __attribute__((ext_vector_type(2))) float f2x;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf2x;  // v_cvt_pk_bf16_f32 (RNE)
+
+// A finished 64 x 128 wave tile as bf16 pairs, converted once with the hardware RNE pair
+// conversion: hv[fm][fn][2 rg + h] holds rows fm*32 + rg*8 + fh*4 + 2h and + 1 of the
+// lane's column fn*32 + lane%32. Unless `full`, elements outside the valid extent are
+// cleared to +0 (whatever they held): rem_i counts the valid rows from this lane's first
+// row (fh*4 included), rem_j the valid columns from its column.
+MUON_DEVICE void v2_pack(const f32x16 (&acc)[2][4], float alpha, bool full, int rem_i,
+                         int rem_j, uint32_t (&hv)[2][4][8]) {
+#pragma unroll
+  for (int fm = 0; fm < 2; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < 4; ++fn)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const f2x v = {alpha * acc[fm][fn][r], alpha * acc[fm][fn][r + 1]};
+        hv[fm][fn][r >> 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2x));
+      }
+  if (full) return;
+#pragma unroll
+  for (int fm = 0; fm < 2; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < 4; ++fn)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const int il0 = fm * 32 + (r >> 2) * 8 + (r & 3);
+        const bool vj = fn * 32 < rem_j;
+        const uint32_t keep = (vj && il0 < rem_i ? 0x0000ffffu : 0u) |
+                              (vj && il0 + 1 < rem_i ? 0xffff0000u : 0u);
+        hv[fm][fn][r >> 1] &= keep;
+      }
+}
+
+MUON_DEVICE int clamp_rem(int64_t v) { return (int)std::max<int64_t>(-1, std::min<int64_t>(v, 1 << 20)); }
+
 template <int MODE, bool PK>
 __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
   // PK: the launch mixes the full tiles of the first T-1 tile columns' triangle with the
@@ -731,24 +767,9 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
     // stored, mirrored in place); later rows are padding, not stored.
     const int64_t c0 = brow0;
     bf16_t* out = (bf16_t*)g.out + (int64_t)bidx * g.so;
-    // the tile as bf16 pairs, converted once: hv[fm][fn][2 rg + h] holds rows
-    // 4 rg + 2 h, +1 of the accumulator's lane column (zeros outside Mv x Nv)
-    const int rem_i = (int)std::max<int64_t>(
-        -1, std::min<int64_t>(g.Mv - (arow0 + wm * WM + fh * 4), 1 << 20));
-    const int rem_j = (int)std::max<int64_t>(-1, std::min<int64_t>(g.Nv - (c0 + fr), 1 << 20));
     uint32_t hv[FM][FN][8];
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) {
-          const int il0 = fm * 32 + (r >> 2) * 8 + (r & 3);  // this lane's row, less fh*4
-          const bool vj = fn * 32 < rem_j;
-          const float v0 = vj && il0 < rem_i ? alpha * acc[fm][fn][r] : 0.0f;
-          const float v1 = vj && il0 + 1 < rem_i ? alpha * acc[fm][fn][r + 1] : 0.0f;
-          hv[fm][fn][r >> 1] = (uint32_t)f32_to_bf16(v0) | ((uint32_t)f32_to_bf16(v1) << 16);
-        }
+    v2_pack(acc, alpha, arow0 + 512 <= g.Mv && c0 + 128 <= g.Nv,
+            clamp_rem(g.Mv - (arow0 + wm * WM + fh * 4)), clamp_rem(g.Nv - (c0 + fr)), hv);
     // mirror: T[jl][il], 4 consecutive il per lane -> one 8-byte write
     lds_barrier();
 #pragma unroll
@@ -809,11 +830,9 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
   }
   const bool diag = MODE == MODE_SYRK && tm == tn;
   const int row0w = wm * WM, col0w = wn * WN;  // wave origin within the tile
-  auto val = [&](int fm, int fn, int r) -> float {
-    const int64_t i = arow0 + row0w + fm * 32 + (r >> 2) * 8 + fh * 4 + (r & 3);
-    const int64_t j = brow0 + col0w + fn * 32 + fr;
-    return (i < g.Mv && j < g.Nv) ? alpha * acc[fm][fn][r] : 0.0f;
-  };
+  uint32_t hv[FM][FN][8];
+  v2_pack(acc, alpha, arow0 + 256 <= g.Mv && brow0 + 256 <= g.Nv,
+          clamp_rem(g.Mv - (arow0 + row0w + fh * 4)), clamp_rem(g.Nv - (brow0 + col0w + fr)), hv);
   bf16_t* out = g.out ? (bf16_t*)g.out + (int64_t)bidx * g.so : nullptr;
   bf16_t* out_t = g.out_t ? (bf16_t*)g.out_t + (int64_t)bidx * g.st : nullptr;
   const int64_t ldt = MODE == MODE_SYRK ? g.ldo : g.ldt;
@@ -832,12 +851,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
         for (int rg = 0; rg < 4; ++rg) {
           const int jl = col0w + fn * 32 + fr;
           const int il = row0w + fm * 32 + rg * 8 + fh * 4;
-          uint2 w;
-          w.x = (uint32_t)f32_to_bf16(val(fm, fn, rg * 4)) |
-                ((uint32_t)f32_to_bf16(val(fm, fn, rg * 4 + 1)) << 16);
-          w.y = (uint32_t)f32_to_bf16(val(fm, fn, rg * 4 + 2)) |
-                ((uint32_t)f32_to_bf16(val(fm, fn, rg * 4 + 3)) << 16);
-          *(uint2*)(T + jl * V2_EP_PITCH + il) = w;
+          *(uint2*)(T + jl * V2_EP_PITCH + il) = make_uint2(hv[fm][fn][2 * rg], hv[fm][fn][2 * rg + 1]);
         }
     lds_barrier();
 #pragma unroll 4
@@ -859,7 +873,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
         for (int r = 0; r < 16; ++r) {
           const int il = row0w + fm * 32 + (r >> 2) * 8 + fh * 4 + (r & 3);
           const int jl = col0w + fn * 32 + fr;
-          T[il * V2_EP_PITCH + jl] = f32_to_bf16(val(fm, fn, r));
+          T[il * V2_EP_PITCH + jl] = (bf16_t)(hv[fm][fn][r >> 1] >> (16 * (r & 1)));
         }
     lds_barrier();
 #pragma unroll 4
@@ -946,8 +960,6 @@ constexpr int N4_EPB = 32 * 256;                 // epilogue staging per wave: 3
 constexpr int N4_SMEM = 2 * NN_STAGEB + 4 * N4_EPB;  // 160 KiB
 typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
-typedef __attribute__((ext_vector_type(2))) float f2x;
-typedef __attribute__((ext_vector_type(2))) __bf16 bf2x;  // v_cvt_pk_bf16_f32 (RNE)
 
 // buffer descriptor words (raw, stride 0, 2^31 - 1 bytes; num_records 0 for `none`)
 MUON_DEVICE u32x4 n4_rsrc(const void* base, bool none) {
