@@ -1417,6 +1417,364 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn4_kernel(GemmArgs g) {
   }
 }
 
+// ----------------------------------------------------------------------------------
+// The persistent B X kernel on 16 x 16 x 32 MFMAs, for K of at least 2048.
+//
+// Same tiling, waves, LDS layout, tile order and epilogue staging as gemm_bf16_nn4_kernel;
+// the wave's 128 x 128 block is 8 x 8 accumulators of 16 x 16 (AGPRs) and a K-tile is two
+// 32-k substeps of 64 MFMAs. A single wave issues v_mfma_f32_32x32x16_bf16 at most every 32
+// cycles and each 16-byte fragment read between them costs it issue time; with
+// v_mfma_f32_16x16x32_bf16 the same LDS bytes per FLOP ride along at almost no cost: a
+// probe loop with this kernel's reads, DMA and barrier took 35.7 cycles per
+// 32 x 32 x 16-equivalent against about 48 for the 32 x 32 x 16 loop.
+//
+// Fragments (lane l, r = l % 16, g = l / 16): srcA is X^T, 8 consecutive k (two tr reads)
+// of column 16 fj + r; srcB is B, 8 consecutive k (one b128) of row 16 fi + r; the
+// accumulator register q of block (fi, fj) is X'(16 fi + r, 16 fj + 4 g + q).
+//
+// The beta term is added into the accumulators during the two K-tiles whose k range is the
+// wave's rows (no registers hold X values through the loop, which the double-buffered
+// fragments need); those two K-tiles are peeled off the loop. It takes its own K-loop
+// structure and per-tile work, so below K = 2048 (where that work weighs more)
+// gemm_bf16_nn4_kernel is faster and is used instead.
+#define M16(C, X, B) "v_mfma_f32_16x16x32_bf16 %[" #C "], %[" #X "], %[" #B "], %[" #C "]\n\t"
+#define N16_OUT(ACC)                                                                      \
+  [c0] "+a"(ACC[0]), [c1] "+a"(ACC[1]), [c2] "+a"(ACC[2]), [c3] "+a"(ACC[3]),               \
+  [c4] "+a"(ACC[4]), [c5] "+a"(ACC[5]), [c6] "+a"(ACC[6]), [c7] "+a"(ACC[7]),               \
+  [nb] "=&v"(nb), [nl] "=&v"(nl), [nh] "=&v"(nh)
+#define N16_IN                                                                            \
+  [b] "v"(cb), [x0] "v"(cx[0]), [x1] "v"(cx[1]), [x2] "v"(cx[2]), [x3] "v"(cx[3]),          \
+  [x4] "v"(cx[4]), [x5] "v"(cx[5]), [x6] "v"(cx[6]), [x7] "v"(cx[7]), [ba] "v"(ba),         \
+  [xa] "v"(xa), [o0] "i"(XO), [o1] "i"(XO + 4 * NN_XROWB), [ob] "i"(FI * 16 * V2_ROWB)
+// One block of a 32-k substep: the 8 MFMAs of row block FI (accumulators acc[0..7] hold
+// X' rows 16 FI + lane%16, columns 16 fj + 4 (lane/16) .. +3) on the current fragments,
+// with 3 reads of the next substep's fragments: both halves of X fragment FI (tr reads at
+// xa + XO, + 2 KB) and B fragment FI (b128 at ba + 2 KB FI).
+template <int FI, int XO>
+MUON_DEVICE void n16_block(f32x4 (&acc)[8], const bf16x8_mfma& cb, const bf16x8_mfma (&cx)[8],
+                           bf16x8_mfma& nb, i16x4& nl, i16x4& nh, uint32_t ba, uint32_t xa) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %[nl], %[xa] offset:%[o0]\n\t" M16(c0, x0, b)
+      M16(c1, x1, b) M16(c2, x2, b)
+      "ds_read_b64_tr_b16 %[nh], %[xa] offset:%[o1]\n\t" M16(c3, x3, b)
+      M16(c4, x4, b) M16(c5, x5, b)
+      "ds_read_b128 %[nb], %[ba] offset:%[ob]\n\t" M16(c6, x6, b)
+      M16(c7, x7, b)
+      : N16_OUT(acc)
+      : N16_IN);
+}
+// The same with two loads of the DMA of a K-tile (slabs 2 FI and 2 FI + 1 of the 16 this
+// wave issues per K-tile: B panel slabs for FI < 4, X panel slabs for FI >= 4), each after an
+// MFMA. m0 and the scalar offsets of both loads come in precomputed.
+template <int FI, int XO>
+MUON_DEVICE void n16_block_dma(f32x4 (&acc)[8], const bf16x8_mfma& cb, const bf16x8_mfma (&cx)[8],
+                               bf16x8_mfma& nb, i16x4& nl, i16x4& nh, uint32_t ba, uint32_t xa,
+                               int vo, u32x4 rs, int so0, int so1, uint32_t m00, uint32_t m01) {
+  asm volatile(
+      "s_mov_b32 m0, %[m00]\n\t"
+      "ds_read_b64_tr_b16 %[nl], %[xa] offset:%[o0]\n\t" M16(c0, x0, b)
+      "buffer_load_dwordx4 %[vo], %[rs], %[so0] offen lds\n\t"
+      M16(c1, x1, b) "s_mov_b32 m0, %[m01]\n\t" M16(c2, x2, b)
+      "ds_read_b64_tr_b16 %[nh], %[xa] offset:%[o1]\n\t" M16(c3, x3, b)
+      "buffer_load_dwordx4 %[vo], %[rs], %[so1] offen lds\n\t"
+      M16(c4, x4, b) M16(c5, x5, b)
+      "ds_read_b128 %[nb], %[ba] offset:%[ob]\n\t" M16(c6, x6, b)
+      M16(c7, x7, b)
+      : N16_OUT(acc)
+      : N16_IN, [vo] "v"(vo), [rs] "s"(rs), [so0] "s"(so0), [so1] "s"(so1), [m00] "s"(m00),
+        [m01] "s"(m01)
+      : "m0", "memory");
+}
+#undef N16_OUT
+#undef N16_IN
+#undef M16
+
+// All 24 fragment reads of one substep without MFMAs (pipeline start).
+template <int XO>
+MUON_DEVICE void n16_frag_load(bf16x8_mfma (&nb)[8], i16x4 (&nl)[8], i16x4 (&nh)[8], uint32_t ba,
+                               const uint32_t (&xa)[8]) {
+#pragma unroll
+  for (int f = 0; f < 8; ++f) {
+    asm volatile("ds_read_b64_tr_b16 %0, %3 offset:%4\n\t"
+                 "ds_read_b64_tr_b16 %1, %3 offset:%5\n\t"
+                 "ds_read_b128 %2, %6 offset:%7"
+                 : "=&v"(nl[f]), "=&v"(nh[f]), "=&v"(nb[f])
+                 : "v"(xa[f]), "i"(XO), "i"(XO + 4 * NN_XROWB), "v"(ba), "i"(0));
+    ba += 16 * V2_ROWB;
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+MUON_DEVICE void n16_join(bf16x8_mfma (&cx)[8], const i16x4 (&lo)[8], const i16x4 (&hi)[8]) {
+#pragma unroll
+  for (int f = 0; f < 8; ++f) {
+    const __attribute__((ext_vector_type(8))) short v = __builtin_shufflevector(lo[f], hi[f], 0, 1, 2, 3, 4, 5, 6, 7);
+    cx[f] = __builtin_bit_cast(bf16x8_mfma, v);
+  }
+}
+
+// One 32-k substep: 8 blocks, then the wait for its 24 reads.
+template <int XO>
+MUON_DEVICE void n16_substep(f32x4 (&acc)[8][8], const bf16x8_mfma (&cb)[8], const bf16x8_mfma (&cx)[8],
+                             bf16x8_mfma (&nb)[8], i16x4 (&nl)[8], i16x4 (&nh)[8], uint32_t ba,
+                             const uint32_t (&xa)[8]) {
+  n16_block<0, XO>(acc[0], cb[0], cx, nb[0], nl[0], nh[0], ba, xa[0]);
+  n16_block<1, XO>(acc[1], cb[1], cx, nb[1], nl[1], nh[1], ba, xa[1]);
+  n16_block<2, XO>(acc[2], cb[2], cx, nb[2], nl[2], nh[2], ba, xa[2]);
+  n16_block<3, XO>(acc[3], cb[3], cx, nb[3], nl[3], nh[3], ba, xa[3]);
+  n16_block<4, XO>(acc[4], cb[4], cx, nb[4], nl[4], nh[4], ba, xa[4]);
+  n16_block<5, XO>(acc[5], cb[5], cx, nb[5], nl[5], nh[5], ba, xa[5]);
+  n16_block<6, XO>(acc[6], cb[6], cx, nb[6], nl[6], nh[6], ba, xa[6]);
+  n16_block<7, XO>(acc[7], cb[7], cx, nb[7], nl[7], nh[7], ba, xa[7]);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// The substep after the barrier, carrying the DMA of one whole K-tile into one stage: blocks
+// 0-3 load the B panel slabs (rows 32 q + 8 wave .. +7, q = 0..7), blocks 4-7 the X panel
+// slabs (rows 8 q + 2 wave, +1).
+template <int XO>
+MUON_DEVICE void n16_substep_dma(f32x4 (&acc)[8][8], const bf16x8_mfma (&cb)[8],
+                                 const bf16x8_mfma (&cx)[8], bf16x8_mfma (&nb)[8], i16x4 (&nl)[8],
+                                 i16x4 (&nh)[8], uint32_t ba, const uint32_t (&xa)[8], int voa,
+                                 int vox, u32x4 rsa, u32x4 rsx, int soa, int sox, int sta, int stx,
+                                 uint32_t m0a, uint32_t m0x) {
+  n16_block_dma<0, XO>(acc[0], cb[0], cx, nb[0], nl[0], nh[0], ba, xa[0], voa, rsa, soa, soa + sta, m0a, m0a + 0x1000);
+  n16_block_dma<1, XO>(acc[1], cb[1], cx, nb[1], nl[1], nh[1], ba, xa[1], voa, rsa, soa + 2 * sta, soa + 3 * sta, m0a + 0x2000, m0a + 0x3000);
+  n16_block_dma<2, XO>(acc[2], cb[2], cx, nb[2], nl[2], nh[2], ba, xa[2], voa, rsa, soa + 4 * sta, soa + 5 * sta, m0a + 0x4000, m0a + 0x5000);
+  n16_block_dma<3, XO>(acc[3], cb[3], cx, nb[3], nl[3], nh[3], ba, xa[3], voa, rsa, soa + 6 * sta, soa + 7 * sta, m0a + 0x6000, m0a + 0x7000);
+  n16_block_dma<4, XO>(acc[4], cb[4], cx, nb[4], nl[4], nh[4], ba, xa[4], vox, rsx, sox, sox + stx, m0x, m0x + 0x1000);
+  n16_block_dma<5, XO>(acc[5], cb[5], cx, nb[5], nl[5], nh[5], ba, xa[5], vox, rsx, sox + 2 * stx, sox + 3 * stx, m0x + 0x2000, m0x + 0x3000);
+  n16_block_dma<6, XO>(acc[6], cb[6], cx, nb[6], nl[6], nh[6], ba, xa[6], vox, rsx, sox + 4 * stx, sox + 5 * stx, m0x + 0x4000, m0x + 0x5000);
+  n16_block_dma<7, XO>(acc[7], cb[7], cx, nb[7], nl[7], nh[7], ba, xa[7], vox, rsx, sox + 6 * stx, sox + 7 * stx, m0x + 0x6000, m0x + 0x7000);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// ratio * X(i, j .. j+3) added into the accumulators of row blocks FI0 .. FI0+3 (X panel
+// rows (fi - FI0) * 16 + lane%16 of the K-tile staged at sx, columns 128 wn + 16 fj +
+// 4 (lane/16)). Each accumulator is copied out of and back into its own AGPRs.
+template <int FI0>
+MUON_DEVICE void n16_beta(f32x4 (&acc)[8][8], uint32_t sx, int wn, int lane, float ratio) {
+  asm volatile("" : "+v"(sx));
+  const int r = lane & 15, g = lane >> 4;
+  const uint32_t rowb = sx + r * NN_XROWB + (g & 1) * 8;
+#pragma unroll
+  for (int fj = 0; fj < 8; ++fj) {
+    const uint32_t a = rowb + ((((wn * 16 + fj * 2 + (g >> 1)) ^ ((r & 3) << 2))) << 4);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u32x2 w = *(const u32x2 __attribute__((address_space(3)))*)(a + q * 16 * NN_XROWB);
+      f32x4 av;
+      asm volatile("" : "=v"(av) : "0"(acc[FI0 + q][fj]));
+      av[0] += ratio * __uint_as_float(w.x << 16);
+      av[1] += ratio * __uint_as_float(w.x & 0xffff0000u);
+      av[2] += ratio * __uint_as_float(w.y << 16);
+      av[3] += ratio * __uint_as_float(w.y & 0xffff0000u);
+      asm volatile("" : "=a"(acc[FI0 + q][fj]) : "0"(av));
+    }
+  }
+}
+
+__global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g) {
+  constexpr int WM = 128, WN = 128;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int G = gridDim.x, T = g.tiles_total;
+  const int x = blockIdx.x & 7, l = blockIdx.x >> 3;
+  const int gx = (G >> 3) + (x < (G & 7) ? 1 : 0);
+  const int nfull = T / (8 * N4_STRIPE) * N4_STRIPE;
+  const int rq = (T - 8 * nfull) >> 3, rr = (T - 8 * nfull) & 7;
+  const int tcount = nfull + rq + (x < rr ? 1 : 0);
+  auto tile_of = [&](int i) {
+    return i < nfull ? ((i / N4_STRIPE) * 8 + x) * N4_STRIPE + i % N4_STRIPE
+                     : 8 * nfull + x * rq + min(x, rr) + (i - nfull);
+  };
+  int li = l;
+  if (li >= tcount) return;
+
+  const int lda_b = (int)(g.lda * 2), ldx_b = (int)(g.ldb * 2);
+  const int ra_in = wave * 8 + (lane >> 3);
+  const int voa = ra_in * lda_b + (((lane & 7) ^ kswz(ra_in)) << 4);
+  const int rx_in = wave * 2 + (lane >> 5);
+  const int vox = rx_in * ldx_b + (((lane & 31) ^ ((rx_in & 3) << 2)) << 4);
+  const int sta = 32 * lda_b, stx = 8 * ldx_b;
+  const bf16_t* const A0 = (const bf16_t*)g.a;
+  const bf16_t* const X0 = (const bf16_t*)g.b;
+
+  // fragment addresses. B (srcB): lane l -> panel row 128 wm + 16 fi + l%16, logical chunk
+  // 4 ks + l/16 (8 consecutive k). X (srcA): tr reads, lane l -> panel row 32 ks + 8 (l/16) +
+  // (l%16)/4 (+4 for the high half), columns 128 wn + 16 fj + 4 (l%4) .. +3.
+  const int fr = lane & 15, fg = lane >> 4;
+  int foff[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) foff[ks] = fr * V2_ROWB + (((ks * 4 + fg) ^ kswz(fr)) << 4);
+  const int abase = wm * WM * V2_ROWB;
+  uint32_t xoff[8];
+#pragma unroll
+  for (int f = 0; f < 8; ++f) {
+    const int chunk = (wn * 16 + f * 2 + ((fr & 3) >> 1)) ^ (((fr >> 2) & 3) << 2);
+    xoff[f] = NN_ATILEB + (8 * fg + (fr >> 2)) * NN_XROWB + chunk * 16 + (fr & 1) * 8;
+  }
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  auto baddr = [&](int st, int ks) -> uint32_t { return lds0 + st * NN_STAGEB + abase + foff[ks]; };
+  uint32_t xa[8];
+  auto set_xa = [&](int st) {
+#pragma unroll
+    for (int f = 0; f < 8; ++f) xa[f] = lds0 + st * NN_STAGEB + xoff[f];
+  };
+  const uint32_t m0w = lds0 + wave * 1024;
+  const int KT = (int)(g.K / V2_BK);
+
+  int bidx;
+  int64_t arow0, bcol0;
+  nn4_tile(g, tile_of(li), bidx, arow0, bcol0);
+  u32x4 rsa = n4_rsrc(A0 + (int64_t)bidx * g.sa + arow0 * g.lda, false);
+  u32x4 rsx = n4_rsrc(X0 + (int64_t)bidx * g.sb + bcol0, false);
+
+  bf16x8_mfma b0[8], b1[8], x0[8], x1[8];
+  i16x4 xl[8], xh[8];
+  // K-tiles 0 and 1 of the first tile
+  nn4_dma(voa, vox, rsa, rsx, 0, 0, sta, stx, m0w, m0w + NN_ATILEB);
+  wait_vmcnt0();
+  lds_barrier();
+  nn4_dma(voa, vox, rsa, rsx, V2_ROWB, V2_BK * ldx_b, sta, stx, m0w + NN_STAGEB,
+          m0w + NN_STAGEB + NN_ATILEB);
+  set_xa(0);
+  n16_frag_load<0>(b0, xl, xh, baddr(0, 0), xa);
+  n16_join(x0, xl, xh);
+
+  f32x4 acc[8][8];
+  for (;;) {
+    const int lnext = li + gx;
+    const bool has_next = lnext < tcount;
+    int nbidx = 0;
+    int64_t narow0 = 0, nbcol0 = 0;
+    if (has_next) nn4_tile(g, tile_of(lnext), nbidx, narow0, nbcol0);
+    const u32x4 rsa_n = n4_rsrc(A0 + (int64_t)nbidx * g.sa + narow0 * g.lda, !has_next);
+    const u32x4 rsx_n = n4_rsrc(X0 + (int64_t)nbidx * g.sb + nbcol0, !has_next);
+
+    float alpha = g.alpha, beta = g.beta;
+    if (g.scale_mode == 1) {
+      const float sc = g.scale[bidx];
+      alpha *= sc;
+      beta *= sc;
+    }
+    const float ratio = beta != 0.0f ? beta / alpha : 0.0f;
+    // the wave's 128 output rows are the k rows of K-tiles kd0 and kd0 + 1; rows at or beyond
+    // K are padding, whose X rows are zero
+    const int kd = (int)((arow0 + wm * WM) / V2_BK);
+    const int kd0 = ratio != 0.0f && kd < KT ? kd : -1;
+
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // one K-tile: substep 0 (reading substep 1's fragments), [the beta term], wait for K-tile
+    // kt + 1's DMA, barrier, substep 1 (reading K-tile kt + 1's first fragments) with the DMA
+    // of K-tile kt + 2 (this tile's or the next's) into this K-tile's stage. The two K-tiles
+    // that carry the beta term (ratio * X added into the accumulators of the rows their k
+    // range covers) are peeled off the loops, which keeps the accumulators in one register
+    // assignment inside them.
+    auto kstep = [&](int kt, auto beta_fi0) {
+      const int cs = kt & 1;
+      set_xa(cs);
+      n16_substep<16 * NN_XROWB * 2>(acc, b0, x0, b1, xl, xh, baddr(cs, 1), xa);
+      n16_join(x1, xl, xh);
+      if constexpr (decltype(beta_fi0)::value >= 0) {
+        mfma_to_valu_wait();
+        n16_beta<decltype(beta_fi0)::value>(acc, lds0 + cs * NN_STAGEB + NN_ATILEB, wn, lane, ratio);
+        valu_to_mfma_wait();
+      }
+      wait_vmcnt0();
+      lds_barrier();
+      const bool c2 = kt + 2 < KT;
+      const int k2 = c2 ? kt + 2 : kt + 2 - KT;
+      set_xa(cs ^ 1);
+      const uint32_t m0a = m0w + cs * NN_STAGEB;
+      n16_substep_dma<0>(acc, b1, x1, b0, xl, xh, baddr(cs ^ 1, 0), xa, voa, vox, c2 ? rsa : rsa_n,
+                         c2 ? rsx : rsx_n, k2 * V2_ROWB, k2 * V2_BK * ldx_b, sta, stx, m0a,
+                         m0a + NN_ATILEB);
+      n16_join(x0, xl, xh);
+    };
+    using no_beta = std::integral_constant<int, -1>;
+    int kt = 0;
+    if (kd0 >= 0) {
+      for (; kt < kd0; ++kt) kstep(kt, no_beta{});
+      kstep(kt++, std::integral_constant<int, 0>{});
+      kstep(kt++, std::integral_constant<int, 4>{});
+    }
+    for (; kt < KT; ++kt) kstep(kt, no_beta{});
+    mfma_to_valu_wait();
+
+    // epilogue: accumulator (fi, fj) element q is X'(i, j + q) with i = 128 wm + 16 fi +
+    // lane%16, j = 128 wn + 16 fj + 4 (lane/16). Two row blocks (32 rows) at a time go through
+    // the wave's LDS staging rows (16-byte chunk k of row r at chunk k ^ (r & 15)), then out as
+    // 4 whole rows of 256 bytes per non-temporal store.
+    bf16_t* outw = (bf16_t*)g.out + (int64_t)bidx * g.so + (arow0 + wm * WM) * g.ldo + bcol0 + wn * WN;
+    const __amdgpu_buffer_rsrc_t rso =
+        __builtin_amdgcn_make_buffer_rsrc((void*)outw, 0, 0x7fffffff, 0x00020000);
+    const int ldo_b = (int)(g.ldo * 2);
+    const uint32_t ep = lds0 + 2 * NN_STAGEB + wave * N4_EPB;
+    const uint32_t epr = ep + (lane >> 4) * 256;
+    const int vor = (lane >> 4) * ldo_b + (lane & 15) * 16;
+    const bool full = arow0 + 256 <= g.Mv && bcol0 + 256 <= g.Nv;
+    const int rem_i = (int)g.Mv - (int)(arow0 + wm * WM + fr);
+    const int rem_j = (int)g.Nv - (int)(bcol0 + wn * WN + 4 * fg);
+    auto emit = [&](auto masked) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int fi = 2 * p + h;
+#pragma unroll
+          for (int fj = 0; fj < 8; ++fj) {
+            f32x4 av;
+            asm volatile("" : "=v"(av) : "0"(acc[fi][fj]));
+            f2x v01 = {alpha * av[0], alpha * av[1]};
+            f2x v23 = {alpha * av[2], alpha * av[3]};
+            if (decltype(masked)::value) {
+              const int jq = fj * 16;
+              const bool vi = fi * 16 < rem_i;
+              v01.x = vi && jq + 0 < rem_j ? v01.x : 0.0f;
+              v01.y = vi && jq + 1 < rem_j ? v01.y : 0.0f;
+              v23.x = vi && jq + 2 < rem_j ? v23.x : 0.0f;
+              v23.y = vi && jq + 3 < rem_j ? v23.y : 0.0f;
+            }
+            const u32x2 w = {__builtin_bit_cast(uint32_t, __builtin_convertvector(v01, bf2x)),
+                             __builtin_bit_cast(uint32_t, __builtin_convertvector(v23, bf2x))};
+            uint32_t ea = ep + (h * 16 + fr) * 256 + (fg & 1) * 8, fx = fr;
+            asm volatile("" : "+v"(ea), "+v"(fx));
+            *(u32x2 __attribute__((address_space(3)))*)(ea + (((2 * fj + (fg >> 1)) ^ fx) << 4)) = w;
+          }
+        }
+        uint32_t ra = epr, lc = lane & 15, lr = lane >> 4;
+        int vs = vor;
+        asm volatile("" : "+v"(ra), "+v"(vs), "+v"(lc), "+v"(lr));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t c = lc ^ ((4 * i + lr) & 15);
+          const u32x4 q4 = *(const u32x4 __attribute__((address_space(3)))*)(ra + i * 1024 + (c << 4));
+          __builtin_amdgcn_raw_buffer_store_b128(q4, rso, vs + i * 4 * ldo_b, p * 32 * ldo_b, 2);
+        }
+      }
+    };
+    if (full)
+      emit(std::false_type{});
+    else
+      emit(std::true_type{});
+    if (!has_next) break;
+    li = lnext;
+    bidx = nbidx;
+    arow0 = narow0;
+    bcol0 = nbcol0;
+    rsa = rsa_n;
+    rsx = rsx_n;
+  }
+}
+
 // Wave grid of the register-staged bf16 kernel (gemm_bf16_kernel), which serves the
 // masked gram_ path and SYRKs whose beta term has no alpha to fold into: 4 x 2
 // wavefronts, each 64 x 128, two waves per SIMD.
@@ -1451,6 +1809,9 @@ int reserve_bf16_lds() {
         hipSuccess)
       status = -1;
     if (hipFuncSetAttribute((const void*)gemm_bf16_nn4_kernel,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, N4_SMEM) != hipSuccess)
+      status = -1;
+    if (hipFuncSetAttribute((const void*)gemm_bf16_nn16_kernel,
                             hipFuncAttributeMaxDynamicSharedMemorySize, N4_SMEM) != hipSuccess)
       status = -1;
   });
@@ -1568,7 +1929,10 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
       }
       // persistent: one workgroup per CU walks the tile list
       const int wgs = (int)std::min<int64_t>(blocks, device_cus());
-      hipLaunchKernelGGL(gemm_bf16_nn4_kernel, dim3((unsigned)wgs), dim3(256), N4_SMEM, stream, g);
+      if (K >= 2048)
+        hipLaunchKernelGGL(gemm_bf16_nn16_kernel, dim3((unsigned)wgs), dim3(256), N4_SMEM, stream, g);
+      else
+        hipLaunchKernelGGL(gemm_bf16_nn4_kernel, dim3((unsigned)wgs), dim3(256), N4_SMEM, stream, g);
     } else if (!masked && (alpha != 0.0f || beta == 0.0f)) {
       // the last 128 rows padding only: the last tile column's real unit in packed tiles,
       // in the same launch as the full tiles
