@@ -326,19 +326,27 @@ def blas_ceiling(config: str, dev, reps: int = 3) -> dict:
             "orth_tflops_symmetric_minimal": round(total_flops / (total_ms * 1e-3) / 1e12, 1)}
 
 
-def _measured_traffic(kernel: str, config: str, lp):
-    """HBM bytes per dispatch of `kernel` from the committed rocprofv3 PMC summary
-    (FETCH_SIZE + WRITE_SIZE, each scaled by a 1 GiB copy), for the workload it was
-    measured on; None elsewhere."""
+def _measured_traffic(kernels, config: str, lp):
+    """HBM bytes per dispatch of `kernels` (one name, or several that serve one product:
+    their dispatch-weighted mean over those the profile saw) from the committed rocprofv3
+    PMC summary (FETCH_SIZE + WRITE_SIZE, each scaled by a 1 GiB copy), for the workload
+    it was measured on; None elsewhere."""
     files = {"llama": "muon_step_llama3_8b_traffic.json", "moe_flat": "muon_step_moe_flat_traffic.json"}
     if config not in files or lp:
         return None, None
+    if isinstance(kernels, str):
+        kernels = [kernels]
     path = os.path.join(ROOT, "profiles", files[config])
     try:
         with open(path) as f:
             data = json.load(f)
-        return data["kernels"][kernel]["traffic_bytes"], os.path.relpath(path, ROOT)
-    except (OSError, KeyError, ValueError):
+        seen = [data["kernels"][k] for k in kernels if k in data["kernels"]]
+        n = sum(int(k["dispatches"]) for k in seen)
+        if n == 0:
+            return None, None
+        traffic = sum(k["traffic_bytes"] * int(k["dispatches"]) for k in seen) / n
+        return int(round(traffic)), os.path.relpath(path, ROOT)
+    except (OSError, KeyError, ValueError, TypeError):
         return None, None
 
 
@@ -524,12 +532,14 @@ def main() -> None:
         achieved = (gwork / max(gn, 1)) / (avg_ms * 1e-3) / 1e12
         # the optimizer iterates in bf16 whatever the params' dtype (zeropower casts to
         # bf16, orthogonalize.py:101-102), so fp32 params (plumbing) run this kernel too
-        kname = "gemm_bf16_nn4_kernel"
+        # two kernels serve this product: gemm_bf16_nn16_kernel for K >= 2048 and
+        # gemm_bf16_nn4_kernel below; the launch brackets time whichever ran
+        knames = ["gemm_bf16_nn16_kernel", "gemm_bf16_nn4_kernel"]
         peak = PEAK_BF16_TFLOPS
-        traffic, traffic_src = _measured_traffic(kname, args.config, args.lp)
+        traffic, traffic_src = _measured_traffic(knames, args.config, args.lp)
         roofline = {
             "bound": "mfma",
-            "kernel": f"{kname} (X' = a X + B X)",
+            "kernel": "gemm_bf16_nn16_kernel (K >= 2048) / gemm_bf16_nn4_kernel (X' = a X + B X)",
             "achieved": round(achieved, 1),
             "peak": peak,
             "unit": "TFLOP/s",

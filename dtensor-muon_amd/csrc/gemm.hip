@@ -1775,6 +1775,320 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g) {
   }
 }
 
+// ----------------------------------------------------------------------------------
+// The SYRK kernel (X X^T, A A) on 16 x 16 x 32 MFMAs.
+//
+// Tiles, tile order, waves (8, two per SIMD, 64 x 128 each), LDS stages and epilogue
+// staging as gemm_bf16_v2_kernel; the wave's block is 4 x 8 accumulators of 16 x 16 and a
+// K-tile is two 32-k substeps of 32 MFMAs, each substep reading the next one's 12 fragments
+// (4 a, 8 b) between its MFMAs. The DMA of K-tile k + 2 is spread over the second substep
+// of K-tile k (two loads per block of 8 MFMAs), right after the barrier that ends the reads
+// of its stage. On the Llama shapes X X^T and A A run 6-7% faster than on 32 x 32 x 16
+// MFMAs; launches with packed tiles measured 5% slower and stay on gemm_bf16_v2_kernel.
+//
+// Fragments (lane l, r = l % 16, g = l / 16): srcA is a-panel row 16 fi + r, srcB is
+// b-panel row 16 fj + r, both 8 consecutive k (logical chunk 4 ks + g of the row); the
+// accumulator register q of block (fi, fj) is C(16 fi + 4 g + q, 16 fj + r).
+#define S16(C, B) "v_mfma_f32_16x16x32_bf16 %[" #C "], %[a], %[" #B "], %[" #C "]\n\t"
+#define S16_OUT                                                                             \
+  [c0] "+v"(acc[0]), [c1] "+v"(acc[1]), [c2] "+v"(acc[2]), [c3] "+v"(acc[3]),                \
+  [c4] "+v"(acc[4]), [c5] "+v"(acc[5]), [c6] "+v"(acc[6]), [c7] "+v"(acc[7]),                \
+  [na] "=&v"(na), [nb0] "=&v"(nb0), [nb1] "=&v"(nb1)
+#define S16_IN                                                                              \
+  [a] "v"(ca), [b0] "v"(cb[0]), [b1] "v"(cb[1]), [b2] "v"(cb[2]), [b3] "v"(cb[3]),           \
+  [b4] "v"(cb[4]), [b5] "v"(cb[5]), [b6] "v"(cb[6]), [b7] "v"(cb[7]), [aa] "v"(aa),          \
+  [ba] "v"(ba), [oa] "i"(FI * 16 * V2_ROWB), [ob0] "i"(2 * FI * 16 * V2_ROWB),                \
+  [ob1] "i"((2 * FI + 1) * 16 * V2_ROWB)
+#define S16_RA "ds_read_b128 %[na], %[aa] offset:%[oa]\n\t"
+#define S16_RB0 "ds_read_b128 %[nb0], %[ba] offset:%[ob0]\n\t"
+#define S16_RB1 "ds_read_b128 %[nb1], %[ba] offset:%[ob1]\n\t"
+#define S16_M0(N) "s_mov_b32 m0, %[mz" #N "]\n\t"
+#define S16_DL(N) "buffer_load_dwordx4 %[vo" #N "], %[rs" #N "], %[so" #N "] offen lds\n\t"
+#define S16_LD(N)                                                                           \
+  [vo##N] "v"(vo##N), [rs##N] "s"(rs##N), [so##N] "s"(so##N), [mz##N] "s"(mz##N)
+// One block of a 32-k substep: the 8 MFMAs of a fragment FI (accumulators acc[0..7]) with
+// the reads of the next substep's a fragment FI (aa + 2 KB FI) and b fragments 2 FI and
+// 2 FI + 1 (ba + 2 KB (2 FI), + 2 KB (2 FI + 1)).
+template <int FI>
+MUON_DEVICE void s16_block(f32x4 (&acc)[8], const bf16x8_mfma& ca, const bf16x8_mfma (&cb)[8],
+                           bf16x8_mfma& na, bf16x8_mfma& nb0, bf16x8_mfma& nb1, uint32_t aa,
+                           uint32_t ba) {
+  asm volatile(S16_RA S16(c0, b0) S16(c1, b1) S16(c2, b2)
+               S16_RB0 S16(c3, b3) S16(c4, b4) S16(c5, b5)
+               S16_RB1 S16(c6, b6) S16(c7, b7)
+               : S16_OUT
+               : S16_IN);
+}
+// The same with two loads of a K-tile's DMA, each after an MFMA that follows its M0 write.
+template <int FI>
+MUON_DEVICE void s16_block_dma(f32x4 (&acc)[8], const bf16x8_mfma& ca, const bf16x8_mfma (&cb)[8],
+                               bf16x8_mfma& na, bf16x8_mfma& nb0, bf16x8_mfma& nb1, uint32_t aa,
+                               uint32_t ba, int vo0, u32x4 rs0, int so0, uint32_t mz0, int vo1,
+                               u32x4 rs1, int so1, uint32_t mz1) {
+  asm volatile(S16_M0(0) S16_RA S16(c0, b0) S16_DL(0) S16(c1, b1) S16_M0(1) S16(c2, b2)
+               S16_RB0 S16(c3, b3) S16_DL(1) S16(c4, b4) S16(c5, b5)
+               S16_RB1 S16(c6, b6) S16(c7, b7)
+               : S16_OUT
+               : S16_IN, S16_LD(0), S16_LD(1)
+               : "m0", "memory");
+}
+#undef S16
+#undef S16_OUT
+#undef S16_IN
+#undef S16_RA
+#undef S16_RB0
+#undef S16_RB1
+#undef S16_M0
+#undef S16_DL
+#undef S16_LD
+
+typedef bf16x8_mfma s16_frags[12];  // a fragments 0-3, b fragments 0-7
+
+// One substep without DMA, then the wait for its 12 reads.
+MUON_DEVICE void s16_substep(f32x4 (&acc)[4][8], const s16_frags& c, s16_frags& n, uint32_t aa,
+                             uint32_t ba) {
+  const bf16x8_mfma(&cb)[8] = *(const bf16x8_mfma(*)[8]) & c[4];
+  s16_block<0>(acc[0], c[0], cb, n[0], n[4], n[5], aa, ba);
+  s16_block<1>(acc[1], c[1], cb, n[1], n[6], n[7], aa, ba);
+  s16_block<2>(acc[2], c[2], cb, n[2], n[8], n[9], aa, ba);
+  s16_block<3>(acc[3], c[3], cb, n[3], n[10], n[11], aa, ba);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// One substep with the DMA of one K-tile into one stage: this wave's slabs q = 0..3 of the a
+// panel (scalar offsets soa + q sta, M0 ma + 8 KB q) and of the b panel (sob + q stb, mb +
+// 8 KB q), two after each block. A slab is the wave's 1 KB of 8 panel rows.
+MUON_DEVICE void s16_substep_dma(f32x4 (&acc)[4][8], const s16_frags& c, s16_frags& n, uint32_t aa,
+                                 uint32_t ba, int voa, int vob, u32x4 rsa, u32x4 rsb, int soa,
+                                 int sta, int sob, int stb, uint32_t ma, uint32_t mb) {
+  const bf16x8_mfma(&cb)[8] = *(const bf16x8_mfma(*)[8]) & c[4];
+  s16_block_dma<0>(acc[0], c[0], cb, n[0], n[4], n[5], aa, ba, voa, rsa, soa, ma, voa, rsa,
+                      soa + sta, ma + 0x2000);
+  s16_block_dma<1>(acc[1], c[1], cb, n[1], n[6], n[7], aa, ba, voa, rsa, soa + 2 * sta,
+                      ma + 0x4000, voa, rsa, soa + 3 * sta, ma + 0x6000);
+  s16_block_dma<2>(acc[2], c[2], cb, n[2], n[8], n[9], aa, ba, vob, rsb, sob, mb, vob, rsb,
+                      sob + stb, mb + 0x2000);
+  s16_block_dma<3>(acc[3], c[3], cb, n[3], n[10], n[11], aa, ba, vob, rsb, sob + 2 * stb,
+                      mb + 0x4000, vob, rsb, sob + 3 * stb, mb + 0x6000);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// All 12 fragment reads of one substep without MFMAs (pipeline start).
+MUON_DEVICE void s16_frag_load(s16_frags& n, uint32_t aa, uint32_t ba) {
+#pragma unroll
+  for (int f = 0; f < 4; ++f)
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(n[f]) : "v"(aa), "i"(f * 16 * V2_ROWB));
+#pragma unroll
+  for (int f = 0; f < 8; ++f)
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(n[4 + f]) : "v"(ba), "i"(f * 16 * V2_ROWB));
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// A finished 64 x 128 wave tile as bf16 pairs (hardware RNE pair conversion): hv[fi][fj][h]
+// holds rows 16 fi + 4 g + 2 h and + 1 of the lane's column 16 fj + r. Unless `full`,
+// elements outside the valid extent are cleared to +0: rem_i counts the valid rows from the
+// lane's first row (4 g included), rem_j the valid columns from its column.
+MUON_DEVICE void s16_pack(const f32x4 (&acc)[4][8], float alpha, bool full, int rem_i, int rem_j,
+                          uint32_t (&hv)[4][8][2]) {
+#pragma unroll
+  for (int fi = 0; fi < 4; ++fi)
+#pragma unroll
+    for (int fj = 0; fj < 8; ++fj)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const f2x v = {alpha * acc[fi][fj][2 * h], alpha * acc[fi][fj][2 * h + 1]};
+        hv[fi][fj][h] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2x));
+      }
+  if (full) return;
+#pragma unroll
+  for (int fi = 0; fi < 4; ++fi)
+#pragma unroll
+    for (int fj = 0; fj < 8; ++fj)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int il0 = fi * 16 + 2 * h;
+        const bool vj = fj * 16 < rem_j;
+        const uint32_t keep = (vj && il0 < rem_i ? 0x0000ffffu : 0u) |
+                              (vj && il0 + 1 < rem_i ? 0xffff0000u : 0u);
+        hv[fi][fj][h] &= keep;
+      }
+}
+
+__global__ __launch_bounds__(512, 1) void gemm_bf16_s16_kernel(GemmArgs g) {
+  constexpr int NW = 8, WM = 64, WN = 128;
+  extern __shared__ __align__(16) uint8_t smem[];
+
+  int bidx, tm, tn;
+  map_tile(g, MODE_SYRK, bidx, tm, tn);
+  const int64_t arow0 = (int64_t)tm * 256, brow0 = (int64_t)tn * 256;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const bf16_t* A = (const bf16_t*)g.a + (int64_t)bidx * g.sa;
+  const bf16_t* B = (const bf16_t*)g.b + (int64_t)bidx * g.sb;
+  const int lda_b = (int)(g.lda * 2), ldb_b = (int)(g.ldb * 2);
+  const u32x4 rsa = n4_rsrc(A + arow0 * g.lda, false);
+  const u32x4 rsb = n4_rsrc(B + brow0 * g.ldb, false);
+  const u32x4 rs_none = n4_rsrc(A, true);
+  const __amdgpu_buffer_rsrc_t rsa_p =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(A + arow0 * g.lda), 0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb_p =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(B + brow0 * g.ldb), 0, 0x7fffffff, 0x00020000);
+  // load slab q*NW + wave = panel rows (q*NW + wave)*8 .. +7; lane -> row lane/8, chunk
+  // position lane%8, which holds logical chunk (lane%8) ^ kswz(row)
+  const int r_in = wave * 8 + (lane >> 3);
+  const int lch = (lane & 7) ^ kswz(r_in);
+  const int voa = r_in * lda_b + lch * 16;
+  const int vob = r_in * ldb_b + lch * 16;
+  const int sta = NW * 8 * lda_b, stb = NW * 8 * ldb_b;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  const uint32_t m0w = lds0 + wave * 1024;
+
+  // fragment read offsets: lane -> row r of the fragment, logical chunk 4 ks + g
+  const int fr = lane & 15, fg = lane >> 4;
+  int foff[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) foff[ks] = fr * V2_ROWB + (((ks * 4 + fg) ^ kswz(fr)) << 4);
+  const int abase = wm * WM * V2_ROWB, bbase = V2_TILEB + wn * WN * V2_ROWB;
+
+  float alpha = g.alpha, beta = g.beta;
+  if (g.scale_mode != 0) {
+    const float s = g.scale[bidx];
+    if (g.scale_mode == 1) {
+      alpha *= s;
+      beta *= s;
+    } else {
+      alpha *= s * s;
+    }
+  }
+  const float ratio = beta != 0.0f ? beta / alpha : 0.0f;
+  // K-tile whose k range equals this wave's output rows (WM == BK)
+  const int kdiag = ratio != 0.0f ? (int)((arow0 + wm * WM) / V2_BK) : -1;
+
+  f32x4 acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int KT = (int)(g.K / V2_BK);
+  auto aaddr = [&](int st, int ks) -> uint32_t { return lds0 + st * V2_STAGEB + abase + foff[ks]; };
+  auto baddr = [&](int st, int ks) -> uint32_t { return lds0 + st * V2_STAGEB + bbase + foff[ks]; };
+  // the DMA of K-tile kt into stage st (pipeline start; later K-tiles ride in the substeps)
+  auto issue = [&](int kt, int st) {
+    uint8_t* sa = smem + st * V2_STAGEB;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa_p, (lds_ptr_t)(sa + (q * NW + wave) * 1024), 16,
+                                               voa, q * sta + kt * V2_ROWB, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb_p,
+                                               (lds_ptr_t)(sa + V2_TILEB + (q * NW + wave) * 1024),
+                                               16, vob, q * stb + kt * V2_ROWB, 0, 0);
+    }
+  };
+  s16_frags f0, f1;
+  issue(0, 0);
+  wait_vmcnt0();
+  lds_barrier();
+  if (KT > 1) issue(1, 1);
+  s16_frag_load(f0, aaddr(0, 0), baddr(0, 0));
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cs = kt & 1;
+    s16_substep(acc, f0, f1, aaddr(cs, 1), baddr(cs, 1));
+    if (kt == kdiag) {
+      // cin(i, j) = b(j, i): row j of the b panel, k offset i - kt*BK (the 4 rows of one
+      // accumulator are 8 contiguous bytes of that row)
+      mfma_to_valu_wait();
+      const uint32_t sb = lds0 + cs * V2_STAGEB + bbase + fr * V2_ROWB + (fg & 1) * 8;
+#pragma unroll
+      for (int fi = 0; fi < 4; ++fi)
+#pragma unroll
+        for (int fj = 0; fj < 8; ++fj) {
+          const u32x2 w = *(const u32x2 __attribute__((address_space(3)))*)(
+              sb + fj * 16 * V2_ROWB + (((2 * fi + (fg >> 1)) ^ kswz(fr)) << 4));
+          acc[fi][fj][0] += ratio * __uint_as_float(w.x << 16);
+          acc[fi][fj][1] += ratio * __uint_as_float(w.x & 0xffff0000u);
+          acc[fi][fj][2] += ratio * __uint_as_float(w.y << 16);
+          acc[fi][fj][3] += ratio * __uint_as_float(w.y & 0xffff0000u);
+        }
+      valu_to_mfma_wait();
+    }
+    wait_vmcnt0();
+    lds_barrier();
+    // K-tile kt + 2 into this K-tile's stage; past the last K-tile the null descriptor
+    // reads no memory
+    const bool more = kt + 2 < KT;
+    const int kb = (kt + 2) * V2_ROWB;
+    const uint32_t ma = m0w + cs * V2_STAGEB;
+    s16_substep_dma(acc, f1, f0, aaddr(cs ^ 1, 0), baddr(cs ^ 1, 0), voa, vob, more ? rsa : rs_none,
+                    more ? rsb : rs_none, kb, sta, kb, stb, ma, ma + V2_TILEB);
+  }
+  mfma_to_valu_wait();
+  wait_vmcnt0();
+
+  // ---- epilogue: stage through LDS, store 16-byte row chunks ----
+  if (g.out == nullptr) return;
+  bf16_t* T = (bf16_t*)smem;
+  const bool diag = tm == tn;
+  const int row0w = wm * WM, col0w = wn * WN;  // wave origin within the tile
+  uint32_t hv[4][8][2];
+  s16_pack(acc, alpha, arow0 + 256 <= g.Mv && brow0 + 256 <= g.Nv,
+           clamp_rem(g.Mv - (arow0 + row0w + fg * 4)), clamp_rem(g.Nv - (brow0 + col0w + fr)), hv);
+  bf16_t* out = (bf16_t*)g.out + (int64_t)bidx * g.so;
+  if (!diag) {
+    // mirror half of the symmetric output: T[j][i], 4 consecutive i per lane -> one 8-byte
+    // write
+    lds_barrier();
+#pragma unroll
+    for (int fi = 0; fi < 4; ++fi)
+#pragma unroll
+      for (int fj = 0; fj < 8; ++fj) {
+        const int jl = col0w + fj * 16 + fr;
+        const int il = row0w + fi * 16 + fg * 4;
+        *(uint2*)(T + jl * V2_EP_PITCH + il) = make_uint2(hv[fi][fj][0], hv[fi][fj][1]);
+      }
+    lds_barrier();
+#pragma unroll 4
+    for (int it = 0; it < 16; ++it) {
+      const int id = it * 512 + tid;
+      const int jl = id >> 5, c = (id & 31) * 8;
+      const uint4 w = *(const uint4*)(T + jl * V2_EP_PITCH + c);
+      *(uint4*)(out + (brow0 + jl) * g.ldo + arow0 + c) = w;
+    }
+  }
+  // row-major stage: T[i][j]
+  lds_barrier();
+#pragma unroll
+  for (int fi = 0; fi < 4; ++fi)
+#pragma unroll
+    for (int fj = 0; fj < 8; ++fj)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int il = row0w + fi * 16 + fg * 4 + q;
+        const int jl = col0w + fj * 16 + fr;
+        T[il * V2_EP_PITCH + jl] = (bf16_t)(hv[fi][fj][q >> 1] >> (16 * (q & 1)));
+      }
+  lds_barrier();
+#pragma unroll 4
+  for (int it = 0; it < 16; ++it) {
+    const int id = it * 512 + tid;
+    const int il = id >> 5, c = (id & 31) * 8;
+    uint4 w;
+    if (!diag || c >= il) {
+      w = *(const uint4*)(T + il * V2_EP_PITCH + c);
+    } else {
+      // diagonal tile, chunk reaching below the diagonal: those columns come from the
+      // computed (upper) element of the mirror position
+      uint16_t e[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        e[q] = (c + q < il) ? T[(c + q) * V2_EP_PITCH + il] : T[il * V2_EP_PITCH + c + q];
+      __builtin_memcpy(&w, e, 16);
+    }
+    *(uint4*)(out + (arow0 + il) * g.ldo + brow0 + c) = w;
+  }
+}
+
 // Wave grid of the register-staged bf16 kernel (gemm_bf16_kernel), which serves the
 // masked gram_ path and SYRKs whose beta term has no alpha to fold into: 4 x 2
 // wavefronts, each 64 x 128, two waves per SIMD.
@@ -1800,13 +2114,12 @@ int reserve_bf16_lds() {
       if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, BF_SMEM) !=
           hipSuccess)
         status = -1;
-    if (hipFuncSetAttribute((const void*)gemm_bf16_v2_kernel<MODE_SYRK, false>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, v2_smem(false)) !=
-        hipSuccess)
-      status = -1;
     if (hipFuncSetAttribute((const void*)gemm_bf16_v2_kernel<MODE_SYRK, true>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, v2_smem(true)) !=
         hipSuccess)
+      status = -1;
+    if (hipFuncSetAttribute((const void*)gemm_bf16_s16_kernel,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, V2_SMEM) != hipSuccess)
       status = -1;
     if (hipFuncSetAttribute((const void*)gemm_bf16_nn4_kernel,
                             hipFuncAttributeMaxDynamicSharedMemorySize, N4_SMEM) != hipSuccess)
@@ -1945,8 +2258,8 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
                            dim3((unsigned)(gp.tiles_per_batch * batch)), dim3(512),
                            v2_smem(true), stream, gp);
       } else {
-        hipLaunchKernelGGL((gemm_bf16_v2_kernel<MODE_SYRK, false>), grid, dim3(512),
-                           v2_smem(false), stream, g);
+        // full tiles only: the 16 x 16 x 32 MFMA kernel
+        hipLaunchKernelGGL(gemm_bf16_s16_kernel, grid, dim3(512), V2_SMEM, stream, g);
       }
     } else {
       if (masked) LAUNCH_BF(MODE_SYRK, true); else LAUNCH_BF(MODE_SYRK, false);
