@@ -326,6 +326,42 @@ def blas_ceiling(config: str, dev, reps: int = 3) -> dict:
             "orth_tflops_symmetric_minimal": round(total_flops / (total_ms * 1e-3) / 1e12, 1)}
 
 
+def hbm_ceiling(dev, reps: int = 5) -> dict:
+    """Library reference for the update passes: torch's own streaming kernels on 2 GiB bf16
+    buffers (far above the 256 MB Infinity Cache) at several read:write mixes, the median of
+    `reps` timed calls each, as bytes moved per second."""
+    import torch
+
+    n = 1 << 30
+    gen = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(n, device=dev, dtype=torch.bfloat16, generator=gen)
+    y = torch.randn(n, device=dev, dtype=torch.bfloat16, generator=gen)
+    z = torch.empty_like(x)
+    cases = {
+        "read (x.sum())": (lambda: x.sum(), 2 * n),
+        "write (z.fill_)": (lambda: z.fill_(1.0), 2 * n),
+        "copy 1R:1W (z.copy_(x))": (lambda: z.copy_(x), 4 * n),
+        "add 2R:1W (torch.add(x, y, out=z))": (lambda: torch.add(x, y, out=z), 6 * n),
+    }
+    out = {}
+    for name, (fn, nbytes) in cases.items():
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        ms = sorted(ts)[len(ts) // 2]
+        out[name] = {"ms": round(ms, 4), "bytes": nbytes,
+                     "tbs": round(nbytes / (ms * 1e-3) / 1e12, 3)}
+    return {"hbm_ceiling": "torch streaming kernels, bf16, 2 GiB buffers", "results": out}
+
+
 def _measured_traffic(kernels, config: str, lp):
     """HBM bytes per dispatch of `kernels` (one name, or several that serve one product:
     their dispatch-weighted mean over those the profile saw) from the committed rocprofv3
@@ -364,6 +400,9 @@ def main() -> None:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device-to-device copy 5 times (PMC calibration)")
+    ap.add_argument("--hbm-ceiling", action="store_true",
+                    help="only time torch's streaming kernels (read, write, copy, add) on 2 GiB "
+                         "buffers as a reference for the update passes")
     ap.add_argument("--blas-ceiling", action="store_true",
                     help="only time the iteration's three products per bucket with torch.bmm "
                          "(hipBLASLt) as a library reference")
@@ -399,6 +438,9 @@ def main() -> None:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": src.numel() * 2, "dispatches": 5}))
+        return
+    if args.hbm_ceiling:
+        print(json.dumps(hbm_ceiling(dev)), flush=True)
         return
     if args.blas_ceiling:
         print(json.dumps(blas_ceiling(args.config, dev)), flush=True)

@@ -1432,6 +1432,13 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn4_kernel(GemmArgs g) {
 // of column 16 fj + r; srcB is B, 8 consecutive k (one b128) of row 16 fi + r; the
 // accumulator register q of block (fi, fj) is X'(16 fi + r, 16 fj + 4 g + q).
 //
+// The X panel's chunk swizzle adds row bit 3 to gemm_bf16_nn4_kernel's: chunk c of row k sits
+// at c ^ ((k & 3) << 2) ^ (((k >> 3) & 1) << 1). A transposing read serves 32 lanes at a time,
+// lanes 0-15 from rows 8 g' .. +3 and lanes 16-31 from rows 8 g' + 8 .. +11 (g' even); with
+// the low-bit swizzle alone both groups hit the same 32 banks (35% of LDS-active cycles were
+// bank conflicts), with bit 3 they use the other 32. The DMA takes the row parity of each X
+// slab from one of two per-lane offsets (slab q holds rows 8 q .. 8 q + 7).
+//
 // The beta term is added into the accumulators during the two K-tiles whose k range is the
 // wave's rows (no registers hold X values through the loop, which the double-buffered
 // fragments need); those two K-tiles are peeled off the loop. It takes its own K-loop
@@ -1465,29 +1472,58 @@ MUON_DEVICE void n16_block(f32x4 (&acc)[8], const bf16x8_mfma& cb, const bf16x8_
 }
 // The same with two loads of the DMA of a K-tile (slabs 2 FI and 2 FI + 1 of the 16 this
 // wave issues per K-tile: B panel slabs for FI < 4, X panel slabs for FI >= 4), each after an
-// MFMA. m0 and the scalar offsets of both loads come in precomputed.
+// MFMA, with per-lane offsets vo0 and vo1. m0 and the scalar offsets of both loads come in
+// precomputed.
 template <int FI, int XO>
 MUON_DEVICE void n16_block_dma(f32x4 (&acc)[8], const bf16x8_mfma& cb, const bf16x8_mfma (&cx)[8],
                                bf16x8_mfma& nb, i16x4& nl, i16x4& nh, uint32_t ba, uint32_t xa,
-                               int vo, u32x4 rs, int so0, int so1, uint32_t m00, uint32_t m01) {
+                               int vo0, int vo1, u32x4 rs, int so0, int so1, uint32_t m00,
+                               uint32_t m01) {
   asm volatile(
       "s_mov_b32 m0, %[m00]\n\t"
       "ds_read_b64_tr_b16 %[nl], %[xa] offset:%[o0]\n\t" M16(c0, x0, b)
-      "buffer_load_dwordx4 %[vo], %[rs], %[so0] offen lds\n\t"
+      "buffer_load_dwordx4 %[vo0], %[rs], %[so0] offen lds\n\t"
       M16(c1, x1, b) "s_mov_b32 m0, %[m01]\n\t" M16(c2, x2, b)
       "ds_read_b64_tr_b16 %[nh], %[xa] offset:%[o1]\n\t" M16(c3, x3, b)
-      "buffer_load_dwordx4 %[vo], %[rs], %[so1] offen lds\n\t"
+      "buffer_load_dwordx4 %[vo1], %[rs], %[so1] offen lds\n\t"
       M16(c4, x4, b) M16(c5, x5, b)
       "ds_read_b128 %[nb], %[ba] offset:%[ob]\n\t" M16(c6, x6, b)
       M16(c7, x7, b)
       : N16_OUT(acc)
-      : N16_IN, [vo] "v"(vo), [rs] "s"(rs), [so0] "s"(so0), [so1] "s"(so1), [m00] "s"(m00),
+      : N16_IN, [vo0] "v"(vo0), [vo1] "v"(vo1), [rs] "s"(rs), [so0] "s"(so0), [so1] "s"(so1), [m00] "s"(m00),
         [m01] "s"(m01)
       : "m0", "memory");
 }
 #undef N16_OUT
 #undef N16_IN
 #undef M16
+
+#define DA "buffer_load_dwordx4 %[voa], %[rsa], %[ta] offen lds\n\t"
+#define DXE "buffer_load_dwordx4 %[voxe], %[rsx], %[tx] offen lds\n\t"
+#define DXO "buffer_load_dwordx4 %[voxo], %[rsx], %[tx] offen lds\n\t"
+#define NA "s_add_u32 m0, m0, 0x1000\n\ts_add_u32 %[ta], %[ta], %[sta]\n\ts_nop 0\n\t"
+#define NX "s_add_u32 m0, m0, 0x1000\n\ts_add_u32 %[tx], %[tx], %[stx]\n\ts_nop 0\n\t"
+// The DMA of one K-tile without MFMAs (pipeline start); X slab q takes the per-lane offsets
+// of its row parity (voxe for even q, voxo for odd).
+MUON_DEVICE void n16_dma(int voa, int voxe, int voxo, u32x4 rsa, u32x4 rsx, int soa, int sox,
+                         int sta, int stx, uint32_t m0a, uint32_t m0x) {
+  int ta, tx;
+  asm volatile(
+      "s_mov_b32 m0, %[m0a]\n\ts_mov_b32 %[ta], %[soa]\n\ts_nop 0\n\t"
+      DA NA DA NA DA NA DA NA DA NA DA NA DA NA DA
+      "s_mov_b32 m0, %[m0x]\n\ts_mov_b32 %[tx], %[sox]\n\ts_nop 0\n\t"
+      DXE NX DXO NX DXE NX DXO NX DXE NX DXO NX DXE NX DXO
+      : [ta] "=&s"(ta), [tx] "=&s"(tx)
+      : [voa] "v"(voa), [voxe] "v"(voxe), [voxo] "v"(voxo), [rsa] "s"(rsa), [rsx] "s"(rsx),
+        [soa] "s"(soa), [sox] "s"(sox), [sta] "s"(sta), [stx] "s"(stx), [m0a] "s"(m0a),
+        [m0x] "s"(m0x)
+      : "m0", "scc", "memory");
+}
+#undef DA
+#undef DXE
+#undef DXO
+#undef NA
+#undef NX
 
 // All 24 fragment reads of one substep without MFMAs (pipeline start).
 template <int XO>
@@ -1536,22 +1572,23 @@ template <int XO>
 MUON_DEVICE void n16_substep_dma(f32x4 (&acc)[8][8], const bf16x8_mfma (&cb)[8],
                                  const bf16x8_mfma (&cx)[8], bf16x8_mfma (&nb)[8], i16x4 (&nl)[8],
                                  i16x4 (&nh)[8], uint32_t ba, const uint32_t (&xa)[8], int voa,
-                                 int vox, u32x4 rsa, u32x4 rsx, int soa, int sox, int sta, int stx,
+                                 int voxe, int voxo, u32x4 rsa, u32x4 rsx, int soa, int sox, int sta, int stx,
                                  uint32_t m0a, uint32_t m0x) {
-  n16_block_dma<0, XO>(acc[0], cb[0], cx, nb[0], nl[0], nh[0], ba, xa[0], voa, rsa, soa, soa + sta, m0a, m0a + 0x1000);
-  n16_block_dma<1, XO>(acc[1], cb[1], cx, nb[1], nl[1], nh[1], ba, xa[1], voa, rsa, soa + 2 * sta, soa + 3 * sta, m0a + 0x2000, m0a + 0x3000);
-  n16_block_dma<2, XO>(acc[2], cb[2], cx, nb[2], nl[2], nh[2], ba, xa[2], voa, rsa, soa + 4 * sta, soa + 5 * sta, m0a + 0x4000, m0a + 0x5000);
-  n16_block_dma<3, XO>(acc[3], cb[3], cx, nb[3], nl[3], nh[3], ba, xa[3], voa, rsa, soa + 6 * sta, soa + 7 * sta, m0a + 0x6000, m0a + 0x7000);
-  n16_block_dma<4, XO>(acc[4], cb[4], cx, nb[4], nl[4], nh[4], ba, xa[4], vox, rsx, sox, sox + stx, m0x, m0x + 0x1000);
-  n16_block_dma<5, XO>(acc[5], cb[5], cx, nb[5], nl[5], nh[5], ba, xa[5], vox, rsx, sox + 2 * stx, sox + 3 * stx, m0x + 0x2000, m0x + 0x3000);
-  n16_block_dma<6, XO>(acc[6], cb[6], cx, nb[6], nl[6], nh[6], ba, xa[6], vox, rsx, sox + 4 * stx, sox + 5 * stx, m0x + 0x4000, m0x + 0x5000);
-  n16_block_dma<7, XO>(acc[7], cb[7], cx, nb[7], nl[7], nh[7], ba, xa[7], vox, rsx, sox + 6 * stx, sox + 7 * stx, m0x + 0x6000, m0x + 0x7000);
+  n16_block_dma<0, XO>(acc[0], cb[0], cx, nb[0], nl[0], nh[0], ba, xa[0], voa, voa, rsa, soa, soa + sta, m0a, m0a + 0x1000);
+  n16_block_dma<1, XO>(acc[1], cb[1], cx, nb[1], nl[1], nh[1], ba, xa[1], voa, voa, rsa, soa + 2 * sta, soa + 3 * sta, m0a + 0x2000, m0a + 0x3000);
+  n16_block_dma<2, XO>(acc[2], cb[2], cx, nb[2], nl[2], nh[2], ba, xa[2], voa, voa, rsa, soa + 4 * sta, soa + 5 * sta, m0a + 0x4000, m0a + 0x5000);
+  n16_block_dma<3, XO>(acc[3], cb[3], cx, nb[3], nl[3], nh[3], ba, xa[3], voa, voa, rsa, soa + 6 * sta, soa + 7 * sta, m0a + 0x6000, m0a + 0x7000);
+  n16_block_dma<4, XO>(acc[4], cb[4], cx, nb[4], nl[4], nh[4], ba, xa[4], voxe, voxo, rsx, sox, sox + stx, m0x, m0x + 0x1000);
+  n16_block_dma<5, XO>(acc[5], cb[5], cx, nb[5], nl[5], nh[5], ba, xa[5], voxe, voxo, rsx, sox + 2 * stx, sox + 3 * stx, m0x + 0x2000, m0x + 0x3000);
+  n16_block_dma<6, XO>(acc[6], cb[6], cx, nb[6], nl[6], nh[6], ba, xa[6], voxe, voxo, rsx, sox + 4 * stx, sox + 5 * stx, m0x + 0x4000, m0x + 0x5000);
+  n16_block_dma<7, XO>(acc[7], cb[7], cx, nb[7], nl[7], nh[7], ba, xa[7], voxe, voxo, rsx, sox + 6 * stx, sox + 7 * stx, m0x + 0x6000, m0x + 0x7000);
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
 // ratio * X(i, j .. j+3) added into the accumulators of row blocks FI0 .. FI0+3 (X panel
 // rows (fi - FI0) * 16 + lane%16 of the K-tile staged at sx, columns 128 wn + 16 fj +
-// 4 (lane/16)). Each accumulator is copied out of and back into its own AGPRs.
+// 4 (lane/16), in the nn16 swizzle). Each accumulator is copied out of and back into its own
+// AGPRs.
 template <int FI0>
 MUON_DEVICE void n16_beta(f32x4 (&acc)[8][8], uint32_t sx, int wn, int lane, float ratio) {
   asm volatile("" : "+v"(sx));
@@ -1559,7 +1596,7 @@ MUON_DEVICE void n16_beta(f32x4 (&acc)[8][8], uint32_t sx, int wn, int lane, flo
   const uint32_t rowb = sx + r * NN_XROWB + (g & 1) * 8;
 #pragma unroll
   for (int fj = 0; fj < 8; ++fj) {
-    const uint32_t a = rowb + ((((wn * 16 + fj * 2 + (g >> 1)) ^ ((r & 3) << 2))) << 4);
+    const uint32_t a = rowb + ((((wn * 16 + fj * 2 + (g >> 1)) ^ ((r & 3) << 2) ^ (((r >> 3) & 1) << 1))) << 4);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const u32x2 w = *(const u32x2 __attribute__((address_space(3)))*)(a + q * 16 * NN_XROWB);
@@ -1599,6 +1636,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g) {
   const int voa = ra_in * lda_b + (((lane & 7) ^ kswz(ra_in)) << 4);
   const int rx_in = wave * 2 + (lane >> 5);
   const int vox = rx_in * ldx_b + (((lane & 31) ^ ((rx_in & 3) << 2)) << 4);
+  const int voxo = rx_in * ldx_b + (((lane & 31) ^ ((rx_in & 3) << 2) ^ 2) << 4);
   const int sta = 32 * lda_b, stx = 8 * ldx_b;
   const bf16_t* const A0 = (const bf16_t*)g.a;
   const bf16_t* const X0 = (const bf16_t*)g.b;
@@ -1614,7 +1652,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g) {
   uint32_t xoff[8];
 #pragma unroll
   for (int f = 0; f < 8; ++f) {
-    const int chunk = (wn * 16 + f * 2 + ((fr & 3) >> 1)) ^ (((fr >> 2) & 3) << 2);
+    const int chunk = (wn * 16 + f * 2 + ((fr & 3) >> 1)) ^ (((fr >> 2) & 3) << 2) ^ ((fg & 1) << 1);
     xoff[f] = NN_ATILEB + (8 * fg + (fr >> 2)) * NN_XROWB + chunk * 16 + (fr & 1) * 8;
   }
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
@@ -1636,10 +1674,10 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g) {
   bf16x8_mfma b0[8], b1[8], x0[8], x1[8];
   i16x4 xl[8], xh[8];
   // K-tiles 0 and 1 of the first tile
-  nn4_dma(voa, vox, rsa, rsx, 0, 0, sta, stx, m0w, m0w + NN_ATILEB);
+  n16_dma(voa, vox, voxo, rsa, rsx, 0, 0, sta, stx, m0w, m0w + NN_ATILEB);
   wait_vmcnt0();
   lds_barrier();
-  nn4_dma(voa, vox, rsa, rsx, V2_ROWB, V2_BK * ldx_b, sta, stx, m0w + NN_STAGEB,
+  n16_dma(voa, vox, voxo, rsa, rsx, V2_ROWB, V2_BK * ldx_b, sta, stx, m0w + NN_STAGEB,
           m0w + NN_STAGEB + NN_ATILEB);
   set_xa(0);
   n16_frag_load<0>(b0, xl, xh, baddr(0, 0), xa);
@@ -1694,7 +1732,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g) {
       const int k2 = c2 ? kt + 2 : kt + 2 - KT;
       set_xa(cs ^ 1);
       const uint32_t m0a = m0w + cs * NN_STAGEB;
-      n16_substep_dma<0>(acc, b1, x1, b0, xl, xh, baddr(cs ^ 1, 0), xa, voa, vox, c2 ? rsa : rsa_n,
+      n16_substep_dma<0>(acc, b1, x1, b0, xl, xh, baddr(cs ^ 1, 0), xa, voa, vox, voxo, c2 ? rsa : rsa_n,
                          c2 ? rsx : rsx_n, k2 * V2_ROWB, k2 * V2_BK * ldx_b, sta, stx, m0a,
                          m0a + NN_ATILEB);
       n16_join(x0, xl, xh);
