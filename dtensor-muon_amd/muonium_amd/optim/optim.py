@@ -81,7 +81,9 @@ def _per_tensor_runs(algorithm: MuonAlgorithm, params, grads, state, split_sizes
     return list(keyed.values())
 
 
-_MAX_SIDE_STREAMS = 4  # GPU_MAX_HW_QUEUES is 4 by default: one hardware queue each
+# GPU_MAX_HW_QUEUES is 4 by default: with the caller's stream, one hardware queue each (a
+# fourth side stream shared a queue with the third, which serialized their buckets)
+_MAX_SIDE_STREAMS = 3
 _side_streams: dict[tuple[int, int], torch.cuda.Stream] = {}
 
 
@@ -95,22 +97,29 @@ def _side_stream(device: torch.device, slot: int) -> torch.cuda.Stream:
     return stream
 
 
-def _concurrent_slots(buckets, algorithm: MuonAlgorithm, batch_size: int | None) -> dict[int, int]:
-    """Side-stream slot per bucket index for buckets too small to fill the device.
+def _concurrent_plan(buckets, algorithm: MuonAlgorithm,
+                     batch_size: int | None) -> tuple[dict[int, int], list[int]]:
+    """Side-stream slot per bucket index for buckets too small to fill the device, and the
+    order in which to enqueue the buckets.
 
     A bucket whose Gram products (upper-triangle 256-row tiles x matrices) launch fewer
     workgroups than the device has compute units leaves most of it idle (the GPT-2 set:
-    72 workgroups per product on 256 CUs); such buckets run concurrently, one stream per
-    padded workspace shape, so each side stream holds at most one workspace per shape
-    (workspaces are cached per stream: a side stream never touches the buffer of the
-    current stream or of another side stream). Large buckets stay on the current
-    stream. Built-in algorithms only."""
+    72 workgroups per product on 256 CUs); such buckets run concurrently. When every bucket
+    is small, the smallest stays on the caller's stream and the others take side streams,
+    largest first; otherwise all small buckets take side streams and the large ones stay on
+    the caller's stream. Buckets on side streams are enqueued first, so each forks from the
+    caller's stream as the step starts and the largest is not held back by the host time of
+    enqueueing the others (about 15 us per launch, 17 launches per bucket). Workspaces are
+    cached per stream, so a side stream never touches the buffer of the current stream or of
+    another side stream, also when two buckets pad to the same workspace shape (the GPT-2
+    mlp c_fc and the transposed c_proj: on one stream they ran one after the other and made
+    the step's critical path). Built-in algorithms only."""
+    natural = list(range(len(buckets)))
     if not type(algorithm).__module__.startswith("muonium_amd.") or torch.compiler.is_compiling():
-        return {}  # (under an outer torch.compile the buckets run in the traced order)
-    from muonium_amd import _ops
+        return {}, natural  # (under an outer torch.compile the buckets run in the traced order)
 
     cus: dict[torch.device, int] = {}
-    small: dict[int, tuple] = {}
+    work: dict[int, int] = {}
     for bi, (device, _, dev_g, _, _) in enumerate(buckets):
         if device.type != "cuda" or dev_g[0].dim() < 2:
             continue
@@ -120,11 +129,13 @@ def _concurrent_slots(buckets, algorithm: MuonAlgorithm, batch_size: int | None)
         nmat = math.prod(dev_g[0].shape[:-2]) * min(len(dev_g), batch_size or len(dev_g))
         tiles = -(-min(rows, cols) // 256)
         if tiles * (tiles + 1) // 2 * nmat < cus[device]:
-            small[bi] = (device, _ops._padded_extents(torch.bfloat16, rows, cols))
-    if len(small) < 2:
-        return {}
-    keys: dict[tuple, int] = {}
-    return {bi: keys.setdefault(key, len(keys)) % _MAX_SIDE_STREAMS for bi, key in small.items()}
+            work[bi] = min(rows, cols) ** 2 * max(rows, cols) * nmat
+    if len(work) < 2:
+        return {}, natural
+    ranked = sorted(work, key=lambda bi: -work[bi])
+    side = ranked[:-1] if len(work) == len(buckets) else ranked
+    slots = {bi: k % _MAX_SIDE_STREAMS for k, bi in enumerate(side)}
+    return slots, side + [bi for bi in natural if bi not in slots]
 
 
 class Muon(torch.optim.Optimizer):
@@ -479,9 +490,10 @@ class Muon(torch.optim.Optimizer):
             return
 
         buckets = _group_muon_tensors(params, grads, state, lr_ratios)
-        slots = _concurrent_slots(buckets, algorithm, self.batch_size)
+        slots, order = _concurrent_plan(buckets, algorithm, self.batch_size)
         forked: dict[tuple[torch.device, int], torch.cuda.Stream] = {}
-        for bi, (device, dev_p, dev_g, dev_state, dev_lr) in enumerate(buckets):
+        for bi in order:
+            device, dev_p, dev_g, dev_state, dev_lr = buckets[bi]
             if bi in slots:
                 side = _side_stream(device, slots[bi])
                 if (device, slots[bi]) not in forked:

@@ -45,7 +45,9 @@ def test_gpt2_set_one_optimizer_matches_oracle():
     optim_mod._side_streams.clear()
     opt.step()
     torch.cuda.synchronize()
-    # three padded workspace shapes (3072 x 768 pads as 768 x 3072 does), one stream each
+    # four small buckets: the three largest on side streams (768 x 3072 and 3072 x 768, which
+    # pad alike, on two of them, each with its own workspace), the 768 x 768 bucket on the
+    # caller's stream
     assert len(optim_mod._side_streams) == 3
 
     coeffs, prescale = muon_ref.strategy_coeffs("polar_express", 5)

@@ -491,9 +491,10 @@ def test_plumbing_config_is_bit_repeatable():
 
 
 def test_small_buckets_on_side_streams_match_sequential_buckets():
-    """Buckets too small to fill the device run concurrently on side streams (one per
-    workspace shape); the result is the same, bit for bit, as one bucket at a time, and
-    the step is ordered after earlier work on the caller's stream and before later work."""
+    """Buckets too small to fill the device run concurrently (the smallest on the caller's
+    stream, the others on side streams, two of them with the same workspace shape); the
+    result is the same, bit for bit, as one bucket at a time, and the step is ordered after
+    earlier work on the caller's stream and before later work."""
     from muonium_amd.optim import optim as optim_mod
 
     # workspace shapes (m_pad, n_pad): (256, 512), (256, 256), (256, 768) twice, (256, 512)
