@@ -151,6 +151,34 @@ def test_lp_tiled_prepass_outputs_exact(fmt, cls, block, shape, gdtype):
     _check_tiled_prepass(fmt, cls, block, shape, gdtype)
 
 
+@pytest.mark.parametrize("fmt,cls,block", [("8bit", OptimState8bit, 256), ("4bit", OptimState4bit, 128),
+                                           ("fp8", OptimStateFp8, 256), ("8bit", OptimState8bit, 2048),
+                                           ("fp8", OptimStateFp8, 2048)])
+def test_lp_extreme_values_exact(fmt, cls, block):
+    """Blocks at the edges of fp32 through the tiled pre-pass (one-pass and deferred
+    scales): a 1e38 absmax (a scale above 2^125, whose reciprocal is subnormal); values of
+    1e-35 and subnormals beside an absmax of 1; a block clipped at 1e-12 holding 1e-31;
+    signed zeros and all-zero blocks. Codes and scales bit-exact against the oracle's IEEE
+    quotients, X0 equal to bf16(g'). (The norm partials of values near 1e38 overflow fp32;
+    not checked.)"""
+    gen = torch.Generator().manual_seed(17)
+    g = torch.randn(256, 512, generator=gen)
+    special = [
+        [1e38, -3e37, 1e30, 1.0, 1e-10, -2.5e36],
+        [1.0, 1e-35, -2e-38, 3e-39, -1e-40, 1e-45, 0.0, -0.0],
+        [1e-20, 1e-40, -1e-25, 0.0],
+        [5e-31, -1e-31, 7e-31, 8e-31, 1e-32],
+        [0.0, -0.0],
+    ]
+    for r, vals in enumerate(special):
+        row = torch.tensor(vals, dtype=torch.float32)
+        reps = -(-512 // len(vals))
+        g[2 * r] = row.repeat(reps)[:512] * (torch.rand(512, generator=gen) < 0.97)
+        g[2 * r + 1] = row.flip(0).repeat(reps)[:512]
+    g[10, 300:] = 0.0
+    _check_tiled_prepass(fmt, cls, block, (256, 512), torch.float32, g=g, check_partials=False)
+
+
 # blocks of more than 256 values: the reference's default 2048 (optim_lp.py:49), other
 # multiples of 256, and one block per tensor (an fp8 per-tensor scale)
 DEFERRED = [("8bit", OptimState8bit, 2048), ("4bit", OptimState4bit, 2048),
@@ -175,7 +203,7 @@ def test_lp_deferred_scale_prepass_outputs_exact(fmt, cls, block, shape, gdtype)
     _check_tiled_prepass(fmt, cls, block, shape, gdtype)
 
 
-def _check_tiled_prepass(fmt, cls, block, shape, gdtype):
+def _check_tiled_prepass(fmt, cls, block, shape, gdtype, g=None, check_partials=True):
     from muonium_amd import _lib
 
     lib = _lib.load()
@@ -185,8 +213,9 @@ def _check_tiled_prepass(fmt, cls, block, shape, gdtype):
     for d in shape[:-2]:
         nb *= d
     rows, cols = shape[-2:]
-    gen = torch.Generator().manual_seed(5)
-    g = (torch.randn(shape, generator=gen) * torch.exp(torch.randn(*shape[:-1], 1, generator=gen)))
+    if g is None:
+        gen = torch.Generator().manual_seed(5)
+        g = torch.randn(shape, generator=gen) * torch.exp(torch.randn(*shape[:-1], 1, generator=gen))
     g = g.to(gdtype)
     st = _state(cls, shape, block)
     codes = np.zeros(st.codes.numel(), np.uint8)
@@ -215,6 +244,8 @@ def _check_tiled_prepass(fmt, cls, block, shape, gdtype):
     x = torch.from_numpy(gq).view(nb, rows, cols).bfloat16().float()
     exp[:, :m, :n] = x.transpose(1, 2) if rows > cols else x
     assert torch.equal(X0, exp)
+    if not check_partials:
+        return
     rup = lambda v: -(-v // 256) * 256
     off = 2 * rup(nb * mp * npad * 2) + 2 * rup(nb * mp * mp * 2)
     parts = (mp // 64) * (npad // 64)
