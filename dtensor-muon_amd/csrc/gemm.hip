@@ -1439,11 +1439,11 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn4_kernel(GemmArgs g) {
 // bank conflicts), with bit 3 they use the other 32. The DMA takes the row parity of each X
 // slab from one of two per-lane offsets (slab q holds rows 8 q .. 8 q + 7).
 //
-// The beta term is added into the accumulators during the two K-tiles whose k range is the
-// wave's rows (no registers hold X values through the loop, which the double-buffered
-// fragments need); those two K-tiles are peeled off the loop. It takes its own K-loop
-// structure and per-tile work, so below K = 2048 (where that work weighs more)
-// gemm_bf16_nn4_kernel is faster and is used instead.
+// The beta term is added during the two K-tiles whose k range is the wave's rows (no
+// registers hold X values through the loop, which the double-buffered fragments need), by
+// 32 more MFMAs per substep (n16_beta), so the accumulators never leave their AGPRs; those
+// two K-tiles are peeled off the loop. It takes its own K-loop structure and per-tile work,
+// so below K = 2048 (where that work weighs more) gemm_bf16_nn4_kernel is used instead.
 #define M16(C, X, B) "v_mfma_f32_16x16x32_bf16 %[" #C "], %[" #X "], %[" #B "], %[" #C "]\n\t"
 #define N16_OUT(ACC)                                                                      \
   [c0] "+a"(ACC[0]), [c1] "+a"(ACC[1]), [c2] "+a"(ACC[2]), [c3] "+a"(ACC[3]),               \
@@ -1585,31 +1585,55 @@ MUON_DEVICE void n16_substep_dma(f32x4 (&acc)[8][8], const bf16x8_mfma (&cb)[8],
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
-// ratio * X(i, j .. j+3) added into the accumulators of row blocks FI0 .. FI0+3 (X panel
-// rows (fi - FI0) * 16 + lane%16 of the K-tile staged at sx, columns 128 wn + 16 fj +
-// 4 (lane/16), in the nn16 swizzle). Each accumulator is copied out of and back into its own
-// AGPRs.
-template <int FI0>
-MUON_DEVICE void n16_beta(f32x4 (&acc)[8][8], uint32_t sx, int wn, int lane, float ratio) {
-  asm volatile("" : "+v"(sx));
+// The beta term on the matrix cores: ratio * X(i, j) = sum_k X(k, j) (ratio delta(k, i)), so
+// an MFMA with the substep's X fragment as srcA (k = the substep's 32 rows) and a diagonal
+// fragment as srcB adds it to the accumulators of the two row blocks those rows are. ratio is
+// split into two bf16 parts, hi = RNE(ratio) and lo = RNE(ratio - hi) (16 significant bits),
+// so every product is exact; the accumulators never leave their AGPRs. (A read-modify-write
+// through VGPRs made the compiler move accumulators between AGPRs next to the inline-asm
+// MFMAs, whose latency it does not see, and the moves raced their results: B X then differed
+// by an ulp from run to run.) db[par][part]: lane l (r = l%16, g = l/16) holds B(k, n) for
+// k = 8 g .. 8 g + 7, n = r: part at k = 16 par + r, else zero.
+MUON_DEVICE void n16_beta_frags(float ratio, int lane, bf16x8_mfma (&db)[2][2]) {
+  const float hi = bf16_to_f32(f32_to_bf16(ratio));
+  const float lo = ratio - hi;
+  const uint32_t parts[2] = {(uint32_t)f32_to_bf16(hi), (uint32_t)f32_to_bf16(lo)};
   const int r = lane & 15, g = lane >> 4;
-  const uint32_t rowb = sx + r * NN_XROWB + (g & 1) * 8;
 #pragma unroll
-  for (int fj = 0; fj < 8; ++fj) {
-    const uint32_t a = rowb + ((((wn * 16 + fj * 2 + (g >> 1)) ^ ((r & 3) << 2) ^ (((r >> 3) & 1) << 1))) << 4);
+  for (int par = 0; par < 2; ++par)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const u32x2 w = *(const u32x2 __attribute__((address_space(3)))*)(a + q * 16 * NN_XROWB);
-      f32x4 av;
-      asm volatile("" : "=v"(av) : "0"(acc[FI0 + q][fj]));
-      av[0] += ratio * __uint_as_float(w.x << 16);
-      av[1] += ratio * __uint_as_float(w.x & 0xffff0000u);
-      av[2] += ratio * __uint_as_float(w.y << 16);
-      av[3] += ratio * __uint_as_float(w.y & 0xffff0000u);
-      asm volatile("" : "=a"(acc[FI0 + q][fj]) : "0"(av));
+    for (int pt = 0; pt < 2; ++pt) {
+      const int e = 16 * par + r - 8 * g;  // element of this lane's 8 holding the diagonal
+      uint32_t w[4];
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        w[d] = (e == 2 * d ? parts[pt] : 0u) | (e == 2 * d + 1 ? parts[pt] << 16 : 0u);
+      db[par][pt] = __builtin_bit_cast(bf16x8_mfma, u32x4{w[0], w[1], w[2], w[3]});
     }
-  }
 }
+
+#define M16(C, X, B) "v_mfma_f32_16x16x32_bf16 %[" #C "], %[" #X "], %[" #B "], %[" #C "]\n\t"
+#define NB_ROW(P, F, B)                                                                      \
+  M16(P##0, x0, B) M16(P##1, x1, B) M16(P##2, x2, B) M16(P##3, x3, B)                         \
+  M16(P##4, x4, B) M16(P##5, x5, B) M16(P##6, x6, B) M16(P##7, x7, B)
+// ratio * X added to row blocks FI and FI + 1 (rows 32 ks .. 32 ks + 31 of the K-tile whose
+// X fragments cx are the substep's): 32 MFMAs, the hi parts of both row blocks first.
+template <int FI>
+MUON_DEVICE void n16_beta(f32x4 (&acc)[8][8], const bf16x8_mfma (&cx)[8],
+                          const bf16x8_mfma (&db)[2][2]) {
+  asm volatile(NB_ROW(a, FI, d0h) NB_ROW(b, FI + 1, d1h) NB_ROW(a, FI, d0l) NB_ROW(b, FI + 1, d1l)
+               : [a0] "+a"(acc[FI][0]), [a1] "+a"(acc[FI][1]), [a2] "+a"(acc[FI][2]),
+                 [a3] "+a"(acc[FI][3]), [a4] "+a"(acc[FI][4]), [a5] "+a"(acc[FI][5]),
+                 [a6] "+a"(acc[FI][6]), [a7] "+a"(acc[FI][7]), [b0] "+a"(acc[FI + 1][0]),
+                 [b1] "+a"(acc[FI + 1][1]), [b2] "+a"(acc[FI + 1][2]), [b3] "+a"(acc[FI + 1][3]),
+                 [b4] "+a"(acc[FI + 1][4]), [b5] "+a"(acc[FI + 1][5]), [b6] "+a"(acc[FI + 1][6]),
+                 [b7] "+a"(acc[FI + 1][7])
+               : [x0] "v"(cx[0]), [x1] "v"(cx[1]), [x2] "v"(cx[2]), [x3] "v"(cx[3]),
+                 [x4] "v"(cx[4]), [x5] "v"(cx[5]), [x6] "v"(cx[6]), [x7] "v"(cx[7]),
+                 [d0h] "v"(db[0][0]), [d0l] "v"(db[0][1]), [d1h] "v"(db[1][0]), [d1l] "v"(db[1][1]));
+}
+#undef NB_ROW
+#undef M16
 
 __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g) {
   constexpr int WM = 128, WN = 128;
@@ -1710,22 +1734,22 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // one K-tile: substep 0 (reading substep 1's fragments), [the beta term], wait for K-tile
-    // kt + 1's DMA, barrier, substep 1 (reading K-tile kt + 1's first fragments) with the DMA
-    // of K-tile kt + 2 (this tile's or the next's) into this K-tile's stage. The two K-tiles
-    // that carry the beta term (ratio * X added into the accumulators of the rows their k
-    // range covers) are peeled off the loops, which keeps the accumulators in one register
-    // assignment inside them.
+    // one K-tile: substep 0 (reading substep 1's fragments), wait for K-tile kt + 1's DMA,
+    // barrier, substep 1 (reading K-tile kt + 1's first fragments) with the DMA of K-tile
+    // kt + 2 (this tile's or the next's) into this K-tile's stage. In the two K-tiles whose k
+    // range is the wave's rows (peeled off the loops), each substep also adds ratio * X to
+    // the two row blocks its 32 k rows are.
     auto kstep = [&](int kt, auto beta_fi0) {
+      constexpr int FB = decltype(beta_fi0)::value;
       const int cs = kt & 1;
       set_xa(cs);
       n16_substep<16 * NN_XROWB * 2>(acc, b0, x0, b1, xl, xh, baddr(cs, 1), xa);
-      n16_join(x1, xl, xh);
-      if constexpr (decltype(beta_fi0)::value >= 0) {
-        mfma_to_valu_wait();
-        n16_beta<decltype(beta_fi0)::value>(acc, lds0 + cs * NN_STAGEB + NN_ATILEB, wn, lane, ratio);
-        valu_to_mfma_wait();
+      if constexpr (FB >= 0) {
+        bf16x8_mfma db[2][2];
+        n16_beta_frags(ratio, lane, db);
+        n16_beta<FB>(acc, x0, db);
       }
+      n16_join(x1, xl, xh);
       wait_vmcnt0();
       lds_barrier();
       const bool c2 = kt + 2 < KT;
@@ -1735,6 +1759,11 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g) {
       n16_substep_dma<0>(acc, b1, x1, b0, xl, xh, baddr(cs ^ 1, 0), xa, voa, vox, voxo, c2 ? rsa : rsa_n,
                          c2 ? rsx : rsx_n, k2 * V2_ROWB, k2 * V2_BK * ldx_b, sta, stx, m0a,
                          m0a + NN_ATILEB);
+      if constexpr (FB >= 0) {
+        bf16x8_mfma db[2][2];
+        n16_beta_frags(ratio, lane, db);
+        n16_beta<FB + 2>(acc, x1, db);
+      }
       n16_join(x0, xl, xh);
     };
     using no_beta = std::integral_constant<int, -1>;
