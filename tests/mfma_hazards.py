@@ -11,6 +11,11 @@ states. This scan walks each kernel's instruction stream and reports
 * a register written by a VALU instruction and read by an MFMA (any operand) fewer than 3
   wait states later.
 
+The wait counts are conservative: one pass class above what the compiler itself inserts
+after the same MFMAs when they come from builtins (short.hip's, at 13-16 wait states for
+32 x 32 x 16). The scan is meant for kernels whose MFMAs are inline asm (gemm.hip); for
+builtin MFMAs the compiler's own hazard recognizer places the waits.
+
 Every instruction between the two counts as one wait state, `s_nop N` as N + 1; the scan
 follows straight-line order within a basic block only (a label restarts it), so it can miss
 a hazard across a branch but does not invent one. Usage:
