@@ -1418,7 +1418,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn4_kernel(GemmArgs g) {
 }
 
 // ----------------------------------------------------------------------------------
-// The persistent B X kernel on 16 x 16 x 32 MFMAs, for K of at least 2048.
+// The persistent B X kernel on 16 x 16 x 32 MFMAs, for K of at least 1024.
 //
 // Same tiling, waves, LDS layout, tile order and epilogue staging as gemm_bf16_nn4_kernel;
 // the wave's 128 x 128 block is 8 x 8 accumulators of 16 x 16 (AGPRs) and a K-tile is two
@@ -1443,7 +1443,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn4_kernel(GemmArgs g) {
 // registers hold X values through the loop, which the double-buffered fragments need), by
 // 32 more MFMAs per substep (n16_beta), so the accumulators never leave their AGPRs; those
 // two K-tiles are peeled off the loop. It takes its own K-loop structure and per-tile work,
-// so below K = 2048 (where that work weighs more) gemm_bf16_nn4_kernel is used instead.
+// so below K = 1024 (where that work weighs more) gemm_bf16_nn4_kernel is used instead.
 #define M16(C, X, B) "v_mfma_f32_16x16x32_bf16 %[" #C "], %[" #X "], %[" #B "], %[" #C "]\n\t"
 #define N16_OUT(ACC)                                                                      \
   [c0] "+a"(ACC[0]), [c1] "+a"(ACC[1]), [c2] "+a"(ACC[2]), [c3] "+a"(ACC[3]),               \
@@ -2309,7 +2309,7 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
       }
       // persistent: one workgroup per CU walks the tile list
       const int wgs = (int)std::min<int64_t>(blocks, device_cus());
-      if (K >= 2048)
+      if (K >= 1024)
         hipLaunchKernelGGL(gemm_bf16_nn16_kernel, dim3((unsigned)wgs), dim3(256), N4_SMEM, stream, g);
       else
         hipLaunchKernelGGL(gemm_bf16_nn4_kernel, dim3((unsigned)wgs), dim3(256), N4_SMEM, stream, g);
