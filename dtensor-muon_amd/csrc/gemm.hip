@@ -1851,7 +1851,8 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g) {
 // (4 a, 8 b) between its MFMAs. The DMA of K-tile k + 2 is spread over the second substep
 // of K-tile k (two loads per block of 8 MFMAs), right after the barrier that ends the reads
 // of its stage. On the Llama shapes X X^T and A A run 6-7% faster than on 32 x 32 x 16
-// MFMAs; launches with packed tiles measured 5% slower and stay on gemm_bf16_v2_kernel.
+// MFMAs; launches with packed tiles measured 2-5% slower on X X^T (also with a K loop per
+// tile kind) and stay on gemm_bf16_v2_kernel.
 //
 // Fragments (lane l, r = l % 16, g = l / 16): srcA is a-panel row 16 fi + r, srcB is
 // b-panel row 16 fj + r, both 8 consecutive k (logical chunk 4 ks + g of the row); the
