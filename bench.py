@@ -12,6 +12,10 @@ ms_per_step = Muon step time, plus the roofline of the dominant kernel (the B X 
 from hipEvent timing of every launch, per-kernel breakdowns, and the CPU baseline
 (the oracle's per-parameter loop on a bounded sample, on this host's cores).
 
+The K timed steps run without per-launch events (the step as a caller runs it); K more
+steps with the library's per-launch hipEvent brackets on give the per-kernel breakdown and
+the roofline, and their step time is printed beside (breakdown_ms_per_step).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
        [--config llama|gpt2|moe|moe_flat|plumbing] [--lp 8bit|4bit|fp8 [--block-size N|tensor]]
        [--no-cpu-baseline] | --reference-suite | --blas-ceiling | --calibrate-copy
@@ -493,34 +497,59 @@ def main() -> None:
         opt = cls(groups, foreach=True, block_size=block, **kw)
     else:
         opt = Muon(groups, foreach=args.config != "plumbing", **kw)
+    # Every step starts from the same synthetic gradients, as in training, where backward
+    # writes fresh gradients before each step. The foreach update adds the momentum into
+    # the gradients in place (Nesterov, muon.py:107-108), so stepping on without a refill
+    # grows them about 2.5x per step until, after about 37 steps, the fp32 sum of squares
+    # of a 4096 x 4096 matrix overflows and the iteration runs on zeros (measured 10%
+    # faster). The refill is a device copy between steps, outside the timed intervals.
+    grads = [p.grad for p in params]
+    grads0 = [g.clone() for g in grads]
+
+    def refill():
+        torch._foreach_copy_(grads, grads0)
+
     torch.cuda.synchronize()
     print(f"[bench] params={numel / 1e9:.3f}e9, warmup {args.warmup}", file=sys.stderr, flush=True)
 
     for i in range(args.warmup):
+        refill()
         opt.step()
         torch.cuda.synchronize()
         print(f"[bench] warmup step {i} done", file=sys.stderr, flush=True)
 
-    _lib.timing_enable(True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    # one event between consecutive steps (no synchronization inside the timed region):
-    # the mean over the K steps is ms_per_step, their median is reported beside it
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    evs[0].record()
-    for i in range(args.steps):
-        opt.step()
-        evs[i + 1].record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    kern = _lib.timing_read()
-    _lib.timing_enable(False)
-    ms_per_step = evs[0].elapsed_time(evs[-1]) / args.steps
-    step_ms = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps))
-    median_ms = step_ms[len(step_ms) // 2] if len(step_ms) % 2 else \
-        0.5 * (step_ms[len(step_ms) // 2 - 1] + step_ms[len(step_ms) // 2])
+    def timed_steps(bracketed: bool):
+        """K steps between a synchronize on each side, each step between its own pair of
+        events (no synchronization inside; the gradient refill before a step lies outside
+        its pair): (mean ms per step, median ms per step, wall s). With `bracketed` every
+        library launch also records its own hipEvent pair."""
+        _lib.timing_enable(bracketed)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(args.steps)]
+        for e0, e1 in evs:
+            refill()
+            e0.record()
+            opt.step()
+            e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        step_ms = sorted(e0.elapsed_time(e1) for e0, e1 in evs)
+        mean = sum(step_ms) / args.steps
+        med = step_ms[len(step_ms) // 2] if len(step_ms) % 2 else \
+            0.5 * (step_ms[len(step_ms) // 2 - 1] + step_ms[len(step_ms) // 2])
+        return mean, med, wall
+
+    # the timed region: the step as a caller runs it, no per-launch events
+    ms_per_step, median_ms, wall = timed_steps(False)
     print(f"[bench] {args.steps} steps: {ms_per_step:.2f} ms/step (wall {wall:.2f}s)",
           file=sys.stderr, flush=True)
+    # the breakdown region: the same K steps with every launch bracketed
+    brk_ms, _, _ = timed_steps(True)
+    kern = _lib.timing_read()
+    _lib.timing_enable(False)
+    print(f"[bench] {args.steps} bracketed steps: {brk_ms:.2f} ms/step", file=sys.stderr, flush=True)
 
     # the matrices the iteration sees: flatten=True collapses (e, r, c) to (e, r * c)
     orth_shapes = [(s[0], math.prod(s[1:])) if flatten and len(s) > 2 else s for s in shapes]
@@ -614,6 +643,7 @@ def main() -> None:
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 3),
         "median_ms_per_step": round(median_ms, 3),
+        "breakdown_ms_per_step": round(brk_ms, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
