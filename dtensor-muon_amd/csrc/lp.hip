@@ -550,6 +550,8 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
   int64_t blk0 = 0;
   bool one_block = false;
   uint32_t tmax = 0;
+  // tall tiles in 32-row halves: the first half's transposed X0 pieces (one per round)
+  uint4 xkeep[TALL && TROWS < LPT_ROWS ? (LPT_COLS * (TROWS / 8)) / 256 : 1];
   if constexpr (DEFER) {
     // (a tile of padding rows only, r0 >= rows, has no block and sends nothing)
     if (r0 < a.rows) {
@@ -625,7 +627,9 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
         // columns jb + 4 (i % 4) .. +3, and receives column jb + i of rows kb .. kb+3; two
         // such reads give the 8 rows of one X0 piece. Round `it`: column group
         // 4 wave + it % 4, lane group gg takes rows 32 (it / 4) + 8 gg, so the four lane
-        // groups write 64 contiguous bytes of each X0 row.
+        // groups write 64 contiguous bytes of each X0 row. With 32-row halves the first
+        // half's pieces stay in registers and go out beside the second half's, so each X0
+        // row's 128 bytes are written together.
         const int tl = tid & 63, gg = tl >> 4, ti = tl & 15;
 #pragma unroll
         for (int it = 0; it < (LPT_COLS * SEGS) / 256; ++it) {
@@ -636,7 +640,17 @@ __global__ __launch_bounds__(256) void lp_prepass_tile_kernel(LpTileArgs a) {
           const lp_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
               (__attribute__((address_space(3))) lp_i16x4*)&tileT[rr + 4 + (ti >> 2)][jb + 4 * (ti & 3)]);
           const uint4 w = __builtin_bit_cast(uint4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-          *(uint4*)(x0 + (c0 + jb + ti) * a.x_pitch + r0 + p0 + rr) = w;
+          bf16_t* const xrow = x0 + (c0 + jb + ti) * a.x_pitch + r0;
+          if constexpr (TROWS < LPT_ROWS) {
+            if (p0 == 0) {
+              xkeep[it] = w;
+            } else {
+              *(uint4*)(xrow + rr) = xkeep[it];
+              *(uint4*)(xrow + p0 + rr) = w;
+            }
+          } else {
+            *(uint4*)(xrow + p0 + rr) = w;
+          }
         }
         if (p != NP - 1) lds_sync();  // the next rows reuse the tile
       }
