@@ -410,9 +410,29 @@ template <int QF>
 MUON_DEVICE void lp_codes8(const float (&m)[8], float sc, bool sparse_map, const uint32_t* qthr,
                            const uint8_t* qtab, int (&cq)[8], uint2& c8) {
 #pragma clang fp contract(off)
+  // The quotients m / sc, correctly rounded, by Markstein's method from the correctly
+  // rounded reciprocal r = 1 / sc (one IEEE division per 8 values): q0 = m r, then the
+  // exact remainder e = m - sc q0 (fma) and y = q0 + e r (fma) is the rounded quotient
+  // (P. Markstein, IBM J. Res. Dev. 34(1), 1990). It needs normal intermediates: r normal
+  // (sc <= 2^125), e exact and normal (|m| >= 2^-78) and q0 normal (|m| >= sc 2^-100).
+  // A lane with any value outside that range (zeros included) takes the IEEE division for
+  // its 8 values; NaN or infinite scales fail the first test. Checked against the IEEE
+  // division on the CPU over every |m| <= sc for eight scales and 9e8 random pairs.
   float ys[8];
+  const float r = 1.0f / sc;
+  const float lim = fmaxf(0x1p-78f, sc * 0x1p-100f);
+  bool fast = sc <= 0x1p125f;
 #pragma unroll
-  for (int k = 0; k < 8; ++k) ys[k] = m[k] / sc;
+  for (int k = 0; k < 8; ++k) {
+    const float q0 = m[k] * r;
+    const float e = __builtin_fmaf(-sc, q0, m[k]);
+    ys[k] = __builtin_fmaf(e, r, q0);
+    fast = fast && fabsf(m[k]) >= lim;
+  }
+  if (!fast) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) ys[k] = m[k] / sc;
+  }
   if constexpr (QF == MUON_Q_FP8) {
     // v_cvt_pk_fp8_f32 writes two codes into the low or high half of the word
     uint32_t w0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ys[0], ys[1], 0, false);
