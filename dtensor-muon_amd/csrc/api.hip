@@ -133,6 +133,13 @@ class Timed {
 static const int64_t PAD = 256;
 static const int64_t SHORT_ROWS = 64;
 static const int64_t SHORT_PART_BYTES = 3 * 1024 * 4;
+// Extra row pitch of the 256-row iterates wider than 4096 columns, in elements (128 bytes
+// in bf16): with rows of a 4096 x 14336 iterate 28 KB apart B X ran 2.3-2.7% and X X^T
+// 1.5-1.9% slower than with 128 more bytes per row (the Llama step 397.3 against 389.5 ms),
+// measured in alternation on one box; at 4096 columns the padding changed nothing and at
+// 2048 (the MoE experts) X X^T lost 2%.
+static const int64_t X_PITCH_PAD = 64;
+static const int64_t X_PITCH_PAD_FROM = 4096;
 
 OrthLayout muon_orth_layout(int dtype, int64_t batch, int64_t rows, int64_t cols) {
   OrthLayout L;
@@ -145,6 +152,7 @@ OrthLayout muon_orth_layout(int dtype, int64_t batch, int64_t rows, int64_t cols
   L.short_m = dtype == MUON_DT_BF16 && L.m <= SHORT_ROWS;
   L.m_pad = L.short_m ? SHORT_ROWS : round_up(std::max<int64_t>(L.m, 1), PAD);
   L.n_pad = round_up(std::max<int64_t>(L.n, 1), PAD);
+  L.x_pitch = !L.short_m && L.n_pad > X_PITCH_PAD_FROM ? L.n_pad + X_PITCH_PAD : L.n_pad;
   L.es = dtype == MUON_DT_F32 ? 4 : 2;
   L.batch = batch;
   L.parts = (L.m_pad / 64) * (L.n_pad / 64);
@@ -155,7 +163,7 @@ OrthLayout muon_orth_layout(int dtype, int64_t batch, int64_t rows, int64_t cols
     off = (size_t)round_up((int64_t)(off + bytes), 256);
     return o;
   };
-  const size_t xs = (size_t)(batch * L.m_pad * L.n_pad * L.es);
+  const size_t xs = (size_t)(batch * L.m_pad * L.x_pitch * L.es);
   const size_t as = (size_t)(batch * L.m_pad * L.m_pad * L.es);
   L.off_x0 = take(xs);
   L.off_x1 = take(xs);
@@ -278,8 +286,8 @@ int muon_orth_result(int dtype, int64_t batch, int64_t rows, int64_t cols, int s
   // The iterate after `steps` GEMMs (or the scaled input for steps == 0) is in
   // X[steps % 2], in the wide orientation; a tall matrix's result is its transpose.
   *offset_bytes = (int64_t)((steps % 2) ? L.off_x1 : L.off_x0);
-  *row_pitch = L.n_pad;
-  *matrix_stride = L.m_pad * L.n_pad;
+  *row_pitch = L.x_pitch;
+  *matrix_stride = L.m_pad * L.x_pitch;
   *transposed = L.tall;
   return MUON_OK;
 }
@@ -330,7 +338,7 @@ int muon_prepass(int ntensors, void* const* grads, void* const* bufs, int g_dtyp
     int rc = muon_launch_prepass(cnt, grads + t0, bufs ? bufs + t0 : nullptr, g_dtype,
                                  buf_dtype, nb, rows, cols, cols, rows * cols, momentum,
                                  nesterov, maximize, write_back_grad, L.tall ? 0 : 1,
-                                 L.tall ? nullptr : x0, L.n_pad, L.tall ? x0 : nullptr, L, ws,
+                                 L.tall ? nullptr : x0, L.x_pitch, L.tall ? x0 : nullptr, L, ws,
                                  ws_dtype, (int64_t)t0 * nb, s);
     if (rc != MUON_OK) return rc;
   }
@@ -364,7 +372,7 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
   char* X[2] = {w + L.off_x0, w + L.off_x1};
   char* A = w + L.off_a;
   char* B = w + L.off_b;
-  const int64_t mp = L.m_pad, np = L.n_pad;
+  const int64_t mp = L.m_pad, np = L.n_pad, xp = L.x_pitch;
   if (steps == 0) {
     Timed t(MUON_K_OTHER, 0.0, s);
     return muon_launch_scale(L, X[0], ws_dtype, batch, scale, s);
@@ -410,8 +418,8 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
     // A = X X^T (the first iteration folds the Frobenius prescale s in as s^2)
     {
     Timed t(MUON_K_SYRK_XX, bm * md * (md + 1) * nd, s);
-    rc = muon_launch_gemm(ws_dtype, MODE_SYRK, false, batch, mp, mp, np, Xc, np, mp * np, Xc, np,
-                          mp * np, nullptr, 0, 0, A, mp, mp * mp, nullptr, 0, 0, L.m, L.m, 1.0f,
+    rc = muon_launch_gemm(ws_dtype, MODE_SYRK, false, batch, mp, mp, np, Xc, xp, mp * xp, Xc, xp,
+                          mp * xp, nullptr, 0, 0, A, mp, mp * mp, nullptr, 0, 0, L.m, L.m, 1.0f,
                           0.0f, scale, first ? 2 : 0, s);
     }
     if (rc != MUON_OK) return rc;
@@ -427,8 +435,8 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
     // result stays in the wide orientation (readers of a tall result transpose on load)
     {
     Timed t(MUON_K_GEMM_BX, bm * 2.0 * md * md * nd, s);
-    rc = muon_launch_gemm(ws_dtype, MODE_GEMM, false, batch, mp, np, kq, B, mp, mp * mp, Xc, np,
-                          mp * np, Xc, np, mp * np, Xn, np, mp * np, nullptr, 0, 0, L.m, L.n,
+    rc = muon_launch_gemm(ws_dtype, MODE_GEMM, false, batch, mp, np, kq, B, mp, mp * mp, Xc, xp,
+                          mp * xp, Xc, xp, mp * xp, Xn, xp, mp * xp, nullptr, 0, 0, L.m, L.n,
                           1.0f, a, scale, first ? 1 : 0, s);
     }
     if (rc != MUON_OK) return rc;
@@ -698,8 +706,8 @@ int muon_lp_prepass(int ntensors, void* const* grads, int g_dtype, void* const* 
   // general path: the stored-layout X goes to X0 (wide) or, for a tall matrix, to X1
   // (n_pad x m_pad) from where the second pass below transposes it into X0
   char* direct = w + (L.tall ? L.off_x1 : L.off_x0);
-  const int64_t d_pitch = L.tall ? L.m_pad : L.n_pad;
-  const int64_t mst = L.m_pad * L.n_pad;
+  const int64_t d_pitch = L.tall ? L.m_pad : L.x_pitch;
+  const int64_t mst = L.m_pad * (L.tall ? L.n_pad : L.x_pitch);
   {
   const double ges = g_dtype == MUON_DT_F32 ? 4.0 : 2.0;
   const double code_b = qformat == MUON_Q_4BIT ? 0.5 : 1.0;
@@ -725,7 +733,7 @@ int muon_lp_prepass(int ntensors, void* const* grads, int g_dtype, void* const* 
     for (int i = 0; i < cnt; ++i) srcs[i] = direct + (m0 + i) * mst * L.es;
     rc = muon_launch_prepass(cnt, srcs, nullptr, MUON_DT_BF16, MUON_DT_BF16, 1, rows, cols,
                              d_pitch, mst, 0.0f, 0, 0, 0, L.tall ? 0 : 2, L.tall ? nullptr : x0,
-                             L.n_pad, L.tall ? x0 : nullptr, L, ws, ws_dtype, m0, s);
+                             L.x_pitch, L.tall ? x0 : nullptr, L, ws, ws_dtype, m0, s);
     if (rc != MUON_OK) return rc;
   }
   return MUON_OK;

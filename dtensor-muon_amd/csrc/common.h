@@ -233,7 +233,8 @@ void muon_set_error(const char* fmt, ...);
   } while (0)
 
 // Workspace layout shared by the prepass, iteration and postpass entry points.
-// X0/X1: the wide iterate (m_pad x n_pad, row-major), ping-ponged by the GEMM; the
+// X0/X1: the wide iterate (m_pad x n_pad in rows of x_pitch elements), ping-ponged by
+// the GEMM; the
 // result of a tall matrix is written transposed (n_pad x m_pad) into one of them.
 // A bf16 iterate with at most 64 rows (short) is padded to 64 rows, not 256, and its
 // iterations run in short.hip with Gram partials per column range (off_gpart).
@@ -241,6 +242,7 @@ struct OrthLayout {
   int64_t rows, cols;  // stored (param) matrix shape
   int64_t m, n;        // m = min, n = max: the iteration runs on the wide m x n matrix
   int64_t m_pad, n_pad;
+  int64_t x_pitch;     // row pitch of X0/X1 in elements: n_pad (+ 64 beyond 4096 columns)
   int tall;            // rows > cols: stored layout is the transpose of X
   int short_m;         // bf16 and m <= 64: short.hip iterations
   int es;              // element size of the iteration dtype

@@ -884,12 +884,12 @@ int muon_launch_prepass(int ntensors, void* const* grads, void* const* bufs, int
   char* w = (char*)ws;
   const int64_t rows_pad = L.tall ? L.n_pad : L.m_pad;
   const int64_t cols_pad = L.tall ? L.m_pad : L.n_pad;
-  const int64_t mst = L.m_pad * L.n_pad;
+  const int64_t mst = L.m_pad * L.x_pitch;  // X0's matrix stride
   a.direct = direct ? (char*)direct + mat0 * mst * L.es : nullptr;
   a.trans = trans ? (char*)trans + mat0 * mst * L.es : nullptr;
   if (write_direct && !direct) write_direct = 0;
   a.d_pitch = d_pitch;
-  a.t_pitch = rows_pad;
+  a.t_pitch = L.x_pitch;  // a transposed (tall) matrix's rows in X0
   a.d_mstride = mst;
   a.t_mstride = mst;
   a.partials = (float*)(w + L.off_part) + mat0 * L.parts;
@@ -977,7 +977,7 @@ int muon_launch_finalize(const OrthLayout& L, void* ws, int64_t batch, float pre
 
 int muon_launch_scale(const OrthLayout& L, void* x, int wdt, int64_t batch, const float* scale,
                       hipStream_t s) {
-  const int64_t mst = L.m_pad * L.n_pad;
+  const int64_t mst = L.m_pad * L.x_pitch;
   dim3 grid((unsigned)std::min<int64_t>((mst + 255) / 256, 4096), (unsigned)batch);
   if (wdt == MUON_DT_BF16)
     hipLaunchKernelGGL((scale_kernel<MUON_DT_BF16>), grid, dim3(256), 0, s, x, mst, scale);

@@ -975,9 +975,9 @@ int muon_launch_lp_prepass_tiled(int ntensors, void* const* grads, int gdt, void
   a.rows = rows;
   a.cols = cols;
   a.block_shift = shift;
-  const int64_t mst = L.m_pad * L.n_pad;
+  const int64_t mst = L.m_pad * L.x_pitch;
   a.x0 = (char*)ws + L.off_x0 + mat0 * mst * 2;
-  a.x_pitch = L.n_pad;
+  a.x_pitch = L.x_pitch;
   a.x_mstride = mst;
   a.partials = (float*)((char*)ws + L.off_part) + mat0 * L.parts;
   a.parts = L.parts;

@@ -71,9 +71,9 @@ def test_short_workspace_pads_rows_to_64():
         assert (off.value, pitch.value, mst.value, trans.value) == (rup(x), 70144, 64 * 70144, t)
     # 65 rows, or an fp32 iteration, keep the 256-row tiles
     assert lib.muon_orth_result(_lib.DT_BF16, 1, 65, 512, 1, off, pitch, mst, trans) == 0
-    assert mst.value == 256 * 512
+    assert (pitch.value, mst.value) == (512, 256 * 512)
     assert lib.muon_orth_result(_lib.DT_F32, 1, 64, 512, 1, off, pitch, mst, trans) == 0
-    assert mst.value == 256 * 512
+    assert (pitch.value, mst.value) == (512, 256 * 512)
 
 
 def test_result_location_follows_orientation():
@@ -90,6 +90,15 @@ def test_result_location_follows_orientation():
         assert (off.value, pitch.value, trans.value) == (0, 512, t)
         assert lib.muon_orth_result(_lib.DT_BF16, 4, rows, cols, 0, off, pitch, mst, trans) == 0
         assert (off.value, trans.value) == (0, t)
+    # iterates wider than 4096 columns get rows of n_pad + 64 elements (128 more bytes in
+    # bf16), in both orientations and in the workspace size
+    for rows, cols in ((300, 14336), (14336, 300)):  # m_pad 512, n_pad 14336
+        assert lib.muon_orth_result(_lib.DT_BF16, 2, rows, cols, 1, off, pitch, mst, trans) == 0
+        assert (off.value, pitch.value, mst.value) == (2 * 512 * 14400 * 2, 14400, 512 * 14400)
+    nb = lib.muon_orth_workspace_bytes(_lib.DT_BF16, 2, 300, 14336)
+    # X0, X1 with the wider rows, A, B, partials over n_pad (not the pitch), ...
+    assert nb == (2 * (2 * 512 * 14400 * 2) + 2 * (2 * 512 * 512 * 2) + 2 * (512 // 64) * (14336 // 64) * 4
+                  + 256 + 16384 + 1280 + 2 * 14336 * 4)
 
 
 @pytest.mark.parametrize(

@@ -5,6 +5,7 @@ and through the fused dequant -> momentum -> requant pre-pass); dequantization i
 exact; the full MuonLP step matches the oracle's arithmetic given the same U.
 """
 
+import ctypes
 import math
 
 import numpy as np
@@ -239,7 +240,14 @@ def _check_tiled_prepass(fmt, cls, block, shape, gdtype, g=None, check_partials=
         assert np.array_equal(st.scale.cpu().numpy().view(np.uint32), scales.view(np.uint32))
     m, n = min(rows, cols), max(rows, cols)
     mp, npad = -(-m // 256) * 256, -(-n // 256) * 256
-    X0 = ws[: nb * mp * npad * 2].view(torch.bfloat16).view(nb, mp, npad).float().cpu()
+    # X0 (the iterate before any step) in rows of `pitch` elements: the padding columns
+    # up to n_pad are rewritten to zero, the rest of each row is never read
+    off0, pitch, mst = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    trans = ctypes.c_int()
+    assert lib.muon_orth_result(_lib.DT_BF16, nb, rows, cols, 0, off0, pitch, mst, trans) == 0
+    assert off0.value == 0 and mst.value == mp * pitch.value and pitch.value >= npad
+    X0 = ws[: nb * mst.value * 2].view(torch.bfloat16).view(nb, mp, pitch.value)[:, :, :npad]
+    X0 = X0.float().cpu()
     exp = torch.zeros(nb, mp, npad)
     x = torch.from_numpy(gq).view(nb, rows, cols).bfloat16().float()
     exp[:, :m, :n] = x.transpose(1, 2) if rows > cols else x
@@ -247,7 +255,7 @@ def _check_tiled_prepass(fmt, cls, block, shape, gdtype, g=None, check_partials=
     if not check_partials:
         return
     rup = lambda v: -(-v // 256) * 256
-    off = 2 * rup(nb * mp * npad * 2) + 2 * rup(nb * mp * mp * 2)
+    off = 2 * rup(nb * mst.value * 2) + 2 * rup(nb * mp * mp * 2)
     parts = (mp // 64) * (npad // 64)
     P = ws[off: off + nb * parts * 4].view(torch.float32).view(nb, parts).double().cpu()
     want = (x.double() ** 2).sum(dim=(1, 2))
