@@ -1588,8 +1588,11 @@ MUON_DEVICE void n16_substep_dma(f32x4 (&acc)[8][8], const bf16x8_mfma (&cb)[8],
 // The beta term on the matrix cores: ratio * X(i, j) = sum_k X(k, j) (ratio delta(k, i)), so
 // an MFMA with the substep's X fragment as srcA (k = the substep's 32 rows) and a diagonal
 // fragment as srcB adds it to the accumulators of the two row blocks those rows are. ratio is
-// split into two bf16 parts, hi = RNE(ratio) and lo = RNE(ratio - hi) (16 significant bits),
-// so every product is exact; the accumulators never leave their AGPRs. (A read-modify-write
+// split into two bf16 parts, hi = RNE(ratio) and lo = RNE(ratio - hi): hi + lo carries 16
+// significant bits of the fp32 ratio, so the coefficient applied is a (1 + d) with
+// |d| <= about 2^-17 (plus the fp32 rounding of beta / alpha), far below the bf16 output's
+// resolution; each bf16 x bf16 product is exact in the fp32 accumulator. The accumulators
+// never leave their AGPRs. (A read-modify-write
 // through VGPRs made the compiler move accumulators between AGPRs next to the inline-asm
 // MFMAs, whose latency it does not see, and the moves raced their results: B X then differed
 // by an ulp from run to run.) db[par][part]: lane l (r = l%16, g = l/16) holds B(k, n) for

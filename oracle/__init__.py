@@ -23,9 +23,15 @@ Pinning status (what fixes each function independently of its own formula):
 * ``muon_ref.normuon_normalize`` / ``normuon_update``: invariants of the method
   (Frobenius norm preserved, equal row norms from a zero variance, the EMA's fixed
   point, the same per split_sizes row block) and the known answers of
-  test_algorithms.py:174-259.
+  test_algorithms.py:174-259; ``normuon_update``'s composition (normalize, then cautious
+  wd on the normalized update, then the apply, normuon.py:118-134) by a 3 x 2 case worked
+  by hand, which the other order fails.
 * ``quant_ref``: the quantized-state arithmetic lives in torchao 0.17.0, which is not
   present here; the restatement follows torchao's published algorithm and is pinned
   by brute-force nearest-code search, map structure, round-trip error bounds and
-  torch's own float8_e4m3fn cast. Bit parity with torchao itself is UNPINNED.
+  torch's own float8_e4m3fn cast. ``lp_momentum_step`` (muon.py:45-56 through the
+  quantized state) by hand-worked cases for each format: Nesterov's input from the
+  unquantized m', codes of m' by brute-force nearest code, and the next step starting
+  from the dequantized state, with a block where requantization is lossy so the two
+  readings differ. Bit parity with torchao itself is UNPINNED.
 """

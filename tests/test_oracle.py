@@ -250,6 +250,100 @@ def test_normuon_invariants():
     torch.testing.assert_close(vb, vn, rtol=1e-12, atol=0)
 
 
+def test_normuon_update_known_answer():
+    """NorMuon.update (normuon.py:74-134) on a 3 x 2 case with an identity orthogonalizer,
+    numbers worked by hand. Order fixed by the reference: normalize u, then cautious wd on
+    the normalized u (mask u * p > 0), then p - lr * lr_ratio * u.
+
+    g rows (0.6, 0.8), (3, -4), (7, 0) have norms 1, 5, 7 (||g||_F = sqrt(75)). With
+    momentum 0.5, no Nesterov and a zero buffer, u = buf' = g. beta2 = 0.75 from v = 0:
+    v' = 0.25 * (row mean of u^2) = r^2 / 8 = (0.125, 3.125, 6.125). Dividing by sqrt(v')
+    gives every row norm 2 sqrt(2); rescaling to ||g||_F gives every row norm
+    sqrt(75 / 3) = 5: u_n = (3, 4), (3, -4), (5, 0). With p = (1, -1), (-1, 1), (2, 2)
+    the mask u_n * p > 0 keeps (0, 0) and (2, 0) only: u = (3.1, 4), (3, -4), (5.2, 0);
+    lr_ratio = sqrt(3 / 2), lr 0.1."""
+    g = torch.tensor([[0.6, 0.8], [3.0, -4.0], [7.0, 0.0]])
+    p = torch.tensor([[1.0, -1.0], [-1.0, 1.0], [2.0, 2.0]])
+    hp = dict(lr=0.1, weight_decay=0.1, cautious_wd=True, momentum=0.5, nesterov=False,
+              maximize=False, beta2=0.75)
+    new_p, new_buf, v_new, u = R.normuon_update(
+        p, g, torch.zeros(3, 2), torch.zeros(3, 1), R.lr_ratio((3, 2)), **hp, **_ID)
+    u_expected = torch.tensor([[3.1, 4.0], [3.0, -4.0], [5.2, 0.0]])
+    torch.testing.assert_close(u, u_expected, rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(v_new, torch.tensor([[0.125], [3.125], [6.125]]), rtol=1e-7, atol=0)
+    torch.testing.assert_close(new_buf, g, rtol=0, atol=0)
+    p_expected = p - 0.1 * math.sqrt(1.5) * u_expected
+    torch.testing.assert_close(new_p, p_expected, rtol=1e-6, atol=1e-6)
+    # the other composition order (wd on the raw update, then normalize) lands elsewhere
+    raw = g + 0.1 * p * (g * p > 0)
+    wrong, _ = R.normuon_normalize(raw, torch.zeros(3, 1), 0.75)
+    assert (wrong - u_expected).abs().max() > 1e-2
+
+
+def _lp_case(fmt):
+    qmap = {"8bit": Q.qmap_8bit(), "4bit": Q.qmap_4bit(), "fp8": None}[fmt]
+    block = 4
+    # c and c / 3 in one block: c / 3 divided by the block scale c is 1/3, which no map
+    # entry and no e4m3 value holds, so requantization is lossy there
+    c = np.float32(1.5)
+    g = np.array([c, c / np.float32(3.0), -0.25, 0.0625, c / np.float32(3.0), -c, 0.75, 0.1],
+                 dtype=np.float32)
+    ncodes = g.size // 2 if fmt == "4bit" else g.size
+    codes0 = np.zeros(ncodes, np.uint8)     # torchao zeros(): codes 0, scales 0 -> m = 0
+    scales0 = np.zeros(g.size // block, np.float32)
+    return qmap, block, g, codes0, scales0
+
+
+def _lookup(codes, fmt, qmap):
+    """Code -> value by the format's definition, independently of quant_ref.dequantize."""
+    if fmt == "fp8":
+        return torch.from_numpy(codes.copy()).view(torch.float8_e4m3fn).float().numpy()
+    if fmt == "4bit":
+        codes = np.stack([codes >> 4, codes & 0xF], axis=-1).reshape(-1)
+    return np.array([qmap[int(k)] for k in codes], np.float32)
+
+
+@pytest.mark.parametrize("fmt", ["8bit", "4bit", "fp8"])
+def test_lp_momentum_step_known_answer(fmt):
+    """MuonLP's momentum on a quantized buffer (muon.py:45-56 through the quantized
+    state): m = dequant(state); m' = m mu + g; the state stores quant(m'); Nesterov's g'
+    is built from the unquantized fp32 m'; the next step starts from dequant(quant(m')).
+    Expected values are worked out here by hand and by brute-force nearest code, not by
+    calling quant_ref.quantize / dequantize."""
+    qmap, block, g, codes0, scales0 = _lp_case(fmt)
+    mu = 0.9
+    c1, s1, gq = Q.lp_momentum_step(codes0, scales0, g, block=block, fmt=fmt, qmap=qmap,
+                                    momentum=mu, nesterov=True, maximize=False)
+    # from m = 0, m' = g exactly; g' = g + mu g, in fp32
+    m1 = g
+    expect_gq = (g + (m1 * np.float32(mu)).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(gq, expect_gq)
+    # block scales: absmax (divided by 448 for fp8)
+    amax = np.abs(m1.reshape(-1, block)).max(1).astype(np.float32)
+    assert np.array_equal(s1, amax / np.float32(448.0) if fmt == "fp8" else amax)
+    # codes: the nearest representable value of m' / scale, ties up (brute force)
+    y = (m1.reshape(-1, block) / s1[:, None]).astype(np.float32).reshape(-1)
+    if fmt == "fp8":
+        expect_vals = torch.from_numpy(y.copy()).to(torch.float8_e4m3fn).float().numpy()
+    else:
+        d = np.abs(qmap[None, :].astype(np.float64) - y[:, None].astype(np.float64))
+        best = d.min(1, keepdims=True)
+        expect_vals = np.array([qmap[np.nonzero(row == b)[0].max()] for row, b in zip(d, best[:, 0])],
+                               np.float32)
+    assert np.array_equal(_lookup(c1, fmt, qmap), expect_vals)
+    # the stored momentum is lossy at c / 3: a g' built from it would differ from the
+    # one above, so the test tells the two Nesterov inputs apart
+    stored = (_lookup(c1, fmt, qmap).reshape(-1, block) * s1[:, None]).astype(np.float32).reshape(-1)
+    assert stored[1] != m1[1]
+    wrong_gq = (g + (stored * np.float32(mu)).astype(np.float32)).astype(np.float32)
+    assert not np.array_equal(gq, wrong_gq)
+    # step 2 starts from the dequantized state: with g = 0 and no Nesterov, g' = m mu
+    _, _, gq2 = Q.lp_momentum_step(c1, s1, np.zeros_like(g), block=block, fmt=fmt, qmap=qmap,
+                                   momentum=mu, nesterov=False, maximize=False)
+    assert np.array_equal(gq2, ((stored * np.float32(mu)).astype(np.float32) + np.float32(0)).astype(np.float32))
+    assert not np.array_equal(gq2, (m1 * np.float32(mu)).astype(np.float32))
+
+
 # ---- quantizers -----------------------------------------------------------------------------
 
 
