@@ -204,6 +204,70 @@ def test_lp_deferred_scale_prepass_outputs_exact(fmt, cls, block, shape, gdtype)
     _check_tiled_prepass(fmt, cls, block, shape, gdtype)
 
 
+@pytest.mark.parametrize("fmt,cls,block,shape", [
+    ("8bit", OptimState8bit, 2048, (256, 768)), ("4bit", OptimState4bit, 2048, (768, 256)),
+    ("fp8", OptimStateFp8, 2048, (256, 768)), ("fp8", OptimStateFp8, "numel", (768, 256)),
+    ("8bit", OptimState8bit, 256, (768, 256))])
+def test_lp_prepass_bucket_spanning_two_chunks(fmt, cls, block, shape):
+    """A foreach bucket of 34 same-shape tensors in one muon_lp_prepass call: more than
+    MUON_MAX_TENSORS (32), so the library launches two chunks (32 + 2), each with its own
+    per-tensor block-max slots, old-scale slots and requant grid on the deferred-scale path
+    (blocks of 2048 and one per tensor). Every tensor's codes, scales and X0 bit-exact
+    against the oracle over two steps, wide and tall."""
+    from muonium_amd import _lib
+
+    lib = _lib.load()
+    dev = torch.device(DEV)
+    _lib.ensure_device(dev)
+    nt = 34
+    rows, cols = shape
+    numel = rows * cols
+    block = numel if block == "numel" else block
+    gen = torch.Generator().manual_seed(21)
+    # per-tensor scales spread over 2^-20 .. 2^20, so a tensor's codes depend on using its
+    # own block maxima, and per-row log-normal scales inside each tensor
+    gs = [(torch.randn(shape, generator=gen) * torch.exp(torch.randn(rows, 1, generator=gen))
+           * 2.0 ** (t * 40 / (nt - 1) - 20)).bfloat16() for t in range(nt)]
+    sts = [_state(cls, shape, block) for _ in range(nt)]
+    ref = [(np.zeros(st.codes.numel(), np.uint8), np.zeros(st.scale.numel(), np.float32))
+           for st in sts]
+    nbytes = lib.muon_orth_workspace_bytes(_lib.DT_BF16, nt, rows, cols)
+    ws = torch.full((nbytes,), 0x7F, dtype=torch.uint8, device=dev)
+    gds = [g.to(dev) for g in gs]
+    qmap = sts[0].qmap
+    for step in range(2):
+        rc = lib.muon_lp_prepass(nt, _lib.ptr_array(gds), _lib.DT_BF16,
+                                 _lib.ptr_array([st.codes for st in sts]),
+                                 _lib.ptr_array([st.scale for st in sts]),
+                                 qmap.data_ptr() if qmap is not None else None, sts[0].qformat,
+                                 block, 1, rows, cols, 0.9, 1, 0, ws.data_ptr(), _lib.DT_BF16, nt,
+                                 _lib.stream(dev))
+        assert rc == 0, _lib.last_error()
+        torch.cuda.synchronize()
+        gqs = []
+        for t in range(nt):
+            c, s, gq = quant_ref.lp_momentum_step(
+                ref[t][0], ref[t][1], gs[t].float().numpy(), block=block, fmt=fmt,
+                qmap=_qmap(fmt), momentum=0.9, nesterov=True, maximize=False)
+            ref[t] = (c, s)
+            gqs.append(gq)
+            assert np.array_equal(sts[t].codes.cpu().numpy(), c), f"tensor {t} codes, step {step}"
+            assert np.array_equal(sts[t].scale.cpu().numpy().view(np.uint32), s.view(np.uint32)), \
+                f"tensor {t} scales, step {step}"
+    m, n = min(rows, cols), max(rows, cols)
+    mp, npad = -(-m // 256) * 256, -(-n // 256) * 256
+    off0, pitch, mst = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    trans = ctypes.c_int()
+    assert lib.muon_orth_result(_lib.DT_BF16, nt, rows, cols, 0, off0, pitch, mst, trans) == 0
+    X0 = ws[: nt * mst.value * 2].view(torch.bfloat16).view(nt, mp, pitch.value)[:, :, :npad]
+    X0 = X0.float().cpu()
+    for t in range(nt):
+        x = torch.from_numpy(gqs[t]).view(rows, cols).bfloat16().float()
+        exp = torch.zeros(mp, npad)
+        exp[:m, :n] = x.T if rows > cols else x
+        assert torch.equal(X0[t], exp), f"tensor {t}: X0 differs"
+
+
 def _check_tiled_prepass(fmt, cls, block, shape, gdtype, g=None, check_partials=True):
     from muonium_amd import _lib
 

@@ -65,8 +65,11 @@ def test_bf16_iteration_matches_oracle(shape, steps, strategy):
 
 
 @pytest.mark.parametrize("strategy", STRATS)
+# (320, 4608) and its transpose: more than 4096 columns, so the iterate rows carry the
+# padded pitch (n_pad + 64 elements) through the fp32 products, the scale and the extract
 @pytest.mark.parametrize("shape", [(4, 256, 128), (128, 256), (3, 130, 70), (2, 512, 512),
-                                   (300, 300), (1, 1024, 1024), (2, 768, 2304)])
+                                   (300, 300), (1, 1024, 1024), (2, 768, 2304), (320, 4608),
+                                   (4608, 320)])
 @pytest.mark.parametrize("seed", [1, 2])
 def test_fp32_iteration_matches_oracle(shape, strategy, seed):
     X = _inputs(shape, seed=seed)
