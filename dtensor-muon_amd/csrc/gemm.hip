@@ -1879,29 +1879,48 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g) {
   [vo##N] "v"(vo##N), [rs##N] "s"(rs##N), [so##N] "s"(so##N), [mz##N] "s"(mz##N)
 // One block of a 32-k substep: the 8 MFMAs of a fragment FI (accumulators acc[0..7]) with
 // the reads of the next substep's a fragment FI (aa + 2 KB FI) and b fragments 2 FI and
-// 2 FI + 1 (ba + 2 KB (2 FI), + 2 KB (2 FI + 1)).
-template <int FI>
+// 2 FI + 1 (ba + 2 KB (2 FI), + 2 KB (2 FI + 1)). MODE (diagonal tiles, below): 0 all 8
+// column blocks; 1 column blocks 4-7 only (the same reads); 2 no MFMAs and no reads.
+template <int FI, int MODE = 0>
 MUON_DEVICE void s16_block(f32x4 (&acc)[8], const bf16x8_mfma& ca, const bf16x8_mfma (&cb)[8],
                            bf16x8_mfma& na, bf16x8_mfma& nb0, bf16x8_mfma& nb1, uint32_t aa,
                            uint32_t ba) {
-  asm volatile(S16_RA S16(c0, b0) S16(c1, b1) S16(c2, b2)
-               S16_RB0 S16(c3, b3) S16(c4, b4) S16(c5, b5)
-               S16_RB1 S16(c6, b6) S16(c7, b7)
-               : S16_OUT
-               : S16_IN);
+  if constexpr (MODE == 0)
+    asm volatile(S16_RA S16(c0, b0) S16(c1, b1) S16(c2, b2)
+                 S16_RB0 S16(c3, b3) S16(c4, b4) S16(c5, b5)
+                 S16_RB1 S16(c6, b6) S16(c7, b7)
+                 : S16_OUT
+                 : S16_IN);
+  else if constexpr (MODE == 1)
+    asm volatile(S16_RA S16(c4, b4) S16_RB0 S16(c5, b5) S16_RB1 S16(c6, b6) S16(c7, b7)
+                 : S16_OUT
+                 : S16_IN);
 }
-// The same with two loads of a K-tile's DMA, each after an MFMA that follows its M0 write.
-template <int FI>
+// The same with two loads of a K-tile's DMA, each after an MFMA that follows its M0 write
+// (MODE 2: the loads alone, each one wait state after its M0 write).
+template <int FI, int MODE = 0>
 MUON_DEVICE void s16_block_dma(f32x4 (&acc)[8], const bf16x8_mfma& ca, const bf16x8_mfma (&cb)[8],
                                bf16x8_mfma& na, bf16x8_mfma& nb0, bf16x8_mfma& nb1, uint32_t aa,
                                uint32_t ba, int vo0, u32x4 rs0, int so0, uint32_t mz0, int vo1,
                                u32x4 rs1, int so1, uint32_t mz1) {
-  asm volatile(S16_M0(0) S16_RA S16(c0, b0) S16_DL(0) S16(c1, b1) S16_M0(1) S16(c2, b2)
-               S16_RB0 S16(c3, b3) S16_DL(1) S16(c4, b4) S16(c5, b5)
-               S16_RB1 S16(c6, b6) S16(c7, b7)
-               : S16_OUT
-               : S16_IN, S16_LD(0), S16_LD(1)
-               : "m0", "memory");
+  if constexpr (MODE == 0)
+    asm volatile(S16_M0(0) S16_RA S16(c0, b0) S16_DL(0) S16(c1, b1) S16_M0(1) S16(c2, b2)
+                 S16_RB0 S16(c3, b3) S16_DL(1) S16(c4, b4) S16(c5, b5)
+                 S16_RB1 S16(c6, b6) S16(c7, b7)
+                 : S16_OUT
+                 : S16_IN, S16_LD(0), S16_LD(1)
+                 : "m0", "memory");
+  else if constexpr (MODE == 1)
+    asm volatile(S16_M0(0) S16_RA S16(c4, b4) S16_DL(0) S16_M0(1) S16_RB0 S16(c5, b5)
+                 S16_DL(1) S16_RB1 S16(c6, b6) S16(c7, b7)
+                 : S16_OUT
+                 : S16_IN, S16_LD(0), S16_LD(1)
+                 : "m0", "memory");
+  else
+    asm volatile(S16_M0(0) "s_nop 0\n\t" S16_DL(0) S16_M0(1) "s_nop 0\n\t" S16_DL(1)
+                 :
+                 : S16_LD(0), S16_LD(1)
+                 : "m0", "memory");
 }
 #undef S16
 #undef S16_OUT
@@ -1916,31 +1935,39 @@ MUON_DEVICE void s16_block_dma(f32x4 (&acc)[8], const bf16x8_mfma& ca, const bf1
 typedef bf16x8_mfma s16_frags[12];  // a fragments 0-3, b fragments 0-7
 
 // One substep without DMA, then the wait for its 12 reads.
+template <int MODE = 0>
 MUON_DEVICE void s16_substep(f32x4 (&acc)[4][8], const s16_frags& c, s16_frags& n, uint32_t aa,
                              uint32_t ba) {
   const bf16x8_mfma(&cb)[8] = *(const bf16x8_mfma(*)[8]) & c[4];
-  s16_block<0>(acc[0], c[0], cb, n[0], n[4], n[5], aa, ba);
-  s16_block<1>(acc[1], c[1], cb, n[1], n[6], n[7], aa, ba);
-  s16_block<2>(acc[2], c[2], cb, n[2], n[8], n[9], aa, ba);
-  s16_block<3>(acc[3], c[3], cb, n[3], n[10], n[11], aa, ba);
+  s16_block<0, MODE>(acc[0], c[0], cb, n[0], n[4], n[5], aa, ba);
+  s16_block<1, MODE>(acc[1], c[1], cb, n[1], n[6], n[7], aa, ba);
+  s16_block<2, MODE>(acc[2], c[2], cb, n[2], n[8], n[9], aa, ba);
+  s16_block<3, MODE>(acc[3], c[3], cb, n[3], n[10], n[11], aa, ba);
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
 // One substep with the DMA of one K-tile into one stage: this wave's slabs q = 0..3 of the a
 // panel (scalar offsets soa + q sta, M0 ma + 8 KB q) and of the b panel (sob + q stb, mb +
-// 8 KB q), two after each block. A slab is the wave's 1 KB of 8 panel rows.
+// 8 KB q), two after each block. A slab is the wave's 1 KB of 8 panel rows. DIAG (a diagonal
+// tile, whose b panel is its a panel): the a panel only.
+template <int MODE = 0, bool DIAG = false>
 MUON_DEVICE void s16_substep_dma(f32x4 (&acc)[4][8], const s16_frags& c, s16_frags& n, uint32_t aa,
                                  uint32_t ba, int voa, int vob, u32x4 rsa, u32x4 rsb, int soa,
                                  int sta, int sob, int stb, uint32_t ma, uint32_t mb) {
   const bf16x8_mfma(&cb)[8] = *(const bf16x8_mfma(*)[8]) & c[4];
-  s16_block_dma<0>(acc[0], c[0], cb, n[0], n[4], n[5], aa, ba, voa, rsa, soa, ma, voa, rsa,
-                      soa + sta, ma + 0x2000);
-  s16_block_dma<1>(acc[1], c[1], cb, n[1], n[6], n[7], aa, ba, voa, rsa, soa + 2 * sta,
-                      ma + 0x4000, voa, rsa, soa + 3 * sta, ma + 0x6000);
-  s16_block_dma<2>(acc[2], c[2], cb, n[2], n[8], n[9], aa, ba, vob, rsb, sob, mb, vob, rsb,
-                      sob + stb, mb + 0x2000);
-  s16_block_dma<3>(acc[3], c[3], cb, n[3], n[10], n[11], aa, ba, vob, rsb, sob + 2 * stb,
-                      mb + 0x4000, vob, rsb, sob + 3 * stb, mb + 0x6000);
+  s16_block_dma<0, MODE>(acc[0], c[0], cb, n[0], n[4], n[5], aa, ba, voa, rsa, soa, ma, voa, rsa,
+                         soa + sta, ma + 0x2000);
+  s16_block_dma<1, MODE>(acc[1], c[1], cb, n[1], n[6], n[7], aa, ba, voa, rsa, soa + 2 * sta,
+                         ma + 0x4000, voa, rsa, soa + 3 * sta, ma + 0x6000);
+  if constexpr (DIAG) {
+    s16_block<2, MODE>(acc[2], c[2], cb, n[2], n[8], n[9], aa, ba);
+    s16_block<3, MODE>(acc[3], c[3], cb, n[3], n[10], n[11], aa, ba);
+  } else {
+    s16_block_dma<2, MODE>(acc[2], c[2], cb, n[2], n[8], n[9], aa, ba, vob, rsb, sob, mb, vob,
+                           rsb, sob + stb, mb + 0x2000);
+    s16_block_dma<3, MODE>(acc[3], c[3], cb, n[3], n[10], n[11], aa, ba, vob, rsb,
+                           sob + 2 * stb, mb + 0x4000, vob, rsb, sob + 3 * stb, mb + 0x6000);
+  }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
@@ -1994,7 +2021,18 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_s16_kernel(GemmArgs g) {
   const int64_t arow0 = (int64_t)tm * 256, brow0 = (int64_t)tn * 256;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  // A diagonal tile (tm == tn) stores only its upper triangle, 10 of its 16 64 x 64 units.
+  // Its waves take the 64 x 128 blocks in another order, so that each SIMD's two waves
+  // (waves w and w + 4 share a SIMD) carry 3, 3, 2 and 2 of those units instead of 2, 4, 1
+  // and 3: waves 0-3 compute blocks (0, 0), (0, 1), (1, 1), (2, 1) whole (MFMA mode 0),
+  // waves 4 and 5 blocks (1, 0) and (3, 1), of which only column blocks 4-7 reach the upper
+  // triangle (mode 1), waves 6 and 7 blocks (2, 0) and (3, 0), wholly below it (mode 2: no
+  // MFMAs). The a and b panels of a diagonal tile are the same rows: only the a panel is
+  // loaded, and the b fragments are read from it.
+  const bool diag = tm == tn;
+  const int wm = diag ? (0x32312100 >> (4 * wave)) & 15 : wave >> 1;
+  const int wn = diag ? (0x00101110 >> (4 * wave)) & 15 : wave & 1;
+  const int wmode = diag ? (0x22110000 >> (4 * wave)) & 15 : 0;
   const bf16_t* A = (const bf16_t*)g.a + (int64_t)bidx * g.sa;
   const bf16_t* B = (const bf16_t*)g.b + (int64_t)bidx * g.sb;
   const int lda_b = (int)(g.lda * 2), ldb_b = (int)(g.ldb * 2);
@@ -2020,7 +2058,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_s16_kernel(GemmArgs g) {
   int foff[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) foff[ks] = fr * V2_ROWB + (((ks * 4 + fg) ^ kswz(fr)) << 4);
-  const int abase = wm * WM * V2_ROWB, bbase = V2_TILEB + wn * WN * V2_ROWB;
+  const int abase = wm * WM * V2_ROWB, bbase = (diag ? 0 : V2_TILEB) + wn * WN * V2_ROWB;
 
   float alpha = g.alpha, beta = g.beta;
   if (g.scale_mode != 0) {
@@ -2036,12 +2074,6 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_s16_kernel(GemmArgs g) {
   // K-tile whose k range equals this wave's output rows (WM == BK)
   const int kdiag = ratio != 0.0f ? (int)((arow0 + wm * WM) / V2_BK) : -1;
 
-  f32x4 acc[4][8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
   const int KT = (int)(g.K / V2_BK);
   auto aaddr = [&](int st, int ks) -> uint32_t { return lds0 + st * V2_STAGEB + abase + foff[ks]; };
   auto baddr = [&](int st, int ks) -> uint32_t { return lds0 + st * V2_STAGEB + bbase + foff[ks]; };
@@ -2052,112 +2084,136 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_s16_kernel(GemmArgs g) {
     for (int q = 0; q < 4; ++q) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa_p, (lds_ptr_t)(sa + (q * NW + wave) * 1024), 16,
                                                voa, q * sta + kt * V2_ROWB, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb_p,
-                                               (lds_ptr_t)(sa + V2_TILEB + (q * NW + wave) * 1024),
-                                               16, vob, q * stb + kt * V2_ROWB, 0, 0);
+      if (!diag)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rsb_p, (lds_ptr_t)(sa + V2_TILEB + (q * NW + wave) * 1024), 16, vob,
+            q * stb + kt * V2_ROWB, 0, 0);
     }
   };
-  s16_frags f0, f1;
   issue(0, 0);
   wait_vmcnt0();
   lds_barrier();
   if (KT > 1) issue(1, 1);
-  s16_frag_load(f0, aaddr(0, 0), baddr(0, 0));
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cs = kt & 1;
-    s16_substep(acc, f0, f1, aaddr(cs, 1), baddr(cs, 1));
-    if (kt == kdiag) {
-      // cin(i, j) = b(j, i): row j of the b panel, k offset i - kt*BK (the 4 rows of one
-      // accumulator are 8 contiguous bytes of that row)
-      mfma_to_valu_wait();
-      const uint32_t sb = lds0 + cs * V2_STAGEB + bbase + fr * V2_ROWB + (fg & 1) * 8;
+  // accumulators and fragments are declared per path: nothing of the K loop is live across
+  // the branch on the mode
+  auto kloop = [&](auto mode_c, auto diag_c) {
+    constexpr int MODE = decltype(mode_c)::value;
+    constexpr bool DIAG = decltype(diag_c)::value;
+    f32x4 acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    s16_frags f0, f1;
+    if (MODE != 2) s16_frag_load(f0, aaddr(0, 0), baddr(0, 0));
+    for (int kt = 0; kt < KT; ++kt) {
+      const int cs = kt & 1;
+      s16_substep<MODE>(acc, f0, f1, aaddr(cs, 1), baddr(cs, 1));
+      if (MODE != 2 && kt == kdiag) {
+        // cin(i, j) = b(j, i): row j of the b panel, k offset i - kt*BK (the 4 rows of one
+        // accumulator are 8 contiguous bytes of that row)
+        mfma_to_valu_wait();
+        const uint32_t sb = lds0 + cs * V2_STAGEB + bbase + fr * V2_ROWB + (fg & 1) * 8;
+#pragma unroll
+        for (int fi = 0; fi < 4; ++fi)
+#pragma unroll
+          for (int fj = 0; fj < 8; ++fj) {
+            const u32x2 w = *(const u32x2 __attribute__((address_space(3)))*)(
+                sb + fj * 16 * V2_ROWB + (((2 * fi + (fg >> 1)) ^ kswz(fr)) << 4));
+            acc[fi][fj][0] += ratio * __uint_as_float(w.x << 16);
+            acc[fi][fj][1] += ratio * __uint_as_float(w.x & 0xffff0000u);
+            acc[fi][fj][2] += ratio * __uint_as_float(w.y << 16);
+            acc[fi][fj][3] += ratio * __uint_as_float(w.y & 0xffff0000u);
+          }
+        valu_to_mfma_wait();
+      }
+      wait_vmcnt0();
+      lds_barrier();
+      // K-tile kt + 2 into this K-tile's stage; past the last K-tile the null descriptor
+      // reads no memory
+      const bool more = kt + 2 < KT;
+      const int kb = (kt + 2) * V2_ROWB;
+      const uint32_t ma = m0w + cs * V2_STAGEB;
+      s16_substep_dma<MODE, DIAG>(acc, f1, f0, aaddr(cs ^ 1, 0), baddr(cs ^ 1, 0), voa, vob,
+                                  more ? rsa : rs_none, more ? rsb : rs_none, kb, sta, kb, stb,
+                                  ma, ma + V2_TILEB);
+    }
+    mfma_to_valu_wait();
+    wait_vmcnt0();
+
+    // ---- epilogue: stage through LDS, store 16-byte row chunks ----
+    if (g.out == nullptr) return;
+    bf16_t* T = (bf16_t*)smem;
+    const int row0w = wm * WM, col0w = wn * WN;  // wave origin within the tile
+    uint32_t hv[4][8][2];
+    s16_pack(acc, alpha, arow0 + 256 <= g.Mv && brow0 + 256 <= g.Nv,
+             clamp_rem(g.Mv - (arow0 + row0w + fg * 4)), clamp_rem(g.Nv - (brow0 + col0w + fr)), hv);
+    bf16_t* out = (bf16_t*)g.out + (int64_t)bidx * g.so;
+    if (!diag) {
+      // mirror half of the symmetric output: T[j][i], 4 consecutive i per lane -> one 8-byte
+      // write
+      lds_barrier();
 #pragma unroll
       for (int fi = 0; fi < 4; ++fi)
 #pragma unroll
         for (int fj = 0; fj < 8; ++fj) {
-          const u32x2 w = *(const u32x2 __attribute__((address_space(3)))*)(
-              sb + fj * 16 * V2_ROWB + (((2 * fi + (fg >> 1)) ^ kswz(fr)) << 4));
-          acc[fi][fj][0] += ratio * __uint_as_float(w.x << 16);
-          acc[fi][fj][1] += ratio * __uint_as_float(w.x & 0xffff0000u);
-          acc[fi][fj][2] += ratio * __uint_as_float(w.y << 16);
-          acc[fi][fj][3] += ratio * __uint_as_float(w.y & 0xffff0000u);
+          const int jl = col0w + fj * 16 + fr;
+          const int il = row0w + fi * 16 + fg * 4;
+          *(uint2*)(T + jl * V2_EP_PITCH + il) = make_uint2(hv[fi][fj][0], hv[fi][fj][1]);
         }
-      valu_to_mfma_wait();
+      lds_barrier();
+#pragma unroll 4
+      for (int it = 0; it < 16; ++it) {
+        const int id = it * 512 + tid;
+        const int jl = id >> 5, c = (id & 31) * 8;
+        const uint4 w = *(const uint4*)(T + jl * V2_EP_PITCH + c);
+        *(uint4*)(out + (brow0 + jl) * g.ldo + arow0 + c) = w;
+      }
     }
-    wait_vmcnt0();
-    lds_barrier();
-    // K-tile kt + 2 into this K-tile's stage; past the last K-tile the null descriptor
-    // reads no memory
-    const bool more = kt + 2 < KT;
-    const int kb = (kt + 2) * V2_ROWB;
-    const uint32_t ma = m0w + cs * V2_STAGEB;
-    s16_substep_dma(acc, f1, f0, aaddr(cs ^ 1, 0), baddr(cs ^ 1, 0), voa, vob, more ? rsa : rs_none,
-                    more ? rsb : rs_none, kb, sta, kb, stb, ma, ma + V2_TILEB);
-  }
-  mfma_to_valu_wait();
-  wait_vmcnt0();
-
-  // ---- epilogue: stage through LDS, store 16-byte row chunks ----
-  if (g.out == nullptr) return;
-  bf16_t* T = (bf16_t*)smem;
-  const bool diag = tm == tn;
-  const int row0w = wm * WM, col0w = wn * WN;  // wave origin within the tile
-  uint32_t hv[4][8][2];
-  s16_pack(acc, alpha, arow0 + 256 <= g.Mv && brow0 + 256 <= g.Nv,
-           clamp_rem(g.Mv - (arow0 + row0w + fg * 4)), clamp_rem(g.Nv - (brow0 + col0w + fr)), hv);
-  bf16_t* out = (bf16_t*)g.out + (int64_t)bidx * g.so;
-  if (!diag) {
-    // mirror half of the symmetric output: T[j][i], 4 consecutive i per lane -> one 8-byte
-    // write
+    // row-major stage: T[i][j]
     lds_barrier();
 #pragma unroll
     for (int fi = 0; fi < 4; ++fi)
 #pragma unroll
-      for (int fj = 0; fj < 8; ++fj) {
-        const int jl = col0w + fj * 16 + fr;
-        const int il = row0w + fi * 16 + fg * 4;
-        *(uint2*)(T + jl * V2_EP_PITCH + il) = make_uint2(hv[fi][fj][0], hv[fi][fj][1]);
-      }
+      for (int fj = 0; fj < 8; ++fj)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int il = row0w + fi * 16 + fg * 4 + q;
+          const int jl = col0w + fj * 16 + fr;
+          T[il * V2_EP_PITCH + jl] = (bf16_t)(hv[fi][fj][q >> 1] >> (16 * (q & 1)));
+        }
     lds_barrier();
 #pragma unroll 4
     for (int it = 0; it < 16; ++it) {
       const int id = it * 512 + tid;
-      const int jl = id >> 5, c = (id & 31) * 8;
-      const uint4 w = *(const uint4*)(T + jl * V2_EP_PITCH + c);
-      *(uint4*)(out + (brow0 + jl) * g.ldo + arow0 + c) = w;
-    }
-  }
-  // row-major stage: T[i][j]
-  lds_barrier();
+      const int il = id >> 5, c = (id & 31) * 8;
+      uint4 w;
+      if (!diag || c >= il) {
+        w = *(const uint4*)(T + il * V2_EP_PITCH + c);
+      } else {
+        // diagonal tile, chunk reaching below the diagonal: those columns come from the
+        // computed (upper) element of the mirror position
+        uint16_t e[8];
 #pragma unroll
-  for (int fi = 0; fi < 4; ++fi)
-#pragma unroll
-    for (int fj = 0; fj < 8; ++fj)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int il = row0w + fi * 16 + fg * 4 + q;
-        const int jl = col0w + fj * 16 + fr;
-        T[il * V2_EP_PITCH + jl] = (bf16_t)(hv[fi][fj][q >> 1] >> (16 * (q & 1)));
+        for (int q = 0; q < 8; ++q)
+          e[q] = (c + q < il) ? T[(c + q) * V2_EP_PITCH + il] : T[il * V2_EP_PITCH + c + q];
+        __builtin_memcpy(&w, e, 16);
       }
-  lds_barrier();
-#pragma unroll 4
-  for (int it = 0; it < 16; ++it) {
-    const int id = it * 512 + tid;
-    const int il = id >> 5, c = (id & 31) * 8;
-    uint4 w;
-    if (!diag || c >= il) {
-      w = *(const uint4*)(T + il * V2_EP_PITCH + c);
-    } else {
-      // diagonal tile, chunk reaching below the diagonal: those columns come from the
-      // computed (upper) element of the mirror position
-      uint16_t e[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q)
-        e[q] = (c + q < il) ? T[(c + q) * V2_EP_PITCH + il] : T[il * V2_EP_PITCH + c + q];
-      __builtin_memcpy(&w, e, 16);
+      *(uint4*)(out + (arow0 + il) * g.ldo + brow0 + c) = w;
     }
-    *(uint4*)(out + (arow0 + il) * g.ldo + brow0 + c) = w;
-  }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  // one K loop and epilogue per mode, so no path merges into another's registers
+  if (!diag)
+    kloop(I0{}, std::false_type{});
+  else if (wmode == 0)
+    kloop(I0{}, std::true_type{});
+  else if (wmode == 1)
+    kloop(I1{}, std::true_type{});
+  else
+    kloop(I2{}, std::true_type{});
 }
 
 // Wave grid of the register-staged bf16 kernel (gemm_bf16_kernel), which serves the
