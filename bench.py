@@ -555,16 +555,22 @@ def main() -> None:
     orth_shapes = [(s[0], math.prod(s[1:])) if flatten and len(s) > 2 else s for s in shapes]
     flops_step = sum(orth_flops(s, 5) for s in orth_shapes)
     value = flops_step / (ms_per_step * 1e-3) / 1e12
-    orth_ms = sum(kern[k][0] for k in ("syrk_xx", "syrk_aa", "gemm_bx")) / args.steps
+    # the last B X of each plain-Muon bucket carries the apply (the post-pass fused into its
+    # epilogue, gemm_bx_apply): its whole time is counted as orthogonalization time
+    orth_ms = sum(kern[k][0] for k in ("syrk_xx", "syrk_aa", "gemm_bx", "gemm_bx_apply")) / args.steps
+    apply_fused = kern["gemm_bx_apply"][1] > 0
     kernels = {}
     for k, (ms, n, work) in kern.items():
         if n == 0:
             continue
         entry = {"ms_per_step": round(ms / args.steps, 3), "launches_per_step": n // args.steps,
                  "avg_launch_ms": round(ms / n, 4)}
-        if k in ("syrk_xx", "syrk_aa", "gemm_bx"):
+        if k in ("syrk_xx", "syrk_aa", "gemm_bx", "gemm_bx_apply"):
             tf = work / (ms * 1e-3) / 1e12
             entry.update(tflops=round(tf, 1), frac=round(tf / PEAK_BF16_TFLOPS, 4))
+            if k == "gemm_bx_apply":
+                # the same product plus the apply: each parameter element read and written
+                entry.update(apply_param_bytes_per_elem=2 * pdtype.itemsize)
         elif k in ("prepass", "postpass", "lp_prepass"):
             gbs = work / (ms * 1e-3) / 1e9
             entry.update(gbs=round(gbs, 1), frac=round(gbs / PEAK_HBM_GBS, 4),
@@ -624,7 +630,11 @@ def main() -> None:
     upd_bytes = sum(kern[k][2] for k in ("prepass", "postpass", "lp_prepass")) / args.steps
     # the survey's convention for the fp32-momentum passes: 18 B per bf16 value
     # (pre 12 + post 6), without the pre-pass's write-back of g' into the gradients
-    upd_bytes18 = 18.0 * numel if (not args.lp and pdtype == torch.bfloat16) else None
+    upd_bytes18 = (18.0 * numel if (not args.lp and pdtype == torch.bfloat16 and not apply_fused)
+                   else None)
+    # with the apply fused, the update kernels are the pre-pass alone: 12 B per value at the
+    # survey's convention (without the write-back of g' into the gradients)
+    upd_bytes12 = 12.0 * numel if (apply_fused and not args.lp and pdtype == torch.bfloat16) else None
 
     cpu = None
     # the oracle's per-parameter loop restates the per-matrix problem; it is not run for
@@ -666,6 +676,9 @@ def main() -> None:
         "update_kernel_bytes_per_elem": round(upd_bytes / numel, 3),
         "update_kernel_gbs_18B": (round(upd_bytes18 / (upd_ms * 1e-3) / 1e9, 1)
                                   if upd_ms and upd_bytes18 else None),
+        "update_kernel_gbs_12B": (round(upd_bytes12 / (upd_ms * 1e-3) / 1e9, 1)
+                                  if upd_ms and upd_bytes12 else None),
+        "update_apply_fused_into": "gemm_bx_apply" if apply_fused else None,
         "kernels": kernels,
         "roofline": roofline,
         "cpu_baseline": cpu,

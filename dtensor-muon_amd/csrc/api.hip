@@ -17,6 +17,10 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
                      void* out, int64_t ldo, int64_t so, void* out_t, int64_t ldt, int64_t st,
                      int64_t Mv, int64_t Nv, float alpha, float beta, const float* scale,
                      int scale_mode, hipStream_t stream);
+int muon_launch_gemm_apply(int64_t batch, int64_t M, int64_t N, int64_t K, const void* a,
+                           int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb,
+                           int64_t Mv, int64_t Nv, float alpha, float beta, const float* scale,
+                           int scale_mode, const MuonApply& ap, int tall, hipStream_t stream);
 int muon_launch_prepass(int ntensors, void* const* grads, void* const* bufs, int gdt, int bdt,
                         int64_t nb, int64_t rows, int64_t cols, int64_t s_pitch,
                         int64_t s_mstride, float momentum, int nesterov, int maximize,
@@ -220,7 +224,7 @@ static bool io_dtype_ok(int dt) {
 
 extern "C" {
 
-int muon_amd_abi_version(void) { return 4; }
+int muon_amd_abi_version(void) { return 5; }
 
 const char* muon_amd_last_error(void) { return g_err; }
 
@@ -345,9 +349,11 @@ int muon_prepass(int ntensors, void* const* grads, void* const* bufs, int g_dtyp
   return MUON_OK;
 }
 
-int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64_t rows,
-                  int64_t cols, const double* coeffs, int steps, float prescale, float eps,
-                  void* stream) {
+// The iteration; with `ap` (eligible shapes only, checked by the caller) the last X' is
+// not stored but applied to the parameters in the GEMM's epilogue.
+static int orth_run_impl(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64_t rows,
+                         int64_t cols, const double* coeffs, int steps, float prescale,
+                         float eps, const MuonApply* ap, void* stream) {
   if (!iter_dtype_ok(ws_dtype)) {
     muon_set_error("orth_run: unsupported dtype %d", ws_dtype);
     return MUON_ERR_DTYPE;
@@ -433,7 +439,11 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
     if (rc != MUON_OK) return rc;
     // X' = a*X + B X into the other buffer (every tile reads whole columns of X); the
     // result stays in the wide orientation (readers of a tall result transpose on load)
-    {
+    if (ap && it + 1 == steps) {
+      Timed t(MUON_K_GEMM_BX_APPLY, bm * 2.0 * md * md * nd, s);
+      rc = muon_launch_gemm_apply(batch, mp, np, kq, B, mp, mp * mp, Xc, xp, mp * xp, L.m, L.n,
+                                  1.0f, a, scale, first ? 1 : 0, *ap, L.tall, s);
+    } else {
     Timed t(MUON_K_GEMM_BX, bm * 2.0 * md * md * nd, s);
     rc = muon_launch_gemm(ws_dtype, MODE_GEMM, false, batch, mp, np, kq, B, mp, mp * mp, Xc, xp,
                           mp * xp, Xc, xp, mp * xp, Xn, xp, mp * xp, nullptr, 0, 0, L.m, L.n,
@@ -442,6 +452,49 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
     if (rc != MUON_OK) return rc;
   }
   return MUON_OK;
+}
+
+int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64_t rows,
+                  int64_t cols, const double* coeffs, int steps, float prescale, float eps,
+                  void* stream) {
+  return orth_run_impl(ws, ws_dtype, ws_batch, batch, rows, cols, coeffs, steps, prescale, eps,
+                       nullptr, stream);
+}
+
+int muon_orth_run_apply(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64_t rows,
+                        int64_t cols, const double* coeffs, int steps, float prescale,
+                        float eps, int ntensors, void* const* params, int p_dtype, int64_t nb,
+                        const float* adjusted_lrs, float wd, int cautious, void* stream) {
+  bool fuse = ws_dtype == MUON_DT_BF16 && p_dtype == MUON_DT_BF16 && steps > 0 && rows > 0 &&
+              cols > 0 && nb > 0 && ntensors > 0 && ntensors <= MUON_APPLY_MAX &&
+              (int64_t)ntensors * nb == batch && batch <= ws_batch && params && adjusted_lrs &&
+              cols % 8 == 0;
+  if (fuse) {
+    const OrthLayout L = muon_orth_layout(ws_dtype, ws_batch, rows, cols);
+    const int64_t kq = std::min(L.m_pad, round_up(L.m, 128));
+    fuse = !L.short_m && kq >= 1024;
+    for (int t = 0; fuse && t < ntensors; ++t) fuse = params[t] && !((uintptr_t)params[t] & 15);
+  }
+  if (!fuse) {
+    int rc = muon_orth_run(ws, ws_dtype, ws_batch, batch, rows, cols, coeffs, steps, prescale,
+                           eps, stream);
+    if (rc != MUON_OK) return rc;
+    return muon_postpass(ntensors, params, p_dtype, nullptr, 0, ws, ws_dtype, ws_batch, steps,
+                         nb, rows, cols, adjusted_lrs, nullptr, wd, cautious, stream);
+  }
+  MuonApply ap;
+  memset(&ap, 0, sizeof(ap));
+  for (int t = 0; t < ntensors; ++t) {
+    ap.params[t] = params[t];
+    ap.adj[t] = adjusted_lrs[t];
+  }
+  ap.nb = nb;
+  ap.prows = rows;
+  ap.pcols = cols;
+  ap.wd = wd;
+  ap.cautious = cautious;
+  return orth_run_impl(ws, ws_dtype, ws_batch, batch, rows, cols, coeffs, steps, prescale, eps,
+                       &ap, stream);
 }
 
 int muon_orth_extract(const void* ws, int ws_dtype, int64_t ws_batch, int64_t batch,

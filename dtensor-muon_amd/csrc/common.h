@@ -218,6 +218,41 @@ MUON_DEVICE float warp_max(float v) {
   return v;
 }
 
+// The apply of one element (weight decay, cautious mask, shape-scaled step), shared by the
+// post-pass and the B X epilogue that fuses it.
+// muon.py:62-77 for one element, eager op order, no contraction.
+template <int PDT, int UDT>
+MUON_DEVICE float apply_elem(float p, float u, float wd, int cautious, float adj) {
+#pragma clang fp contract(off)
+  if (wd != 0.0f) {
+    float t = wd * p;
+    if (cautious) {
+      float prod = u * p;
+      float mask = prod > 0.0f ? 1.0f : 0.0f;
+      t = t * mask;
+    }
+    float v = u + t;
+    float step = adj * v;
+    return p - step;
+  }
+  // 0-dim fp32 tensor * u: type promotion keeps u's dtype, so the scalar is cast to
+  // it first and the product is rounded to it (eager torch semantics).
+  float step = Elem<UDT>::round(Elem<UDT>::round(adj) * u);
+  return p - step;
+}
+
+// The apply fused into the last B X of a bucket of bf16 parameters: one entry per tensor
+// (matrices bidx = t nb .. t nb + nb - 1 of the launch are tensor t's), the stored extents of
+// one matrix, and the post-pass's scalars.
+constexpr int MUON_APPLY_MAX = 128;
+struct MuonApply {
+  void* params[MUON_APPLY_MAX];
+  float adj[MUON_APPLY_MAX];  // lr * lr_ratio per tensor
+  int64_t nb, prows, pcols;
+  float wd;
+  int cautious;
+};
+
 static inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 // Thread-local last-error text for muon_amd_last_error().

@@ -385,27 +385,6 @@ struct PostArgs {
   int cautious;
 };
 
-// muon.py:62-77 for one element, eager op order, no contraction.
-template <int PDT, int UDT>
-MUON_DEVICE float apply_elem(float p, float u, float wd, int cautious, float adj) {
-#pragma clang fp contract(off)
-  if (wd != 0.0f) {
-    float t = wd * p;
-    if (cautious) {
-      float prod = u * p;
-      float mask = prod > 0.0f ? 1.0f : 0.0f;
-      t = t * mask;
-    }
-    float v = u + t;
-    float step = adj * v;
-    return p - step;
-  }
-  // 0-dim fp32 tensor * u: type promotion keeps u's dtype, so the scalar is cast to
-  // it first and the product is rounded to it (eager torch semantics).
-  float step = Elem<UDT>::round(Elem<UDT>::round(adj) * u);
-  return p - step;
-}
-
 // TRANS: U is the wide-orientation iterate of a tall matrix, U(r, c) = u[c][r] (the
 // workspace after the iteration); the 64 x 64 block u[c0 .. c0+63][r0 .. r0+63] is read
 // with coalesced 16-byte loads and transposed through LDS. Its extents are padded to a

@@ -20,6 +20,7 @@
 // that are masked to zeros or not stored.
 #include <algorithm>
 #include <atomic>
+#include <cstring>
 #include <mutex>
 #include <type_traits>
 
@@ -1457,46 +1458,60 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn4_kernel(GemmArgs g) {
 // X' rows 16 FI + lane%16, columns 16 fj + 4 (lane/16) .. +3) on the current fragments,
 // with 3 reads of the next substep's fragments: both halves of X fragment FI (tr reads at
 // xa + XO, + 2 KB) and B fragment FI (b128 at ba + 2 KB FI).
-template <int FI, int XO>
+// SW (the last iteration of a tall matrix, whose update is applied in the parameter's
+// layout): the operands swapped, srcA the B fragment and srcB the X fragments, so the
+// accumulators hold X' columns 16 fj + lane%16, rows 16 FI + 4 (lane/16) .. +3, i.e. the
+// transpose of the block within each 16 x 16 accumulator (the same products and sums).
+#define M16S(C, X, B) "v_mfma_f32_16x16x32_bf16 %[" #C "], %[" #B "], %[" #X "], %[" #C "]\n\t"
+#define N16_BLOCK(M)                                                                      \
+  "ds_read_b64_tr_b16 %[nl], %[xa] offset:%[o0]\n\t" M(c0, x0, b)                          \
+  M(c1, x1, b) M(c2, x2, b)                                                               \
+  "ds_read_b64_tr_b16 %[nh], %[xa] offset:%[o1]\n\t" M(c3, x3, b)                          \
+  M(c4, x4, b) M(c5, x5, b)                                                               \
+  "ds_read_b128 %[nb], %[ba] offset:%[ob]\n\t" M(c6, x6, b)                                \
+  M(c7, x7, b)
+template <int FI, int XO, bool SW = false>
 MUON_DEVICE void n16_block(f32x4 (&acc)[8], const bf16x8_mfma& cb, const bf16x8_mfma (&cx)[8],
                            bf16x8_mfma& nb, i16x4& nl, i16x4& nh, uint32_t ba, uint32_t xa) {
-  asm volatile(
-      "ds_read_b64_tr_b16 %[nl], %[xa] offset:%[o0]\n\t" M16(c0, x0, b)
-      M16(c1, x1, b) M16(c2, x2, b)
-      "ds_read_b64_tr_b16 %[nh], %[xa] offset:%[o1]\n\t" M16(c3, x3, b)
-      M16(c4, x4, b) M16(c5, x5, b)
-      "ds_read_b128 %[nb], %[ba] offset:%[ob]\n\t" M16(c6, x6, b)
-      M16(c7, x7, b)
-      : N16_OUT(acc)
-      : N16_IN);
+  if constexpr (SW)
+    asm volatile(N16_BLOCK(M16S) : N16_OUT(acc) : N16_IN);
+  else
+    asm volatile(N16_BLOCK(M16) : N16_OUT(acc) : N16_IN);
 }
 // The same with two loads of the DMA of a K-tile (slabs 2 FI and 2 FI + 1 of the 16 this
 // wave issues per K-tile: B panel slabs for FI < 4, X panel slabs for FI >= 4), each after an
 // MFMA, with per-lane offsets vo0 and vo1. m0 and the scalar offsets of both loads come in
 // precomputed.
-template <int FI, int XO>
+#define N16_BLOCK_DMA(M)                                                                  \
+  "s_mov_b32 m0, %[m00]\n\t"                                                              \
+  "ds_read_b64_tr_b16 %[nl], %[xa] offset:%[o0]\n\t" M(c0, x0, b)                          \
+  "buffer_load_dwordx4 %[vo0], %[rs], %[so0] offen lds\n\t"                               \
+  M(c1, x1, b) "s_mov_b32 m0, %[m01]\n\t" M(c2, x2, b)                                    \
+  "ds_read_b64_tr_b16 %[nh], %[xa] offset:%[o1]\n\t" M(c3, x3, b)                          \
+  "buffer_load_dwordx4 %[vo1], %[rs], %[so1] offen lds\n\t"                               \
+  M(c4, x4, b) M(c5, x5, b)                                                               \
+  "ds_read_b128 %[nb], %[ba] offset:%[ob]\n\t" M(c6, x6, b)                                \
+  M(c7, x7, b)
+#define N16_DMA_IN                                                                        \
+  N16_IN, [vo0] "v"(vo0), [vo1] "v"(vo1), [rs] "s"(rs), [so0] "s"(so0), [so1] "s"(so1),    \
+      [m00] "s"(m00), [m01] "s"(m01)
+template <int FI, int XO, bool SW = false>
 MUON_DEVICE void n16_block_dma(f32x4 (&acc)[8], const bf16x8_mfma& cb, const bf16x8_mfma (&cx)[8],
                                bf16x8_mfma& nb, i16x4& nl, i16x4& nh, uint32_t ba, uint32_t xa,
                                int vo0, int vo1, u32x4 rs, int so0, int so1, uint32_t m00,
                                uint32_t m01) {
-  asm volatile(
-      "s_mov_b32 m0, %[m00]\n\t"
-      "ds_read_b64_tr_b16 %[nl], %[xa] offset:%[o0]\n\t" M16(c0, x0, b)
-      "buffer_load_dwordx4 %[vo0], %[rs], %[so0] offen lds\n\t"
-      M16(c1, x1, b) "s_mov_b32 m0, %[m01]\n\t" M16(c2, x2, b)
-      "ds_read_b64_tr_b16 %[nh], %[xa] offset:%[o1]\n\t" M16(c3, x3, b)
-      "buffer_load_dwordx4 %[vo1], %[rs], %[so1] offen lds\n\t"
-      M16(c4, x4, b) M16(c5, x5, b)
-      "ds_read_b128 %[nb], %[ba] offset:%[ob]\n\t" M16(c6, x6, b)
-      M16(c7, x7, b)
-      : N16_OUT(acc)
-      : N16_IN, [vo0] "v"(vo0), [vo1] "v"(vo1), [rs] "s"(rs), [so0] "s"(so0), [so1] "s"(so1), [m00] "s"(m00),
-        [m01] "s"(m01)
-      : "m0", "memory");
+  if constexpr (SW)
+    asm volatile(N16_BLOCK_DMA(M16S) : N16_OUT(acc) : N16_DMA_IN : "m0", "memory");
+  else
+    asm volatile(N16_BLOCK_DMA(M16) : N16_OUT(acc) : N16_DMA_IN : "m0", "memory");
 }
+#undef N16_BLOCK
+#undef N16_BLOCK_DMA
+#undef N16_DMA_IN
 #undef N16_OUT
 #undef N16_IN
 #undef M16
+#undef M16S
 
 #define DA "buffer_load_dwordx4 %[voa], %[rsa], %[ta] offen lds\n\t"
 #define DXE "buffer_load_dwordx4 %[voxe], %[rsx], %[tx] offen lds\n\t"
@@ -1550,38 +1565,38 @@ MUON_DEVICE void n16_join(bf16x8_mfma (&cx)[8], const i16x4 (&lo)[8], const i16x
 }
 
 // One 32-k substep: 8 blocks, then the wait for its 24 reads.
-template <int XO>
+template <int XO, bool SW = false>
 MUON_DEVICE void n16_substep(f32x4 (&acc)[8][8], const bf16x8_mfma (&cb)[8], const bf16x8_mfma (&cx)[8],
                              bf16x8_mfma (&nb)[8], i16x4 (&nl)[8], i16x4 (&nh)[8], uint32_t ba,
                              const uint32_t (&xa)[8]) {
-  n16_block<0, XO>(acc[0], cb[0], cx, nb[0], nl[0], nh[0], ba, xa[0]);
-  n16_block<1, XO>(acc[1], cb[1], cx, nb[1], nl[1], nh[1], ba, xa[1]);
-  n16_block<2, XO>(acc[2], cb[2], cx, nb[2], nl[2], nh[2], ba, xa[2]);
-  n16_block<3, XO>(acc[3], cb[3], cx, nb[3], nl[3], nh[3], ba, xa[3]);
-  n16_block<4, XO>(acc[4], cb[4], cx, nb[4], nl[4], nh[4], ba, xa[4]);
-  n16_block<5, XO>(acc[5], cb[5], cx, nb[5], nl[5], nh[5], ba, xa[5]);
-  n16_block<6, XO>(acc[6], cb[6], cx, nb[6], nl[6], nh[6], ba, xa[6]);
-  n16_block<7, XO>(acc[7], cb[7], cx, nb[7], nl[7], nh[7], ba, xa[7]);
+  n16_block<0, XO, SW>(acc[0], cb[0], cx, nb[0], nl[0], nh[0], ba, xa[0]);
+  n16_block<1, XO, SW>(acc[1], cb[1], cx, nb[1], nl[1], nh[1], ba, xa[1]);
+  n16_block<2, XO, SW>(acc[2], cb[2], cx, nb[2], nl[2], nh[2], ba, xa[2]);
+  n16_block<3, XO, SW>(acc[3], cb[3], cx, nb[3], nl[3], nh[3], ba, xa[3]);
+  n16_block<4, XO, SW>(acc[4], cb[4], cx, nb[4], nl[4], nh[4], ba, xa[4]);
+  n16_block<5, XO, SW>(acc[5], cb[5], cx, nb[5], nl[5], nh[5], ba, xa[5]);
+  n16_block<6, XO, SW>(acc[6], cb[6], cx, nb[6], nl[6], nh[6], ba, xa[6]);
+  n16_block<7, XO, SW>(acc[7], cb[7], cx, nb[7], nl[7], nh[7], ba, xa[7]);
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
 // The substep after the barrier, carrying the DMA of one whole K-tile into one stage: blocks
 // 0-3 load the B panel slabs (rows 32 q + 8 wave .. +7, q = 0..7), blocks 4-7 the X panel
 // slabs (rows 8 q + 2 wave, +1).
-template <int XO>
+template <int XO, bool SW = false>
 MUON_DEVICE void n16_substep_dma(f32x4 (&acc)[8][8], const bf16x8_mfma (&cb)[8],
                                  const bf16x8_mfma (&cx)[8], bf16x8_mfma (&nb)[8], i16x4 (&nl)[8],
                                  i16x4 (&nh)[8], uint32_t ba, const uint32_t (&xa)[8], int voa,
                                  int voxe, int voxo, u32x4 rsa, u32x4 rsx, int soa, int sox, int sta, int stx,
                                  uint32_t m0a, uint32_t m0x) {
-  n16_block_dma<0, XO>(acc[0], cb[0], cx, nb[0], nl[0], nh[0], ba, xa[0], voa, voa, rsa, soa, soa + sta, m0a, m0a + 0x1000);
-  n16_block_dma<1, XO>(acc[1], cb[1], cx, nb[1], nl[1], nh[1], ba, xa[1], voa, voa, rsa, soa + 2 * sta, soa + 3 * sta, m0a + 0x2000, m0a + 0x3000);
-  n16_block_dma<2, XO>(acc[2], cb[2], cx, nb[2], nl[2], nh[2], ba, xa[2], voa, voa, rsa, soa + 4 * sta, soa + 5 * sta, m0a + 0x4000, m0a + 0x5000);
-  n16_block_dma<3, XO>(acc[3], cb[3], cx, nb[3], nl[3], nh[3], ba, xa[3], voa, voa, rsa, soa + 6 * sta, soa + 7 * sta, m0a + 0x6000, m0a + 0x7000);
-  n16_block_dma<4, XO>(acc[4], cb[4], cx, nb[4], nl[4], nh[4], ba, xa[4], voxe, voxo, rsx, sox, sox + stx, m0x, m0x + 0x1000);
-  n16_block_dma<5, XO>(acc[5], cb[5], cx, nb[5], nl[5], nh[5], ba, xa[5], voxe, voxo, rsx, sox + 2 * stx, sox + 3 * stx, m0x + 0x2000, m0x + 0x3000);
-  n16_block_dma<6, XO>(acc[6], cb[6], cx, nb[6], nl[6], nh[6], ba, xa[6], voxe, voxo, rsx, sox + 4 * stx, sox + 5 * stx, m0x + 0x4000, m0x + 0x5000);
-  n16_block_dma<7, XO>(acc[7], cb[7], cx, nb[7], nl[7], nh[7], ba, xa[7], voxe, voxo, rsx, sox + 6 * stx, sox + 7 * stx, m0x + 0x6000, m0x + 0x7000);
+  n16_block_dma<0, XO, SW>(acc[0], cb[0], cx, nb[0], nl[0], nh[0], ba, xa[0], voa, voa, rsa, soa, soa + sta, m0a, m0a + 0x1000);
+  n16_block_dma<1, XO, SW>(acc[1], cb[1], cx, nb[1], nl[1], nh[1], ba, xa[1], voa, voa, rsa, soa + 2 * sta, soa + 3 * sta, m0a + 0x2000, m0a + 0x3000);
+  n16_block_dma<2, XO, SW>(acc[2], cb[2], cx, nb[2], nl[2], nh[2], ba, xa[2], voa, voa, rsa, soa + 4 * sta, soa + 5 * sta, m0a + 0x4000, m0a + 0x5000);
+  n16_block_dma<3, XO, SW>(acc[3], cb[3], cx, nb[3], nl[3], nh[3], ba, xa[3], voa, voa, rsa, soa + 6 * sta, soa + 7 * sta, m0a + 0x6000, m0a + 0x7000);
+  n16_block_dma<4, XO, SW>(acc[4], cb[4], cx, nb[4], nl[4], nh[4], ba, xa[4], voxe, voxo, rsx, sox, sox + stx, m0x, m0x + 0x1000);
+  n16_block_dma<5, XO, SW>(acc[5], cb[5], cx, nb[5], nl[5], nh[5], ba, xa[5], voxe, voxo, rsx, sox + 2 * stx, sox + 3 * stx, m0x + 0x2000, m0x + 0x3000);
+  n16_block_dma<6, XO, SW>(acc[6], cb[6], cx, nb[6], nl[6], nh[6], ba, xa[6], voxe, voxo, rsx, sox + 4 * stx, sox + 5 * stx, m0x + 0x4000, m0x + 0x5000);
+  n16_block_dma<7, XO, SW>(acc[7], cb[7], cx, nb[7], nl[7], nh[7], ba, xa[7], voxe, voxo, rsx, sox + 6 * stx, sox + 7 * stx, m0x + 0x6000, m0x + 0x7000);
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
@@ -1616,30 +1631,50 @@ MUON_DEVICE void n16_beta_frags(float ratio, int lane, bf16x8_mfma (&db)[2][2]) 
 }
 
 #define M16(C, X, B) "v_mfma_f32_16x16x32_bf16 %[" #C "], %[" #X "], %[" #B "], %[" #C "]\n\t"
-#define NB_ROW(P, F, B)                                                                      \
-  M16(P##0, x0, B) M16(P##1, x1, B) M16(P##2, x2, B) M16(P##3, x3, B)                         \
-  M16(P##4, x4, B) M16(P##5, x5, B) M16(P##6, x6, B) M16(P##7, x7, B)
+#define M16S(C, X, B) "v_mfma_f32_16x16x32_bf16 %[" #C "], %[" #B "], %[" #X "], %[" #C "]\n\t"
+#define NB_ROW(M, P, F, B)                                                                   \
+  M(P##0, x0, B) M(P##1, x1, B) M(P##2, x2, B) M(P##3, x3, B)                                 \
+  M(P##4, x4, B) M(P##5, x5, B) M(P##6, x6, B) M(P##7, x7, B)
+#define NB_ALL(M) NB_ROW(M, a, FI, d0h) NB_ROW(M, b, FI + 1, d1h) NB_ROW(M, a, FI, d0l) NB_ROW(M, b, FI + 1, d1l)
+#define NB_OUT                                                                               \
+  [a0] "+a"(acc[FI][0]), [a1] "+a"(acc[FI][1]), [a2] "+a"(acc[FI][2]), [a3] "+a"(acc[FI][3]),   \
+  [a4] "+a"(acc[FI][4]), [a5] "+a"(acc[FI][5]), [a6] "+a"(acc[FI][6]), [a7] "+a"(acc[FI][7]),   \
+  [b0] "+a"(acc[FI + 1][0]), [b1] "+a"(acc[FI + 1][1]), [b2] "+a"(acc[FI + 1][2]),             \
+  [b3] "+a"(acc[FI + 1][3]), [b4] "+a"(acc[FI + 1][4]), [b5] "+a"(acc[FI + 1][5]),             \
+  [b6] "+a"(acc[FI + 1][6]), [b7] "+a"(acc[FI + 1][7])
+#define NB_IN                                                                                \
+  [x0] "v"(cx[0]), [x1] "v"(cx[1]), [x2] "v"(cx[2]), [x3] "v"(cx[3]), [x4] "v"(cx[4]),        \
+  [x5] "v"(cx[5]), [x6] "v"(cx[6]), [x7] "v"(cx[7]), [d0h] "v"(db[0][0]), [d0l] "v"(db[0][1]), \
+  [d1h] "v"(db[1][0]), [d1l] "v"(db[1][1])
 // ratio * X added to row blocks FI and FI + 1 (rows 32 ks .. 32 ks + 31 of the K-tile whose
-// X fragments cx are the substep's): 32 MFMAs, the hi parts of both row blocks first.
-template <int FI>
+// X fragments cx are the substep's): 32 MFMAs, the hi parts of both row blocks first. The
+// diagonal fragment serves as srcA as well (SW): its per-lane layout is the same.
+template <int FI, bool SW = false>
 MUON_DEVICE void n16_beta(f32x4 (&acc)[8][8], const bf16x8_mfma (&cx)[8],
                           const bf16x8_mfma (&db)[2][2]) {
-  asm volatile(NB_ROW(a, FI, d0h) NB_ROW(b, FI + 1, d1h) NB_ROW(a, FI, d0l) NB_ROW(b, FI + 1, d1l)
-               : [a0] "+a"(acc[FI][0]), [a1] "+a"(acc[FI][1]), [a2] "+a"(acc[FI][2]),
-                 [a3] "+a"(acc[FI][3]), [a4] "+a"(acc[FI][4]), [a5] "+a"(acc[FI][5]),
-                 [a6] "+a"(acc[FI][6]), [a7] "+a"(acc[FI][7]), [b0] "+a"(acc[FI + 1][0]),
-                 [b1] "+a"(acc[FI + 1][1]), [b2] "+a"(acc[FI + 1][2]), [b3] "+a"(acc[FI + 1][3]),
-                 [b4] "+a"(acc[FI + 1][4]), [b5] "+a"(acc[FI + 1][5]), [b6] "+a"(acc[FI + 1][6]),
-                 [b7] "+a"(acc[FI + 1][7])
-               : [x0] "v"(cx[0]), [x1] "v"(cx[1]), [x2] "v"(cx[2]), [x3] "v"(cx[3]),
-                 [x4] "v"(cx[4]), [x5] "v"(cx[5]), [x6] "v"(cx[6]), [x7] "v"(cx[7]),
-                 [d0h] "v"(db[0][0]), [d0l] "v"(db[0][1]), [d1h] "v"(db[1][0]), [d1l] "v"(db[1][1]));
+  if constexpr (SW)
+    asm volatile(NB_ALL(M16S) : NB_OUT : NB_IN);
+  else
+    asm volatile(NB_ALL(M16) : NB_OUT : NB_IN);
 }
+#undef NB_ALL
+#undef NB_OUT
+#undef NB_IN
+#undef M16S
 #undef NB_ROW
 #undef M16
 
-__global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g) {
+// APPLY 0: X' stored into the workspace. APPLY 1 / 2 (the last iteration, bf16 parameters):
+// X' is not stored; each bf16 element of it is the update u of one parameter element, applied
+// as the post-pass does (apply_elem: cautious weight decay and the shape-scaled step) and the
+// parameter written back. 1: a wide matrix (parameter row i = X' row i); 2: a tall matrix
+// (parameter row j = X' column j), computed with swapped MFMA operands so the accumulators
+// hold parameter rows.
+// MODE (APPLY 1, 2): the form of the apply, from the uniform wd and cautious (below).
+template <int APPLY, int MODE = 0>
+__global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g, MuonApply ap) {
   constexpr int WM = 128, WN = 128;
+  constexpr bool SW = APPLY == 2;
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1746,11 +1781,11 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g) {
       constexpr int FB = decltype(beta_fi0)::value;
       const int cs = kt & 1;
       set_xa(cs);
-      n16_substep<16 * NN_XROWB * 2>(acc, b0, x0, b1, xl, xh, baddr(cs, 1), xa);
+      n16_substep<16 * NN_XROWB * 2, SW>(acc, b0, x0, b1, xl, xh, baddr(cs, 1), xa);
       if constexpr (FB >= 0) {
         bf16x8_mfma db[2][2];
         n16_beta_frags(ratio, lane, db);
-        n16_beta<FB>(acc, x0, db);
+        n16_beta<FB, SW>(acc, x0, db);
       }
       n16_join(x1, xl, xh);
       wait_vmcnt0();
@@ -1759,13 +1794,13 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g) {
       const int k2 = c2 ? kt + 2 : kt + 2 - KT;
       set_xa(cs ^ 1);
       const uint32_t m0a = m0w + cs * NN_STAGEB;
-      n16_substep_dma<0>(acc, b1, x1, b0, xl, xh, baddr(cs ^ 1, 0), xa, voa, vox, voxo, c2 ? rsa : rsa_n,
+      n16_substep_dma<0, SW>(acc, b1, x1, b0, xl, xh, baddr(cs ^ 1, 0), xa, voa, vox, voxo, c2 ? rsa : rsa_n,
                          c2 ? rsx : rsx_n, k2 * V2_ROWB, k2 * V2_BK * ldx_b, sta, stx, m0a,
                          m0a + NN_ATILEB);
       if constexpr (FB >= 0) {
         bf16x8_mfma db[2][2];
         n16_beta_frags(ratio, lane, db);
-        n16_beta<FB + 2>(acc, x1, db);
+        n16_beta<FB + 2, SW>(acc, x1, db);
       }
       n16_join(x0, xl, xh);
     };
@@ -1780,61 +1815,153 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g) {
     mfma_to_valu_wait();
 
     // epilogue: accumulator (fi, fj) element q is X'(i, j + q) with i = 128 wm + 16 fi +
-    // lane%16, j = 128 wn + 16 fj + 4 (lane/16). Two row blocks (32 rows) at a time go through
+    // lane%16, j = 128 wn + 16 fj + 4 (lane/16) (SW: X'(i + q, j) with i = 128 wm + 16 fi +
+    // 4 (lane/16), j = 128 wn + 16 fj + lane%16). Two row blocks (32 rows) at a time go through
     // the wave's LDS staging rows (16-byte chunk k of row r at chunk k ^ (r & 15)), then out as
     // 4 whole rows of 256 bytes per non-temporal store.
-    bf16_t* outw = (bf16_t*)g.out + (int64_t)bidx * g.so + (arow0 + wm * WM) * g.ldo + bcol0 + wn * WN;
-    const __amdgpu_buffer_rsrc_t rso =
-        __builtin_amdgcn_make_buffer_rsrc((void*)outw, 0, 0x7fffffff, 0x00020000);
-    const int ldo_b = (int)(g.ldo * 2);
     const uint32_t ep = lds0 + 2 * NN_STAGEB + wave * N4_EPB;
     const uint32_t epr = ep + (lane >> 4) * 256;
-    const int vor = (lane >> 4) * ldo_b + (lane & 15) * 16;
-    const bool full = arow0 + 256 <= g.Mv && bcol0 + 256 <= g.Nv;
-    const int rem_i = (int)g.Mv - (int)(arow0 + wm * WM + fr);
-    const int rem_j = (int)g.Nv - (int)(bcol0 + wn * WN + 4 * fg);
-    auto emit = [&](auto masked) {
+    // staging rows 32 p .. 32 p + 31: X' rows (APPLY 0, 1) or X' columns (APPLY 2), packed bf16
+    auto stage = [&](int p, auto masked, int rem_i, int rem_j) {
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
+      for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int fi = 2 * p + h;
-#pragma unroll
-          for (int fj = 0; fj < 8; ++fj) {
-            f32x4 av;
-            asm volatile("" : "=v"(av) : "0"(acc[fi][fj]));
-            f2x v01 = {alpha * av[0], alpha * av[1]};
-            f2x v23 = {alpha * av[2], alpha * av[3]};
-            if (decltype(masked)::value) {
-              const int jq = fj * 16;
-              const bool vi = fi * 16 < rem_i;
-              v01.x = vi && jq + 0 < rem_j ? v01.x : 0.0f;
-              v01.y = vi && jq + 1 < rem_j ? v01.y : 0.0f;
-              v23.x = vi && jq + 2 < rem_j ? v23.x : 0.0f;
-              v23.y = vi && jq + 3 < rem_j ? v23.y : 0.0f;
-            }
-            const u32x2 w = {__builtin_bit_cast(uint32_t, __builtin_convertvector(v01, bf2x)),
-                             __builtin_bit_cast(uint32_t, __builtin_convertvector(v23, bf2x))};
-            uint32_t ea = ep + (h * 16 + fr) * 256 + (fg & 1) * 8, fx = fr;
-            asm volatile("" : "+v"(ea), "+v"(fx));
-            *(u32x2 __attribute__((address_space(3)))*)(ea + (((2 * fj + (fg >> 1)) ^ fx) << 4)) = w;
+        for (int k = 0; k < 8; ++k) {
+          f32x4 av;
+          if constexpr (SW)
+            asm volatile("" : "=v"(av) : "0"(acc[k][2 * p + h]));
+          else
+            asm volatile("" : "=v"(av) : "0"(acc[2 * p + h][k]));
+          f2x v01 = {alpha * av[0], alpha * av[1]};
+          f2x v23 = {alpha * av[2], alpha * av[3]};
+          if (decltype(masked)::value) {
+            const int fi = 2 * p + h, jq = k * 16;
+            const bool vi = fi * 16 < rem_i;
+            v01.x = vi && jq + 0 < rem_j ? v01.x : 0.0f;
+            v01.y = vi && jq + 1 < rem_j ? v01.y : 0.0f;
+            v23.x = vi && jq + 2 < rem_j ? v23.x : 0.0f;
+            v23.y = vi && jq + 3 < rem_j ? v23.y : 0.0f;
           }
-        }
-        uint32_t ra = epr, lc = lane & 15, lr = lane >> 4;
-        int vs = vor;
-        asm volatile("" : "+v"(ra), "+v"(vs), "+v"(lc), "+v"(lr));
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t c = lc ^ ((4 * i + lr) & 15);
-          const u32x4 q4 = *(const u32x4 __attribute__((address_space(3)))*)(ra + i * 1024 + (c << 4));
-          __builtin_amdgcn_raw_buffer_store_b128(q4, rso, vs + i * 4 * ldo_b, p * 32 * ldo_b, 2);
+          const u32x2 w = {__builtin_bit_cast(uint32_t, __builtin_convertvector(v01, bf2x)),
+                           __builtin_bit_cast(uint32_t, __builtin_convertvector(v23, bf2x))};
+          uint32_t ea = ep + (h * 16 + fr) * 256 + (fg & 1) * 8, fx = fr;
+          asm volatile("" : "+v"(ea), "+v"(fx));
+          *(u32x2 __attribute__((address_space(3)))*)(ea + (((2 * k + (fg >> 1)) ^ fx) << 4)) = w;
         }
       }
     };
-    if (full)
-      emit(std::false_type{});
-    else
-      emit(std::true_type{});
+    if constexpr (APPLY == 0) {
+      bf16_t* outw = (bf16_t*)g.out + (int64_t)bidx * g.so + (arow0 + wm * WM) * g.ldo + bcol0 + wn * WN;
+      const __amdgpu_buffer_rsrc_t rso =
+          __builtin_amdgcn_make_buffer_rsrc((void*)outw, 0, 0x7fffffff, 0x00020000);
+      const int ldo_b = (int)(g.ldo * 2);
+      const int vor = (lane >> 4) * ldo_b + (lane & 15) * 16;
+      const bool full = arow0 + 256 <= g.Mv && bcol0 + 256 <= g.Nv;
+      const int rem_i = (int)g.Mv - (int)(arow0 + wm * WM + fr);
+      const int rem_j = (int)g.Nv - (int)(bcol0 + wn * WN + 4 * fg);
+      auto emit = [&](auto masked) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          stage(p, masked, rem_i, rem_j);
+          uint32_t ra = epr, lc = lane & 15, lr = lane >> 4;
+          int vs = vor;
+          asm volatile("" : "+v"(ra), "+v"(vs), "+v"(lc), "+v"(lr));
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const uint32_t c = lc ^ ((4 * i + lr) & 15);
+            const u32x4 q4 = *(const u32x4 __attribute__((address_space(3)))*)(ra + i * 1024 + (c << 4));
+            __builtin_amdgcn_raw_buffer_store_b128(q4, rso, vs + i * 4 * ldo_b, p * 32 * ldo_b, 2);
+          }
+        }
+      };
+      if (full)
+        emit(std::false_type{});
+      else
+        emit(std::true_type{});
+    } else {
+      // the parameter block of this wave: rows orow0 .., columns ocol0 .. of matrix mb of
+      // tensor t; staging row r of round p is parameter row orow0 + 32 p + r, chunk c its
+      // columns ocol0 + 8 c .. + 7
+      const int t = (int)(bidx / ap.nb);
+      const int64_t mb = bidx - (int64_t)t * ap.nb;
+      const float adj = ap.adj[t];
+      const int64_t orow0 = SW ? bcol0 + wn * WN : arow0 + wm * WM;
+      const int64_t ocol0 = SW ? arow0 + wm * WM : bcol0 + wn * WN;
+      bf16_t* pw = (bf16_t*)ap.params[t] + mb * ap.prows * ap.pcols + orow0 * ap.pcols + ocol0;
+      const __amdgpu_buffer_rsrc_t rsp =
+          __builtin_amdgcn_make_buffer_rsrc((void*)pw, 0, 0x7fffffff, 0x00020000);
+      const int ldp_b = (int)(ap.pcols * 2);
+      const int lr = lane >> 4, lc = lane & 15;
+      const int vop = lr * ldp_b + lc * 16;
+      const int vrows = (int)std::min<int64_t>(ap.prows - orow0, 1 << 20);  // valid rows from orow0
+      const bool vcol = ocol0 + lc * 8 < ap.pcols;                          // whole 8-column chunks
+      // Chunk i of round p is parameter row 32 p + 4 i + lane/16 of the block; its row offset is
+      // the scalar offset of the access. A lane outside the parameter (padding rows or columns)
+      // takes a per-lane offset past the descriptor's range instead of a branch: its loads
+      // read zeros and its stores are dropped, so the code stays straight and the loads of
+      // round p + 1 go out before round p is applied.
+      const float adjr = bf16_to_f32(f32_to_bf16(adj));
+      auto voff = [&](int p, int i) -> int {
+        return vcol && lr < vrows - (p * 32 + 4 * i) ? vop : (int)0x80000000;
+      };
+      // apply_elem<bf16, bf16> in three straight forms (one kernel each; wd and cautious are
+      // uniform), the same operations in the same order: MODE 1 cautious weight decay, 2 plain
+      // weight decay, 0 no weight decay (the bf16-rounded step)
+      auto rounds = [&](auto mode_c) {
+        constexpr int AM = decltype(mode_c)::value;
+        u32x4 pv[2][8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          pv[0][i] = __builtin_amdgcn_raw_buffer_load_b128(rsp, voff(0, i), 4 * i * ldp_b, 2);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          if (p < 3) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              pv[(p + 1) & 1][i] = __builtin_amdgcn_raw_buffer_load_b128(
+                  rsp, voff(p + 1, i), ((p + 1) * 32 + 4 * i) * ldp_b, 2);
+          }
+          stage(p, std::false_type{}, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const uint32_t c = lc ^ ((4 * i + lr) & 15);
+            const u32x4 q4 = *(const u32x4 __attribute__((address_space(3)))*)(epr + i * 1024 + (c << 4));
+            const u32x4 pq = pv[p & 1][i];
+            uint32_t ow[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              uint32_t r[2];
+#pragma unroll
+              for (int hh = 0; hh < 2; ++hh) {
+                const float u = __uint_as_float(hh ? q4[e] & 0xffff0000u : q4[e] << 16);
+                const float pp = __uint_as_float(hh ? pq[e] & 0xffff0000u : pq[e] << 16);
+                float o;
+                {
+#pragma clang fp contract(off)
+                  if constexpr (AM == 1) {
+                    const float prod = u * pp;
+                    const float m = prod > 0.0f ? 1.0f : 0.0f;
+                    const float tt = (ap.wd * pp) * m;
+                    o = pp - adj * (u + tt);
+                  } else if constexpr (AM == 2) {
+                    o = pp - adj * (u + ap.wd * pp);
+                  } else {
+                    o = pp - bf16_to_f32(f32_to_bf16(adjr * u));
+                  }
+                }
+                // round to nearest even in the high half; NaN -> 0x7fc0 (as f32_to_bf16)
+                const uint32_t x = __float_as_uint(o);
+                r[hh] = o != o ? 0x7fc00000u : x + 0x7fffu + ((x >> 16) & 1u);
+              }
+              ow[e] = __builtin_amdgcn_perm(r[1], r[0], 0x07060302u);
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{ow[0], ow[1], ow[2], ow[3]}, rsp,
+                                                   voff(p, i), (p * 32 + 4 * i) * ldp_b, 2);
+          }
+        }
+      };
+      rounds(std::integral_constant<int, MODE>{});
+    }
     if (!has_next) break;
     li = lnext;
     bidx = nbidx;
@@ -2251,9 +2378,15 @@ int reserve_bf16_lds() {
     if (hipFuncSetAttribute((const void*)gemm_bf16_nn4_kernel,
                             hipFuncAttributeMaxDynamicSharedMemorySize, N4_SMEM) != hipSuccess)
       status = -1;
-    if (hipFuncSetAttribute((const void*)gemm_bf16_nn16_kernel,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, N4_SMEM) != hipSuccess)
-      status = -1;
+    const void* n16[7] = {
+        (const void*)gemm_bf16_nn16_kernel<0>,    (const void*)gemm_bf16_nn16_kernel<1, 0>,
+        (const void*)gemm_bf16_nn16_kernel<1, 1>, (const void*)gemm_bf16_nn16_kernel<1, 2>,
+        (const void*)gemm_bf16_nn16_kernel<2, 0>, (const void*)gemm_bf16_nn16_kernel<2, 1>,
+        (const void*)gemm_bf16_nn16_kernel<2, 2>};
+    for (const void* k : n16)
+      if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, N4_SMEM) !=
+          hipSuccess)
+        status = -1;
   });
   return status;
 }
@@ -2369,8 +2502,12 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
       }
       // persistent: one workgroup per CU walks the tile list
       const int wgs = (int)std::min<int64_t>(blocks, device_cus());
-      if (K >= 1024)
-        hipLaunchKernelGGL(gemm_bf16_nn16_kernel, dim3((unsigned)wgs), dim3(256), N4_SMEM, stream, g);
+      if (K >= 1024) {
+        MuonApply none;
+        none.nb = 1;
+        hipLaunchKernelGGL(gemm_bf16_nn16_kernel<0>, dim3((unsigned)wgs), dim3(256), N4_SMEM,
+                           stream, g, none);
+      }
       else
         hipLaunchKernelGGL(gemm_bf16_nn4_kernel, dim3((unsigned)wgs), dim3(256), N4_SMEM, stream, g);
     } else if (!masked && (alpha != 0.0f || beta == 0.0f)) {
@@ -2406,5 +2543,71 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
     return MUON_ERR_DTYPE;
   }
   MUON_CHECK_LAUNCH("gemm");
+  return MUON_OK;
+}
+
+// The last iteration's X' = a X + B X with the post-pass applied in its epilogue (bf16
+// parameters, K >= 1024: the 16 x 16 x 32 GEMM); extents and operands as muon_launch_gemm's
+// GEMM mode, X' is not stored. tall: the parameter is the transpose of the iterate (its
+// rows are the columns of X'). Parameter rows of whole 8-element chunks (pcols % 8 == 0) and
+// 16-byte aligned tensors are the caller's to check.
+int muon_launch_gemm_apply(int64_t batch, int64_t M, int64_t N, int64_t K, const void* a,
+                           int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb,
+                           int64_t Mv, int64_t Nv, float alpha, float beta, const float* scale,
+                           int scale_mode, const MuonApply& ap, int tall, hipStream_t stream) {
+  if (K < 1024 || K % 128 || M % BF_BM || N % BF_BM || alpha == 0.0f || ap.nb <= 0 ||
+      (batch + ap.nb - 1) / ap.nb > MUON_APPLY_MAX || ap.pcols % 8) {
+    muon_set_error("gemm_apply: unsupported launch (K %lld, batch %lld)", (long long)K,
+                   (long long)batch);
+    return MUON_ERR_ARG;
+  }
+  if (std::max(M * lda, K * ldb) * 2 >= (int64_t)0x7fffffff ||
+      ap.prows * ap.pcols * 2 >= (int64_t)0x7fffffff) {
+    muon_set_error("gemm_apply: operand exceeds the 2 GiB per-matrix limit");
+    return MUON_ERR_SHAPE;
+  }
+  GemmArgs g;
+  memset(&g, 0, sizeof(g));
+  g.a = a;
+  g.b = b;
+  g.cin = b;
+  g.lda = lda;
+  g.ldb = ldb;
+  g.ldc = ldb;
+  g.sa = sa;
+  g.sb = sb;
+  g.sc = sb;
+  g.Mv = Mv;
+  g.Nv = Nv;
+  g.alpha = alpha;
+  g.beta = beta;
+  g.scale = scale;
+  g.scale_mode = scale_mode;
+  g.tiles_m = (int)(M / BF_BM);
+  g.tiles_n = (int)(N / BF_BM);
+  g.K = K;
+  g.tiles_per_batch = g.tiles_m * g.tiles_n;
+  const int64_t blocks = (int64_t)g.tiles_per_batch * batch;
+  if (blocks == 0) return MUON_OK;
+  if (blocks > 0x7fffffffLL) {
+    muon_set_error("gemm_apply: grid too large (%lld tiles)", (long long)blocks);
+    return MUON_ERR_SHAPE;
+  }
+  g.tiles_total = (int)blocks;
+  if (reserve_bf16_lds() != 0) {
+    muon_set_error("gemm_apply: cannot reserve LDS");
+    return MUON_ERR_LAUNCH;
+  }
+  const int wgs = (int)std::min<int64_t>(blocks, device_cus());
+  const int mode = ap.wd == 0.0f ? 0 : (ap.cautious ? 1 : 2);
+#define LAUNCH_APPLY(A, M) \
+  hipLaunchKernelGGL((gemm_bf16_nn16_kernel<A, M>), dim3((unsigned)wgs), dim3(256), N4_SMEM, stream, g, ap)
+  if (tall) {
+    if (mode == 0) LAUNCH_APPLY(2, 0); else if (mode == 1) LAUNCH_APPLY(2, 1); else LAUNCH_APPLY(2, 2);
+  } else {
+    if (mode == 0) LAUNCH_APPLY(1, 0); else if (mode == 1) LAUNCH_APPLY(1, 1); else LAUNCH_APPLY(1, 2);
+  }
+#undef LAUNCH_APPLY
+  MUON_CHECK_LAUNCH("gemm_apply");
   return MUON_OK;
 }

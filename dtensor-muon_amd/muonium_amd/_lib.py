@@ -48,6 +48,12 @@ _SIGNATURES = {
         [_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.POINTER(ctypes.c_double), _c_int,
          _c_f32, _c_f32, _vp],
     ),
+    "muon_orth_run_apply": (
+        _c_int,
+        [_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.POINTER(ctypes.c_double), _c_int,
+         _c_f32, _c_f32, _c_int, _pp, _c_int, _c_i64, ctypes.POINTER(_c_f32), _c_f32, _c_int,
+         _vp],
+    ),
     "muon_orth_extract": (
         _c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _vp, _c_int, _vp]
     ),
@@ -142,7 +148,8 @@ def ensure_device(device: torch.device) -> None:
     _initialized_devices.add(idx)
 
 
-KERNEL_KINDS = ("syrk_xx", "syrk_aa", "gemm_bx", "prepass", "postpass", "lp_prepass", "other")
+KERNEL_KINDS = ("syrk_xx", "syrk_aa", "gemm_bx", "prepass", "postpass", "lp_prepass", "other",
+                "gemm_bx_apply")
 
 
 def timing_enable(on: bool) -> None:

@@ -312,6 +312,18 @@ def _fused_step_impl(params: list[Tensor], grads: list[Tensor], bufs: list[Tenso
                          ws.data_ptr(), _lib.DT_BF16, cap, s),
         "muon_prepass",
     )
+    if u_scales is None:
+        # the iteration and the apply in one call: the library fuses the apply into the last
+        # X' = a X + B X where the shapes allow it, else runs the post-pass after it
+        _lib.check(
+            lib.muon_orth_run_apply(ws.data_ptr(), _lib.DT_BF16, cap, count * nb, rows, cols,
+                                    _flat_coeffs(coeffs), steps, prescale, eps, count,
+                                    _lib.ptr_array(params), _lib.dtype_code(params[0].dtype), nb,
+                                    _lib.f32_array(lrs), float(weight_decay), int(cautious_wd),
+                                    s),
+            "muon_orth_run_apply",
+        )
+        return
     _lib.check(
         lib.muon_orth_run(ws.data_ptr(), _lib.DT_BF16, cap, count * nb, rows, cols,
                           _flat_coeffs(coeffs), steps, prescale, eps, s),
@@ -320,8 +332,7 @@ def _fused_step_impl(params: list[Tensor], grads: list[Tensor], bufs: list[Tenso
     _lib.check(
         lib.muon_postpass(count, _lib.ptr_array(params), _lib.dtype_code(params[0].dtype), None,
                           0, ws.data_ptr(), _lib.DT_BF16, cap, steps, nb, rows, cols,
-                          _lib.f32_array(lrs),
-                          None if u_scales is None else _lib.f32_array(u_scales),
+                          _lib.f32_array(lrs), _lib.f32_array(u_scales),
                           float(weight_decay), int(cautious_wd), s),
         "muon_postpass",
     )

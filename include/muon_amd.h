@@ -53,7 +53,7 @@ extern "C" {
 /* Maximum tensors per multi-tensor launch; larger lists are chunked internally. */
 #define MUON_MAX_TENSORS 32
 
-/* ABI version of this header (bumped on any signature change): 4. */
+/* ABI version of this header (bumped on any signature change): 5. */
 int muon_amd_abi_version(void);
 
 /* Text of the last error reported on the calling thread ("" if none). */
@@ -113,6 +113,21 @@ int muon_prepass(int ntensors, void* const* grads, void* const* bufs, int g_dtyp
 int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64_t rows,
                   int64_t cols, const double* coeffs, int steps, float prescale, float eps,
                   void* stream);
+
+/* muon_orth_run followed by muon_postpass of its result (u = NULL, the same arguments),
+ * with the post-pass fused into the last iteration's X = a*X + B X where the shapes allow
+ * (bf16 workspace and parameters, at least 65 rows and 1024 valid ones after padding to
+ * 128 on the iterate's short side, ntensors * nb == batch, at most 128 tensors,
+ * parameter rows a multiple of 8 elements in the stored orientation, 16-byte aligned
+ * parameters): each bf16 element of the last X' is applied to its parameter element
+ * (cautious weight decay and the shape-scaled step, exactly as muon_postpass) and X' is
+ * not stored, so the workspace does not hold U afterwards. Otherwise the two calls run
+ * one after the other. Replaces the orthogonalize-then-apply sequence of
+ * muonium/optim/algorithms/muon.py:101-140 (foreach_update) and :58-77 (update). */
+int muon_orth_run_apply(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64_t rows,
+                        int64_t cols, const double* coeffs, int steps, float prescale,
+                        float eps, int ntensors, void* const* params, int p_dtype, int64_t nb,
+                        const float* adjusted_lrs, float wd, int cautious, void* stream);
 
 /* Copy U (first `batch` matrices, stored layout) out of the workspace into a
  * contiguous (batch, rows, cols) tensor of out_dtype. Replaces the return/unbind of
@@ -218,7 +233,10 @@ int muon_lp_prepass(int ntensors, void* const* grads, int g_dtype, void* const* 
 #define MUON_K_POSTPASS 4  /* bytes: u + 2 * param per element */
 #define MUON_K_LP_PREPASS 5 /* bytes: grad + 2 * codes + 2 * scales + one bf16 X */
 #define MUON_K_OTHER 6     /* finalize / transpose / scale / extract (no work counted) */
-#define MUON_K_COUNT 7
+#define MUON_K_GEMM_BX_APPLY 7 /* the last X = a X + B X with the post-pass fused
+                                  (muon_orth_run_apply): 2 m^2 n FLOP per matrix; the apply
+                                  moves 2 * param bytes per element besides */
+#define MUON_K_COUNT 8
 int muon_timing_enable(int on);
 int muon_timing_read(double* ms, int64_t* launches, double* work);
 

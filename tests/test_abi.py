@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_text():
     lib = _lib.load()
-    assert lib.muon_amd_abi_version() == 4
+    assert lib.muon_amd_abi_version() == 5
     assert isinstance(_lib.last_error(), str)
 
 
