@@ -521,16 +521,13 @@ def _fused_lp_impl(params: list[Tensor], grads: list[Tensor], codes: list[Tensor
         ),
         "muon_lp_prepass",
     )
+    # the iteration and the apply (fused into the last B X where the shapes allow)
     _lib.check(
-        lib.muon_orth_run(ws.data_ptr(), _lib.DT_BF16, cap, count * nb, rows, cols,
-                          _flat_coeffs(coeffs), steps, prescale, eps, s),
-        "muon_orth_run",
-    )
-    _lib.check(
-        lib.muon_postpass(count, _lib.ptr_array(params), _lib.dtype_code(params[0].dtype), None,
-                          0, ws.data_ptr(), _lib.DT_BF16, cap, steps, nb, rows, cols,
-                          _lib.f32_array(lrs), None, float(weight_decay), int(cautious_wd), s),
-        "muon_postpass",
+        lib.muon_orth_run_apply(ws.data_ptr(), _lib.DT_BF16, cap, count * nb, rows, cols,
+                                _flat_coeffs(coeffs), steps, prescale, eps, count,
+                                _lib.ptr_array(params), _lib.dtype_code(params[0].dtype), nb,
+                                _lib.f32_array(lrs), float(weight_decay), int(cautious_wd), s),
+        "muon_orth_run_apply",
     )
 
 

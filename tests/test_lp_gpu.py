@@ -204,6 +204,23 @@ def test_lp_deferred_scale_prepass_outputs_exact(fmt, cls, block, shape, gdtype)
     _check_tiled_prepass(fmt, cls, block, shape, gdtype)
 
 
+ROWSEG = [("8bit", OptimState8bit), ("4bit", OptimState4bit), ("fp8", OptimStateFp8)]
+ROWSEG_CASES = [(2048, (128, 2048)), (2048, (3000, 2048)), (2048, (192, 4096)), (512, (1024, 512)),
+                (1024, (200, 1024)), (8192, (64, 8192)), (2048, (2, 256, 2048)), (2048, (4096, 6144))]
+
+
+@pytest.mark.parametrize("fmt,cls", ROWSEG)
+@pytest.mark.parametrize("block,shape", ROWSEG_CASES)
+@pytest.mark.parametrize("gdtype", [torch.float32, torch.bfloat16])
+def test_lp_row_segment_blocks_exact(fmt, cls, block, shape, gdtype):
+    """Blocks of 512 to 8192 values whose width divides the column count (the reference's
+    default 2048 on every Llama shape: each block a whole row segment) through the
+    deferred-scale path. Codes, scales, X0 and the norm partials exactly as the oracle, wide
+    and tall (3000 and 4096 rows: partial and whole 64-row tiles), stacked, a 64-row
+    iterate, two steps."""
+    _check_tiled_prepass(fmt, cls, block, shape, gdtype)
+
+
 @pytest.mark.parametrize("fmt,cls,block,shape", [
     ("8bit", OptimState8bit, 2048, (256, 768)), ("4bit", OptimState4bit, 2048, (768, 256)),
     ("fp8", OptimStateFp8, 2048, (256, 768)), ("fp8", OptimStateFp8, "numel", (768, 256)),
@@ -303,7 +320,8 @@ def _check_tiled_prepass(fmt, cls, block, shape, gdtype, g=None, check_partials=
         assert np.array_equal(st.codes.cpu().numpy(), codes), f"codes differ at step {step}"
         assert np.array_equal(st.scale.cpu().numpy().view(np.uint32), scales.view(np.uint32))
     m, n = min(rows, cols), max(rows, cols)
-    mp, npad = -(-m // 256) * 256, -(-n // 256) * 256
+    # iterates of at most 64 rows pad their rows to 64 only (the short path)
+    mp, npad = (64 if m <= 64 else -(-m // 256) * 256), -(-n // 256) * 256
     # X0 (the iterate before any step) in rows of `pitch` elements: the padding columns
     # up to n_pad are rewritten to zero, the rest of each row is never read
     off0, pitch, mst = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
