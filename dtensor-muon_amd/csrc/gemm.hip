@@ -2156,7 +2156,8 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_s16_kernel(GemmArgs g) {
   // triangle (mode 1), waves 6 and 7 blocks (2, 0) and (3, 0), wholly below it (mode 2: no
   // MFMAs). The a and b panels of a diagonal tile are the same rows: only the a panel is
   // loaded, and the b fragments are read from it.
-  const bool diag = tm == tn;
+  const bool dtile = tm == tn;
+  const bool diag = dtile && g.beta != 0.0f;
   const int wm = diag ? (0x32312100 >> (4 * wave)) & 15 : wave >> 1;
   const int wn = diag ? (0x00101110 >> (4 * wave)) & 15 : wave & 1;
   const int wmode = diag ? (0x22110000 >> (4 * wave)) & 15 : 0;
@@ -2276,7 +2277,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_s16_kernel(GemmArgs g) {
     s16_pack(acc, alpha, arow0 + 256 <= g.Mv && brow0 + 256 <= g.Nv,
              clamp_rem(g.Mv - (arow0 + row0w + fg * 4)), clamp_rem(g.Nv - (brow0 + col0w + fr)), hv);
     bf16_t* out = (bf16_t*)g.out + (int64_t)bidx * g.so;
-    if (!diag) {
+    if (!dtile) {
       // mirror half of the symmetric output: T[j][i], 4 consecutive i per lane -> one 8-byte
       // write
       lds_barrier();
@@ -2315,7 +2316,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_s16_kernel(GemmArgs g) {
       const int id = it * 512 + tid;
       const int il = id >> 5, c = (id & 31) * 8;
       uint4 w;
-      if (!diag || c >= il) {
+      if (!dtile || c >= il) {
         w = *(const uint4*)(T + il * V2_EP_PITCH + c);
       } else {
         // diagonal tile, chunk reaching below the diagonal: those columns come from the
