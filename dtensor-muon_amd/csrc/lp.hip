@@ -416,8 +416,12 @@ MUON_DEVICE void lp_codes8(const float (&m)[8], float sc, bool sparse_map, const
   // (P. Markstein, IBM J. Res. Dev. 34(1), 1990). It needs normal intermediates: r normal
   // (sc <= 2^125), e exact and normal (|m| >= 2^-78) and q0 normal (|m| >= sc 2^-100).
   // A lane with any value outside that range (zeros included) takes the IEEE division for
-  // its 8 values; NaN or infinite scales fail the first test. Checked against the IEEE
-  // division on the CPU over every |m| <= sc for eight scales and 9e8 random pairs.
+  // its 8 values; NaN or infinite scales fail the first test. Quotients above 1 (fp8:
+  // sc = absmax / 448, so |m| / sc <= 448) reduce to |m| <= sc: m = 2^k m' with m' in
+  // (sc / 2, sc] scales q0, e and y by exactly 2^k while they stay normal and finite, which
+  // the range above and a finite m (|q0| <= 448, |e| <= ulp(m)) guarantee. Checked against the IEEE
+  // division on the CPU over every |m| <= sc for eight scales and on random pairs with
+  // |m| up to 448 sc.
   float ys[8];
   const float r = 1.0f / sc;
   const float lim = fmaxf(0x1p-78f, sc * 0x1p-100f);

@@ -1,9 +1,13 @@
 /* CPU check of the quotient used by the MuonLP kernels (lp.hip, lp_codes8): for
  * r = 1 / b (IEEE, correctly rounded), q0 = a * r, e = fma(-b, q0, a), y = fma(e, r, q0)
  * equals the IEEE quotient a / b whenever |a| <= b, b <= 2^125 and
- * |a| >= max(2^-78, b * 2^-100) (the kernels' fast-path condition).
+ * |a| >= max(2^-78, b * 2^-100) (the kernels' fast-path condition). Quotients above 1 (the
+ * fp8 scale is absmax / 448, so |a| / b <= 448) reduce to that case: a = 2^k a' with a' in
+ * (b / 2, b] scales q0, e and y by exactly 2^k while they stay normal. The random pairs
+ * test them directly too, with |a| up to 448 b.
  * Usage: markstein_check <random pairs> <exhaustive scales (0..8)>; exit status 1 on a
  * mismatch. */
+#include <float.h>
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -39,7 +43,8 @@ int main(int argc, char** argv) {
       if (bad > 10) return 1;
     }
   }
-  /* random scales in [1e-12, 2^125], random |a| <= b over 40 binades below b */
+  /* random scales in [1e-12, 2^125], random |a| over 40 binades below b and, for one pair in
+   * four, up to 448 b (the fp8 range) */
   uint64_t s = 0x9e3779b97f4a7c15ull;
   for (long k = 0; k < pairs; ++k) {
     s ^= s << 13; s ^= s >> 7; s ^= s << 17;
@@ -47,8 +52,10 @@ int main(int argc, char** argv) {
     if (b < 1e-12f) b = 1e-12f;
     if (b > 0x1p125f) b = 0x1p125f;
     s ^= s << 13; s ^= s >> 7; s ^= s << 17;
-    float a = ldexpf(1.0f + (float)(s & 0x7fffff) / 8388608.0f, ilogbf(b) - (int)((s >> 23) % 40));
-    if (a > b) a = b;
+    const int up = ((s >> 61) & 3) == 0 ? 9 : 0;
+    const double top = up ? fmin(448.0 * (double)b, (double)FLT_MAX) : (double)b;
+    double ad = ldexp(1.0 + (double)(s & 0x7fffff) / 8388608.0, ilogbf(b) + up - (int)((s >> 23) % 40));
+    float a = (float)fmin(ad, top);
     if (s >> 63) a = -a;
     const float r = 1.0f / b, lim = fmaxf(0x1p-78f, b * 0x1p-100f);
     bad += check(a, b, r, lim, &n);
