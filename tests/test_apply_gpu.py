@@ -135,3 +135,28 @@ def test_optimizer_step_uses_fused_apply_and_matches_given_u():
             weight_decay=0.1, cautious_wd=True, momentum=0.0, nesterov=False, maximize=False,
             orth_single=lambda x, u=u: u)
         assert torch.equal(p.detach().cpu(), ref)
+
+
+@pytest.mark.parametrize("shape", [(1024, 2048), (2048, 1024)])
+@pytest.mark.parametrize("wd,cautious", [(0.1, True), (0.1, False), (0.0, True)])
+def test_fused_apply_nonfinite_matches_postpass_bitwise(shape, wd, cautious):
+    """Non-finite and signed-zero parameters, and a NaN gradient element (which makes the
+    whole update of its matrix NaN): the fused epilogue rounds, masks and propagates them
+    exactly as the post-pass does, NaN payloads included (compared as bit patterns)."""
+    p, g, b = _case(shape, 2, torch.bfloat16, seed=sum(shape) + 7)
+    special = torch.tensor([float("nan"), float("inf"), float("-inf"), 0.0, -0.0, 1e-40,
+                            -3e38, 3e38], dtype=torch.bfloat16)
+    p[0][0, : special.numel()] = special
+    p[0][-1, -special.numel():] = special
+    p[1][5, 100] = float("nan")
+    g[1][3, 7] = float("nan")
+    pa = [t.clone().to(DEV) for t in p]
+    pb = [t.clone().to(DEV) for t in p]
+    ga, gb = [t.clone().to(DEV) for t in g], [t.clone().to(DEV) for t in g]
+    ba, bb = [t.clone().to(DEV) for t in b], [t.clone().to(DEV) for t in b]
+    _run(pa, ga, ba, fused=True, wd=wd, cautious=cautious)
+    _run(pb, gb, bb, fused=False, wd=wd, cautious=cautious)
+    assert pa[1].isnan().all(), "a NaN gradient element makes its matrix's update NaN"
+    for i, (x, y) in enumerate(zip(pa, pb)):
+        xi, yi = x.view(torch.int16), y.view(torch.int16)
+        assert torch.equal(xi, yi), f"tensor {i}: {(xi != yi).sum().item()} bit patterns differ"
