@@ -588,14 +588,23 @@ def main() -> None:
     if all(min(s[-2:]) <= 64 for s in orth_shapes) and pdtype == torch.bfloat16:
         # iterates of at most 64 rows run in short.hip: the B X launch streams X in and X'
         # out (bf16, 4 m n bytes per matrix), HBM-bound; it also forms the next Gram
-        # partials from registers
-        bx_bytes = sum(5 * 4 * (math.prod(s[:-2]) if len(s) > 2 else 1) * min(s[-2:]) * max(s[-2:])
-                       for s in orth_shapes) * args.steps / max(gn, 1)
+        # partials from registers. With the apply fused, the last of the 5 iterations is the
+        # gemm_bx_apply launch (X and the parameters in, the parameters out)
+        plain_iters = 5 - (1 if apply_fused else 0)
+        bx_bytes = sum(plain_iters * 4 * (math.prod(s[:-2]) if len(s) > 2 else 1) * min(s[-2:])
+                       * max(s[-2:]) for s in orth_shapes) * args.steps / max(gn, 1)
         achieved = bx_bytes / (avg_ms * 1e-3) / 1e9
-        traffic, traffic_src = _measured_traffic("short_bx_kernel", args.config, args.lp)
+        traffic, traffic_src = _measured_traffic("short_bx_kernel<-1>", args.config, args.lp)
+        if apply_fused:
+            ams, an, _ = kern["gemm_bx_apply"]
+            abytes = (2 + 2 * pdtype.itemsize) * numel * args.steps
+            kernels["gemm_bx_apply"].update(
+                bytes_per_elem=2 + 2 * pdtype.itemsize,
+                gbs=round(abytes / (ams * 1e-3) / 1e9, 1),
+                gbs_frac=round(abytes / (ams * 1e-3) / 1e9 / PEAK_HBM_GBS, 4))
         roofline = {
             "bound": "hbm",
-            "kernel": "short_bx_kernel (X' = a X + B X, 64-row iterate)",
+            "kernel": "short_bx_kernel<-1> (X' = a X + B X, 64-row iterate)",
             "achieved": round(achieved, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",

@@ -67,6 +67,9 @@ int muon_launch_short_poly(const OrthLayout& L, float* part, void* bm, int64_t b
 int muon_launch_short_bx(const OrthLayout& L, const void* x, void* xo, const void* bm,
                          float* part, int64_t batch, float alpha, float beta, const float* scale,
                          int first, int gram, hipStream_t s);
+int muon_launch_short_bx_apply(const OrthLayout& L, const void* x, const void* bm,
+                               int64_t batch, float alpha, float beta, const float* scale,
+                               int first, const MuonApply& ap, hipStream_t s);
 
 enum { MODE_GEMM = 0, MODE_SYRK = 1 };
 
@@ -403,7 +406,10 @@ static int orth_run_impl(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch
         rc = muon_launch_short_poly(L, part, B, batch, c, b, scale, first, s);
       }
       if (rc != MUON_OK) return rc;
-      {
+      if (ap && !more) {
+        Timed t(MUON_K_GEMM_BX_APPLY, bm * 2.0 * md * md * nd, s);
+        rc = muon_launch_short_bx_apply(L, X[it & 1], B, batch, 1.0f, a, scale, first, *ap, s);
+      } else {
         Timed t(MUON_K_GEMM_BX, bm * 2.0 * md * md * nd + (more ? bm * md * (md + 1) * nd : 0.0), s);
         rc = muon_launch_short_bx(L, X[it & 1], X[(it + 1) & 1], B, part, batch, 1.0f, a, scale,
                                   first, more, s);
@@ -472,7 +478,9 @@ int muon_orth_run_apply(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch,
   if (fuse) {
     const OrthLayout L = muon_orth_layout(ws_dtype, ws_batch, rows, cols);
     const int64_t kq = std::min(L.m_pad, round_up(L.m, 128));
-    fuse = !L.short_m && kq >= 1024;
+    // the tiled path from K = 1024; iterates of at most 64 rows when the parameter is wide
+    // (its rows are the iterate's)
+    fuse = L.short_m ? !L.tall : kq >= 1024;
     for (int t = 0; fuse && t < ntensors; ++t) fuse = params[t] && !((uintptr_t)params[t] & 15);
   }
   if (!fuse) {

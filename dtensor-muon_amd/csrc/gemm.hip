@@ -1904,9 +1904,8 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g, Muon
       auto voff = [&](int p, int i) -> int {
         return vcol && lr < vrows - (p * 32 + 4 * i) ? vop : (int)0x80000000;
       };
-      // apply_elem<bf16, bf16> in three straight forms (one kernel each; wd and cautious are
-      // uniform), the same operations in the same order: MODE 1 cautious weight decay, 2 plain
-      // weight decay, 0 no weight decay (the bf16-rounded step)
+      // apply_elem<bf16, bf16> in three straight forms (apply_bf16x8, one kernel each: MODE 1
+      // cautious weight decay, 2 plain weight decay, 0 no weight decay)
       auto rounds = [&](auto mode_c) {
         constexpr int AM = decltype(mode_c)::value;
         u32x4 pv[2][8];
@@ -1926,37 +1925,8 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g, Muon
           for (int i = 0; i < 8; ++i) {
             const uint32_t c = lc ^ ((4 * i + lr) & 15);
             const u32x4 q4 = *(const u32x4 __attribute__((address_space(3)))*)(epr + i * 1024 + (c << 4));
-            const u32x4 pq = pv[p & 1][i];
-            uint32_t ow[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              uint32_t r[2];
-#pragma unroll
-              for (int hh = 0; hh < 2; ++hh) {
-                const float u = __uint_as_float(hh ? q4[e] & 0xffff0000u : q4[e] << 16);
-                const float pp = __uint_as_float(hh ? pq[e] & 0xffff0000u : pq[e] << 16);
-                float o;
-                {
-#pragma clang fp contract(off)
-                  if constexpr (AM == 1) {
-                    const float prod = u * pp;
-                    const float m = prod > 0.0f ? 1.0f : 0.0f;
-                    const float tt = (ap.wd * pp) * m;
-                    o = pp - adj * (u + tt);
-                  } else if constexpr (AM == 2) {
-                    o = pp - adj * (u + ap.wd * pp);
-                  } else {
-                    o = pp - bf16_to_f32(f32_to_bf16(adjr * u));
-                  }
-                }
-                // round to nearest even in the high half; NaN -> 0x7fc0 (as f32_to_bf16)
-                const uint32_t x = __float_as_uint(o);
-                r[hh] = o != o ? 0x7fc00000u : x + 0x7fffu + ((x >> 16) & 1u);
-              }
-              ow[e] = __builtin_amdgcn_perm(r[1], r[0], 0x07060302u);
-            }
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{ow[0], ow[1], ow[2], ow[3]}, rsp,
-                                                   voff(p, i), (p * 32 + 4 * i) * ldp_b, 2);
+            const u32x4 o4 = apply_bf16x8<AM>(q4, pv[p & 1][i], adj, adjr, ap.wd);
+            __builtin_amdgcn_raw_buffer_store_b128(o4, rsp, voff(p, i), (p * 32 + 4 * i) * ldp_b, 2);
           }
         }
       };

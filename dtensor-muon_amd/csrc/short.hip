@@ -18,6 +18,7 @@
 // accumulation of bf16 products, A and B rounded to bf16 once, X' = alpha (acc + ratio X)
 // rounded once; only the summation order of the Gram sums differs (column ranges).
 #include <algorithm>
+#include <cstring>
 
 #include "common.h"
 
@@ -48,6 +49,7 @@ struct ShortArgs {
   const float* scale;  // per-matrix Frobenius prescale s
   int first;           // fold s in (A *= s^2; alpha, beta *= s)
   int gram;            // short_bx_kernel: write the next iteration's partials
+  int64_t b0;          // index of this launch's matrix 0 in the bucket (the apply's tensors)
 };
 
 // Column range [pb, pe) of panels for range p: balanced, non-empty when P <= panels.
@@ -208,7 +210,12 @@ MUON_DEVICE int sg_swz(int row) { return (((row >> 1) & 1) << 2) | ((row >> 2) &
 // consumed) and leaves as whole 128-byte row pieces. The bf16 X' of rows i and i + 32
 // in the same registers forms the Gram fragments of the next iteration (16 columns per
 // fragment: lane l holds columns 16 h + 4 (l / 32) + {0..3, 8..11}).
-__global__ __launch_bounds__(256) void short_bx_kernel(ShortArgs a) {
+// AM >= 0 (the last iteration of a wide bucket of bf16 parameters): X' is not stored; each
+// 16-byte piece of it is the update of 8 parameter elements, applied as the post-pass does
+// (apply_bf16x8, form AM) and the parameter written back. The parameter pieces of a panel
+// load before the next panel's X, so waiting for them never waits for that prefetch.
+template <int AM>
+__global__ __launch_bounds__(256) void short_bx_kernel(ShortArgs a, MuonApply ap) {
   __shared__ __align__(16) float red[4 * SG_PART];  // sub-panels (32 KB), then partials
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int p = blockIdx.x, b = blockIdx.y;
@@ -240,6 +247,29 @@ __global__ __launch_bounds__(256) void short_bx_kernel(ShortArgs a) {
   const bf16_t* xs = a.x + loff;
   bf16_t* xd = a.xo + loff;
   uint4 cur[8];
+  // apply: parameter element (row, col) of this matrix at byte row * ldp_b + 2 col from prm;
+  // a lane outside the parameter takes an offset past the descriptor's range (its loads read
+  // zeros, its stores are dropped)
+  bf16_t* prm = nullptr;
+  int ldp_b = 0, vop = 0;
+  float adj = 0.0f, adjr = 0.0f;
+  muon_u32x4 pv[8];
+  if constexpr (AM >= 0) {
+    const int64_t bg = a.b0 + b;
+    const int t = (int)(bg / ap.nb);
+    const int64_t mb = bg - (int64_t)t * ap.nb;
+    prm = (bf16_t*)ap.params[t] + mb * ap.prows * ap.pcols;
+    ldp_b = (int)(ap.pcols * 2);
+    vop = lr * ldp_b + (wave * 64 + lc * 8) * 2;
+    adj = ap.adj[t];
+    adjr = bf16_to_f32(f32_to_bf16(adj));
+  }
+  const __amdgpu_buffer_rsrc_t rsp =
+      __builtin_amdgcn_make_buffer_rsrc((void*)prm, 0, AM >= 0 ? 0x7fffffff : 0, 0x00020000);
+  auto pvoff = [&](int pn, int t) -> int {
+    return 8 * t + lr < ap.prows && pn * SG_PANEL + wave * 64 + lc * 8 < ap.pcols ? vop
+                                                                                  : (int)0x80000000;
+  };
   auto load = [&](int pn) {
     const int64_t o = (int64_t)pn * SG_PANEL;
 #pragma unroll
@@ -260,6 +290,11 @@ __global__ __launch_bounds__(256) void short_bx_kernel(ShortArgs a) {
     // the transposing reads return other lanes' data: keep every LDS access of the
     // wave in program order (LDS serves one wave's accesses in order)
     asm volatile("" ::: "memory");
+    if constexpr (AM >= 0) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        pv[t] = __builtin_amdgcn_raw_buffer_load_b128(rsp, pvoff(pn, t), 8 * t * ldp_b + pn * 2 * SG_PANEL, 2);
+    }
     if (pn + 1 < pe) load(pn + 1);
 #pragma unroll
     for (int fn = 0; fn < 2; ++fn) {
@@ -298,7 +333,7 @@ __global__ __launch_bounds__(256) void short_bx_kernel(ShortArgs a) {
           *(u32x2*)pos = w[fm][rg];
         }
       }
-      if (a.gram) {
+      if (AM < 0 && a.gram) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const bf16x8_mfma h0 = as_frag(uint4{w[0][2 * h].x, w[0][2 * h].y, w[0][2 * h + 1].x, w[0][2 * h + 1].y});
@@ -314,11 +349,18 @@ __global__ __launch_bounds__(256) void short_bx_kernel(ShortArgs a) {
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const int row = 8 * t + lr;
-      st_nt(xd + o + 8 * t * a.pitch, *(const uint4*)(reg + row * 128 + ((lc ^ sg_swz(row)) << 4)));
+      const uint4 xw = *(const uint4*)(reg + row * 128 + ((lc ^ sg_swz(row)) << 4));
+      if constexpr (AM >= 0) {
+        const muon_u32x4 u4 = {xw.x, xw.y, xw.z, xw.w};
+        __builtin_amdgcn_raw_buffer_store_b128(apply_bf16x8<AM>(u4, pv[t], adj, adjr, ap.wd), rsp,
+                                               pvoff(pn, t), 8 * t * ldp_b + pn * 2 * SG_PANEL, 2);
+      } else {
+        st_nt(xd + o + 8 * t * a.pitch, xw);
+      }
     }
     asm volatile("" ::: "memory");
   }
-  if (a.gram) short_write_partial(a, red, g00, g01, g11, b, p);
+  if (AM < 0 && a.gram) short_write_partial(a, red, g00, g01, g11, b, p);
 }
 
 }  // namespace
@@ -366,13 +408,34 @@ int muon_launch_short_poly(const OrthLayout& L, float* part, void* bm, int64_t b
   return MUON_OK;
 }
 
-int muon_launch_short_bx(const OrthLayout& L, const void* x, void* xo, const void* bm,
-                         float* part, int64_t batch, float alpha, float beta, const float* scale,
-                         int first, int gram, hipStream_t s) {
+// X' = alpha B X + beta X of a short iterate (ap == nullptr: into xo, with the next partials
+// when gram), or the last iteration with the apply of a wide bucket of bf16 parameters
+// (ap: X' is not stored, the parameters are updated in place; no partials).
+static int launch_short_bx(const OrthLayout& L, const void* x, void* xo, const void* bm,
+                           float* part, int64_t batch, float alpha, float beta,
+                           const float* scale, int first, int gram, const MuonApply* ap,
+                           hipStream_t s) {
   if (alpha == 0.0f) {
     muon_set_error("short_bx: alpha must be nonzero");
     return MUON_ERR_ARG;
   }
+  int mode = -1;
+  MuonApply none;
+  memset(&none, 0, sizeof(none));
+  none.nb = 1;
+  if (ap) {
+    if (L.tall || ap->prows > L.m || ap->pcols > L.n || ap->pcols % 8 || ap->nb <= 0 ||
+        (batch + ap->nb - 1) / ap->nb > MUON_APPLY_MAX ||
+        // every byte offset the kernel forms (rows up to 64, plus the out-of-range marker
+        // 2^31 for lanes outside the parameter) stays below 2^32
+        (int64_t)SG_ROWS * ap->pcols * 2 + SG_PANEL * 2 > (int64_t)0x7fffffff) {
+      muon_set_error("short_bx: apply does not fit this layout");
+      return MUON_ERR_ARG;
+    }
+    mode = ap->wd == 0.0f ? 0 : (ap->cautious ? 1 : 2);
+    gram = 0;
+  }
+  const MuonApply& apv = ap ? *ap : none;
   ShortArgs a = {};
   a.x = (const bf16_t*)x;
   a.xo = (bf16_t*)xo;
@@ -390,13 +453,32 @@ int muon_launch_short_bx(const OrthLayout& L, const void* x, void* xo, const voi
   for (int64_t b0 = 0; b0 < batch; b0 += SG_GRID_Y) {
     ShortArgs c = a;
     c.x += b0 * c.mstride;
-    c.xo += b0 * c.mstride;
+    if (c.xo) c.xo += b0 * c.mstride;
     c.bm += b0 * SG_ROWS * SG_ROWS;
-    c.part += b0 * c.P * SG_PART;
+    if (c.part) c.part += b0 * c.P * SG_PART;
     c.scale = scale ? scale + b0 : nullptr;
+    c.b0 = b0;
     const int64_t nb = std::min<int64_t>(SG_GRID_Y, batch - b0);
-    hipLaunchKernelGGL(short_bx_kernel, dim3((unsigned)c.P, (unsigned)nb), dim3(256), 0, s, c);
+    const dim3 grid((unsigned)c.P, (unsigned)nb);
+    switch (mode) {
+      case 0: hipLaunchKernelGGL(short_bx_kernel<0>, grid, dim3(256), 0, s, c, apv); break;
+      case 1: hipLaunchKernelGGL(short_bx_kernel<1>, grid, dim3(256), 0, s, c, apv); break;
+      case 2: hipLaunchKernelGGL(short_bx_kernel<2>, grid, dim3(256), 0, s, c, apv); break;
+      default: hipLaunchKernelGGL(short_bx_kernel<-1>, grid, dim3(256), 0, s, c, apv); break;
+    }
   }
   MUON_CHECK_LAUNCH("short_bx");
   return MUON_OK;
+}
+
+int muon_launch_short_bx(const OrthLayout& L, const void* x, void* xo, const void* bm,
+                         float* part, int64_t batch, float alpha, float beta, const float* scale,
+                         int first, int gram, hipStream_t s) {
+  return launch_short_bx(L, x, xo, bm, part, batch, alpha, beta, scale, first, gram, nullptr, s);
+}
+
+int muon_launch_short_bx_apply(const OrthLayout& L, const void* x, const void* bm,
+                               int64_t batch, float alpha, float beta, const float* scale,
+                               int first, const MuonApply& ap, hipStream_t s) {
+  return launch_short_bx(L, x, nullptr, bm, nullptr, batch, alpha, beta, scale, first, 0, &ap, s);
 }

@@ -6,8 +6,9 @@ equal: the fused epilogue applies muon.py:58-77 (cautious weight decay, the shap
 step; with wd = 0 the bf16-rounded step) to each bf16 element of the last iterate exactly as
 the post-pass does from the stored U. Wide matrices, tall ones (whose last product runs
 with swapped MFMA operands so its accumulators hold parameter rows), partial edge tiles,
-stacked 3D tensors, and the shapes that fall back to the two calls (fp32 parameters, a short
-side below 1024 after padding to 128 rows, fp16 parameters).
+stacked 3D tensors, iterates of at most 64 rows (the short path's last product, wide
+parameters), and the shapes that fall back to the two calls (fp32 parameters, a short side
+from 65 to below 1024 after padding to 128 rows, fp16 parameters, tall short parameters).
 """
 
 import pytest
@@ -68,6 +69,10 @@ def _case(shape, count, dtype, seed):
     ((1100, 1536), 2),     # wide, partial last tile row (1100 of 1280 rows)
     ((1800, 1032), 2),     # tall, partial tiles both ways
     ((2, 1024, 1280), 2),  # stacked: two matrices per tensor
+    ((64, 8192), 3),       # iterate of at most 64 rows: the short path's last B X
+    ((48, 5000), 2),       # short, padding rows 48-63 and a partial last column panel
+    ((3, 32, 4096), 2),    # short, stacked
+    ((64, 1408 * 2048), 1),  # a flattened MoE expert stack
 ])
 @pytest.mark.parametrize("wd,cautious", [(0.1, True), (0.1, False), (0.0, True)])
 def test_fused_apply_matches_postpass_bit_for_bit(shape, count, wd, cautious):
@@ -90,6 +95,8 @@ def test_fused_apply_matches_postpass_bit_for_bit(shape, count, wd, cautious):
     ((1024, 2048), torch.float32),   # fp32 parameters: the separate post-pass
     ((512, 2048), torch.bfloat16),   # short side 512 < 1024: the separate post-pass
     ((2048, 1024), torch.float16),
+    ((4096, 64), torch.bfloat16),    # tall with at most 64 columns: the separate post-pass
+    ((64, 4096), torch.float32),     # short, fp32 parameters
 ])
 def test_fallback_shapes_match_postpass(shape, dtype):
     p, g, b = _case(shape, 2, dtype, seed=5)
@@ -160,3 +167,22 @@ def test_fused_apply_nonfinite_matches_postpass_bitwise(shape, wd, cautious):
     for i, (x, y) in enumerate(zip(pa, pb)):
         xi, yi = x.view(torch.int16), y.view(torch.int16)
         assert torch.equal(xi, yi), f"tensor {i}: {(xi != yi).sum().item()} bit patterns differ"
+
+
+def test_flattened_stack_step_takes_the_short_fused_apply():
+    """flatten=True makes a (16, 48, 320) tensor one (16, 15360) matrix: an iterate of at
+    most 64 rows, whose last B X carries the apply (its timing kind records the launch and no
+    post-pass runs); parameters against the oracle are pinned by test_short_gpu.py."""
+    from muonium_amd import Muon
+
+    gen = torch.Generator().manual_seed(13)
+    p = torch.nn.Parameter(torch.randn(16, 48, 320, generator=gen).bfloat16().to(DEV))
+    p.grad = torch.randn(16, 48, 320, generator=gen).bfloat16().to(DEV)
+    p_init = p.detach().clone()
+    opt = Muon([{"params": [p], "flatten": True}], lr=0.02, foreach=True)
+    _lib.timing_enable(True)
+    opt.step()
+    kern = _lib.timing_read()
+    _lib.timing_enable(False)
+    assert kern["gemm_bx_apply"][1] == 1 and kern["postpass"][1] == 0
+    assert not torch.equal(p.detach(), p_init)
