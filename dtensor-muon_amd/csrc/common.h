@@ -245,38 +245,41 @@ MUON_DEVICE float apply_elem(float p, float u, float wd, int cautious, float adj
 // (pq), 16 bytes each, in one of three straight forms (wd and cautious are uniform over a
 // launch): AM 1 cautious weight decay, 2 plain weight decay, 0 no weight decay (the
 // bf16-rounded step, adjr = bf16(adj)). The same operations in the same order as
-// apply_elem, rounded to nearest even with NaN -> 0x7fc0 as f32_to_bf16, so a fused apply
-// writes the post-pass's parameters bit for bit.
+// apply_elem, and the same rounding as f32_to_bf16: v_cvt_pk_bf16_f32 rounds two values to
+// nearest even (IEEE, denormals kept), and a NaN result becomes 0x7fc0 whatever its sign
+// and payload. So a fused apply writes the post-pass's parameters bit for bit.
 typedef __attribute__((ext_vector_type(4))) unsigned int muon_u32x4;
+typedef __attribute__((ext_vector_type(2))) float muon_f2x;
+typedef __attribute__((ext_vector_type(2))) __bf16 muon_bf2x;
 template <int AM>
 MUON_DEVICE muon_u32x4 apply_bf16x8(muon_u32x4 q4, muon_u32x4 pq, float adj, float adjr,
                                     float wd) {
   uint32_t ow[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    uint32_t r[2];
+    float o[2];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const float u = __uint_as_float(hh ? q4[e] & 0xffff0000u : q4[e] << 16);
       const float pp = __uint_as_float(hh ? pq[e] & 0xffff0000u : pq[e] << 16);
-      float o;
       {
 #pragma clang fp contract(off)
         if constexpr (AM == 1) {
           const float prod = u * pp;
           const float m = prod > 0.0f ? 1.0f : 0.0f;
           const float tt = (wd * pp) * m;
-          o = pp - adj * (u + tt);
+          o[hh] = pp - adj * (u + tt);
         } else if constexpr (AM == 2) {
-          o = pp - adj * (u + wd * pp);
+          o[hh] = pp - adj * (u + wd * pp);
         } else {
-          o = pp - bf16_to_f32(f32_to_bf16(adjr * u));
+          o[hh] = pp - bf16_to_f32(f32_to_bf16(adjr * u));
         }
       }
-      const uint32_t x = __float_as_uint(o);
-      r[hh] = o != o ? 0x7fc00000u : x + 0x7fffu + ((x >> 16) & 1u);
     }
-    ow[e] = __builtin_amdgcn_perm(r[1], r[0], 0x07060302u);
+    uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(muon_f2x{o[0], o[1]}, muon_bf2x));
+    w = o[0] != o[0] ? (w & 0xffff0000u) | 0x7fc0u : w;
+    w = o[1] != o[1] ? (w & 0x0000ffffu) | 0x7fc00000u : w;
+    ow[e] = w;
   }
   return muon_u32x4{ow[0], ow[1], ow[2], ow[3]};
 }
