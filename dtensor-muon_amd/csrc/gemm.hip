@@ -2125,9 +2125,12 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_s16_kernel(GemmArgs g) {
   // waves 4 and 5 blocks (1, 0) and (3, 1), of which only column blocks 4-7 reach the upper
   // triangle (mode 1), waves 6 and 7 blocks (2, 0) and (3, 0), wholly below it (mode 2: no
   // MFMAs). The a and b panels of a diagonal tile are the same rows: only the a panel is
-  // loaded, and the b fragments are read from it.
+  // loaded, and the b fragments are read from it. This applies to A A and to X X^T with
+  // K <= 4096; X X^T over longer rows (K = 14336) ran 1 ms per Llama step slower in this form
+  // and keeps whole 64 x 128 blocks and both panels (the epilogue treats its diagonal tiles
+  // as diagonal either way).
   const bool dtile = tm == tn;
-  const bool diag = dtile && g.beta != 0.0f;
+  const bool diag = dtile && (g.beta != 0.0f || g.K <= 4096);
   const int wm = diag ? (0x32312100 >> (4 * wave)) & 15 : wave >> 1;
   const int wn = diag ? (0x00101110 >> (4 * wave)) & 15 : wave & 1;
   const int wmode = diag ? (0x22110000 >> (4 * wave)) & 15 : 0;
