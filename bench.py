@@ -401,6 +401,9 @@ def main() -> None:
                     help="MuonLP block size (default 256, 4-bit 128), or 'tensor' for one "
                          "scale per tensor")
     ap.add_argument("--strategy", default=None)
+    ap.add_argument("--algorithm", default="muon", choices=["muon", "normuon"],
+                    help="the param group's algorithm (normuon: per-row variance state and "
+                         "its post-pass)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device-to-device copy 5 times (PMC calibration)")
@@ -488,6 +491,8 @@ def main() -> None:
     kw = dict(lr=1e-3, wd=0.1, use_cautious_wd=True, momentum=0.95, nesterov=True, ns_steps=5,
               orthogonalization_strategy=strategy)
     groups = [{"params": params, "flatten": flatten}]  # flatten is a group key
+    if args.algorithm != "muon":
+        groups[0]["algorithm"] = args.algorithm
     if args.lp:
         cls = {"8bit": Muon8bit, "4bit": Muon4bit, "fp8": MuonFp8}[args.lp]
         if args.block_size == "tensor":
@@ -672,7 +677,8 @@ def main() -> None:
         "data": "synthetic (seeded N(0,1) gradients with per-row log-normal scales; random-init bf16 params)",
         "config": {
             "workload": label + (f"; MuonLP {args.lp}, block {block or 'per tensor'}"
-                                 if args.lp else ""),
+                                 if args.lp else "") + ("; NorMuon" if args.algorithm == "normuon" else ""),
+            "algorithm": args.algorithm,
             "params": numel,
             "strategy": strategy,
             "ns_steps": 5,

@@ -612,6 +612,55 @@ __global__ __launch_bounds__(256) void row_sumsq_kernel(RowSsArgs a) {
   }
 }
 
+// The transposed case with 16-byte loads: row r of the update is column r of the stored
+// result (tall matrices), so a lane takes 8 consecutive rows (8 consecutive elements of a
+// stored row) and a workgroup 512 rows; wave w sums stored rows w, w + 4, ... with four
+// loads in flight. The same sums in the same order as row_sumsq_kernel<UDT, 1, true>.
+// Needs rows % 8 == 0 and 16-byte aligned stored rows.
+template <int UDT>
+__global__ __launch_bounds__(256) void row_sumsq_t8_kernel(RowSsArgs a) {
+#pragma clang fp contract(off)
+  __shared__ float part[4][512];
+  const int mat = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t rb = (int64_t)blockIdx.x * 512;
+  const int64_t r = rb + lane * 8;
+  const int64_t base = (int64_t)mat * a.u_mstride;
+  float* ss = a.ss + (int64_t)mat * a.ss_mstride;
+  const float us = a.uscale[mat / a.nb];
+  float s[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  if (r < a.rows) {
+    int64_t c = wave;
+    for (; c + 12 < a.cols; c += 16) {
+      float v[4][8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) Vec8<UDT>::load(a.u, base + (c + 4 * q) * a.u_pitch + r, v[q]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = a.has_uscale ? Elem<UDT>::round(v[q][e] * us) : v[q][e];
+          s[e] += x * x;
+        }
+      }
+    }
+    for (; c < a.cols; c += 4) {
+      float v[8];
+      Vec8<UDT>::load(a.u, base + c * a.u_pitch + r, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = a.has_uscale ? Elem<UDT>::round(v[e] * us) : v[e];
+        s[e] += x * x;
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) part[wave][lane * 8 + e] = s[e];
+  __syncthreads();
+  for (int k = tid; k < 512; k += 256) {
+    if (rb + k < a.rows) ss[rb + k] = ((part[0][k] + part[1][k]) + part[2][k]) + part[3][k];
+  }
+}
+
 // Per (row block, matrix): v' = lerp(v, ss / cols, w) into the variance state, row
 // multipliers d = 1 / (sqrt(v') + 1e-8), and the Frobenius rescale
 // f = ||U|| / max(||U d||, 1e-8) with ||U||^2 = sum ss and ||U d||^2 = sum ss d^2 (double,
@@ -1055,9 +1104,14 @@ int muon_launch_normuon_stats(int ntensors, void* const* vars, int vdt, const vo
   dim3 grid((unsigned)((rows + 63) / 64), (unsigned)nmat);
   const bool vec8 = !u_trans && (cols % 8) == 0 && (u_pitch % 8) == 0 && (u_mstride % 8) == 0 &&
                     !((uintptr_t)u & 15);
+  const bool t8 = u_trans && (rows % 8) == 0 && (u_pitch % 8) == 0 && (u_mstride % 8) == 0 &&
+                  !((uintptr_t)u & 15);
+  const dim3 grid8((unsigned)((rows + 511) / 512), (unsigned)nmat);
 #define ROWSS(UDT_)                                                                        \
   do {                                                                                     \
-    if (u_trans)                                                                           \
+    if (t8)                                                                                \
+      hipLaunchKernelGGL((row_sumsq_t8_kernel<UDT_>), grid8, dim3(256), 0, s, ra);          \
+    else if (u_trans)                                                                      \
       hipLaunchKernelGGL((row_sumsq_kernel<UDT_, 1, true>), grid, dim3(256), 0, s, ra);     \
     else if (vec8)                                                                         \
       hipLaunchKernelGGL((row_sumsq_kernel<UDT_, 8, false>), grid, dim3(256), 0, s, ra);    \
