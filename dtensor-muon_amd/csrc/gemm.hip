@@ -2381,6 +2381,17 @@ int device_cus() {
   return n;
 }
 
+// Workgroups of a persistent launch over `blocks` tiles: as many rounds as one workgroup per
+// CU needs, with the tiles spread evenly over them (a launch of a few hundred tiles leaves
+// the CUs it does not need to kernels on other streams instead of idling them in its last
+// round). Unchanged when the tile count is a multiple of the CU count.
+static int persistent_wgs(int64_t blocks) {
+  const int64_t cus = device_cus();
+  if (blocks <= cus) return (int)blocks;
+  const int64_t rounds = (blocks + cus - 1) / cus;
+  return (int)((blocks + rounds - 1) / rounds);
+}
+
 }  // namespace
 
 // Launch one batched product. `dtype` selects bf16 (256-tiles) or fp32 (128-tiles).
@@ -2474,8 +2485,8 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
         muon_set_error("gemm: bf16 NN products take K a multiple of 128 and no transposed output");
         return MUON_ERR_ARG;
       }
-      // persistent: one workgroup per CU walks the tile list
-      const int wgs = (int)std::min<int64_t>(blocks, device_cus());
+      // persistent: at most one workgroup per CU walks the tile list
+      const int wgs = persistent_wgs(blocks);
       if (K >= 1024) {
         MuonApply none;
         none.nb = 1;
@@ -2572,7 +2583,7 @@ int muon_launch_gemm_apply(int64_t batch, int64_t M, int64_t N, int64_t K, const
     muon_set_error("gemm_apply: cannot reserve LDS");
     return MUON_ERR_LAUNCH;
   }
-  const int wgs = (int)std::min<int64_t>(blocks, device_cus());
+  const int wgs = persistent_wgs(blocks);
   const int mode = ap.wd == 0.0f ? 0 : (ap.cautious ? 1 : 2);
 #define LAUNCH_APPLY(A, M) \
   hipLaunchKernelGGL((gemm_bf16_nn16_kernel<A, M>), dim3((unsigned)wgs), dim3(256), N4_SMEM, stream, g, ap)
