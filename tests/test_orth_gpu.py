@@ -109,6 +109,19 @@ def test_batched_equals_unbatched_exactly(strategy):
         assert torch.equal(u, zeropower(x, strategy=strategy))
 
 
+@pytest.mark.parametrize("shape,count", [((1024, 1280), 20), ((768, 1280), 20), ((1100, 1536), 9)])
+def test_uneven_persistent_grid_equals_single_matrices(shape, count):
+    """Batches whose B X tile count exceeds the CU count without being a multiple of it
+    (400, 300 and 270 tiles: 200, 150 and 135 workgroups walking two tiles each, K = 1024 on
+    the 16 x 16 x 32 kernel, 768 on the 32 x 32 x 16 one, and partial edge tiles) give every
+    matrix bit for bit what it gets alone, whose few tiles take one workgroup each."""
+    gen = torch.Generator(device="cuda").manual_seed(sum(shape) + count)
+    xs = [torch.randn(shape, generator=gen, device="cuda").bfloat16() for _ in range(count)]
+    batched = foreach_zeropower(xs, strategy="polar_express")
+    for i, (x, u) in enumerate(zip(xs, batched)):
+        assert torch.equal(u, zeropower(x, strategy="polar_express")), f"matrix {i}"
+
+
 def test_iteration_is_deterministic():
     X = _inputs((4, 300, 200), seed=4).cuda()
     assert torch.equal(zeropower(X, strategy="polar_express"),
