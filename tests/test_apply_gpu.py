@@ -186,3 +186,18 @@ def test_flattened_stack_step_takes_the_short_fused_apply():
     _lib.timing_enable(False)
     assert kern["gemm_bx_apply"][1] == 1 and kern["postpass"][1] == 0
     assert not torch.equal(p.detach(), p_init)
+
+
+def test_more_tensors_than_the_apply_holds_fall_back_to_the_post_pass():
+    """A bucket of 130 tensors (more than the 128 the fused epilogue's table holds) runs the
+    iteration and then the post-pass inside muon_orth_run_apply: parameters bit for bit those
+    of the two separate calls."""
+    p, g, b = _case((1024, 1024), 130, torch.bfloat16, seed=130)
+    pa = [t.clone().to(DEV) for t in p]
+    pb = [t.clone().to(DEV) for t in p]
+    ga, gb = [t.clone().to(DEV) for t in g], [t.clone().to(DEV) for t in g]
+    ba, bb = [t.clone().to(DEV) for t in b], [t.clone().to(DEV) for t in b]
+    _run(pa, ga, ba, fused=True, wd=0.1, cautious=True)
+    _run(pb, gb, bb, fused=False, wd=0.1, cautious=True)
+    for i, (x, y) in enumerate(zip(pa, pb)):
+        assert torch.equal(x, y), f"tensor {i}"
