@@ -354,9 +354,44 @@ int muon_prepass(int ntensors, void* const* grads, void* const* bufs, int g_dtyp
 
 // The iteration; with `ap` (eligible shapes only, checked by the caller) the last X' is
 // not stored but applied to the parameters in the GEMM's epilogue.
+// The parameters of a fused apply: per tensor a bf16 pointer and lr * lr_ratio, nb matrices
+// of prows x pcols each, wd and cautious. The last product's launches take them in chunks of
+// at most MUON_APPLY_MAX tensors (the table a launch carries).
+struct ApplyReq {
+  void* const* params;
+  const float* adj;
+  int ntensors;
+  int64_t nb, prows, pcols;
+  float wd;
+  int cautious;
+};
+
+// Run `launch(m0, cnt, table)` for consecutive chunks of the apply's tensors: matrices
+// m0 .. m0 + cnt - 1 of the launch, the chunk's table.
+extern "C++" template <typename F>
+static int apply_chunks(const ApplyReq& r, F&& launch) {
+  MuonApply ap;
+  memset(&ap, 0, sizeof(ap));
+  ap.nb = r.nb;
+  ap.prows = r.prows;
+  ap.pcols = r.pcols;
+  ap.wd = r.wd;
+  ap.cautious = r.cautious;
+  for (int t0 = 0; t0 < r.ntensors; t0 += MUON_APPLY_MAX) {
+    const int cnt = std::min(MUON_APPLY_MAX, r.ntensors - t0);
+    for (int t = 0; t < cnt; ++t) {
+      ap.params[t] = r.params[t0 + t];
+      ap.adj[t] = r.adj[t0 + t];
+    }
+    const int rc = launch((int64_t)t0 * r.nb, (int64_t)cnt * r.nb, ap);
+    if (rc != MUON_OK) return rc;
+  }
+  return MUON_OK;
+}
+
 static int orth_run_impl(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64_t rows,
                          int64_t cols, const double* coeffs, int steps, float prescale,
-                         float eps, const MuonApply* ap, void* stream) {
+                         float eps, const ApplyReq* ap, void* stream) {
   if (!iter_dtype_ok(ws_dtype)) {
     muon_set_error("orth_run: unsupported dtype %d", ws_dtype);
     return MUON_ERR_DTYPE;
@@ -408,7 +443,11 @@ static int orth_run_impl(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch
       if (rc != MUON_OK) return rc;
       if (ap && !more) {
         Timed t(MUON_K_GEMM_BX_APPLY, bm * 2.0 * md * md * nd, s);
-        rc = muon_launch_short_bx_apply(L, X[it & 1], B, batch, 1.0f, a, scale, first, *ap, s);
+        const int64_t xs = 64 * L.n_pad * 2, bs = 64 * 64 * 2;  // bytes per matrix
+        rc = apply_chunks(*ap, [&](int64_t m0, int64_t cnt, const MuonApply& tab) {
+          return muon_launch_short_bx_apply(L, X[it & 1] + m0 * xs, B + m0 * bs, cnt, 1.0f, a,
+                                            scale + m0, first, tab, s);
+        });
       } else {
         Timed t(MUON_K_GEMM_BX, bm * 2.0 * md * md * nd + (more ? bm * md * (md + 1) * nd : 0.0), s);
         rc = muon_launch_short_bx(L, X[it & 1], X[(it + 1) & 1], B, part, batch, 1.0f, a, scale,
@@ -447,8 +486,11 @@ static int orth_run_impl(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch
     // result stays in the wide orientation (readers of a tall result transpose on load)
     if (ap && it + 1 == steps) {
       Timed t(MUON_K_GEMM_BX_APPLY, bm * 2.0 * md * md * nd, s);
-      rc = muon_launch_gemm_apply(batch, mp, np, kq, B, mp, mp * mp, Xc, xp, mp * xp, L.m, L.n,
-                                  1.0f, a, scale, first ? 1 : 0, *ap, L.tall, s);
+      rc = apply_chunks(*ap, [&](int64_t m0, int64_t cnt, const MuonApply& tab) {
+        return muon_launch_gemm_apply(cnt, mp, np, kq, B + m0 * mp * mp * 2, mp, mp * mp,
+                                      Xc + m0 * mp * xp * 2, xp, mp * xp, L.m, L.n, 1.0f, a,
+                                      scale + m0, first ? 1 : 0, tab, L.tall, s);
+      });
     } else {
     Timed t(MUON_K_GEMM_BX, bm * 2.0 * md * md * nd, s);
     rc = muon_launch_gemm(ws_dtype, MODE_GEMM, false, batch, mp, np, kq, B, mp, mp * mp, Xc, xp,
@@ -472,8 +514,7 @@ int muon_orth_run_apply(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch,
                         float eps, int ntensors, void* const* params, int p_dtype, int64_t nb,
                         const float* adjusted_lrs, float wd, int cautious, void* stream) {
   bool fuse = ws_dtype == MUON_DT_BF16 && p_dtype == MUON_DT_BF16 && steps > 0 && rows > 0 &&
-              cols > 0 && nb > 0 && ntensors > 0 && ntensors <= MUON_APPLY_MAX &&
-              (int64_t)ntensors * nb == batch && batch <= ws_batch && params && adjusted_lrs &&
+              cols > 0 && nb > 0 && ntensors > 0 && (int64_t)ntensors * nb == batch && batch <= ws_batch && params && adjusted_lrs &&
               cols % 8 == 0;
   if (fuse) {
     const OrthLayout L = muon_orth_layout(ws_dtype, ws_batch, rows, cols);
@@ -490,17 +531,7 @@ int muon_orth_run_apply(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch,
     return muon_postpass(ntensors, params, p_dtype, nullptr, 0, ws, ws_dtype, ws_batch, steps,
                          nb, rows, cols, adjusted_lrs, nullptr, wd, cautious, stream);
   }
-  MuonApply ap;
-  memset(&ap, 0, sizeof(ap));
-  for (int t = 0; t < ntensors; ++t) {
-    ap.params[t] = params[t];
-    ap.adj[t] = adjusted_lrs[t];
-  }
-  ap.nb = nb;
-  ap.prows = rows;
-  ap.pcols = cols;
-  ap.wd = wd;
-  ap.cautious = cautious;
+  const ApplyReq ap = {params, adjusted_lrs, ntensors, nb, rows, cols, wd, cautious};
   return orth_run_impl(ws, ws_dtype, ws_batch, batch, rows, cols, coeffs, steps, prescale, eps,
                        &ap, stream);
 }

@@ -118,9 +118,9 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
  * with the post-pass fused into the last iteration's X = a*X + B X where the shapes allow
  * (bf16 workspace and parameters; on the iterate's short side either at least 1024 valid
  * rows after padding to 128, or at most 64 rows with the parameter stored wide;
- * ntensors * nb == batch, at most 128 tensors, parameter rows a multiple of 8 elements in
- * the stored orientation, 16-byte aligned parameters): each bf16 element of the last X' is
- * applied to its parameter element
+ * ntensors * nb == batch, parameter rows a multiple of 8 elements in the stored
+ * orientation, 16-byte aligned parameters; the last product launches once per 128 tensors):
+ * each bf16 element of the last X' is applied to its parameter element
  * (cautious weight decay and the shape-scaled step, exactly as muon_postpass) and X' is
  * not stored, so the workspace does not hold U afterwards. Otherwise the two calls run
  * one after the other. Replaces the orthogonalize-then-apply sequence of

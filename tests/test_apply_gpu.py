@@ -188,11 +188,12 @@ def test_flattened_stack_step_takes_the_short_fused_apply():
     assert not torch.equal(p.detach(), p_init)
 
 
-def test_more_tensors_than_the_apply_holds_fall_back_to_the_post_pass():
-    """A bucket of 130 tensors (more than the 128 the fused epilogue's table holds) runs the
-    iteration and then the post-pass inside muon_orth_run_apply: parameters bit for bit those
-    of the two separate calls."""
-    p, g, b = _case((1024, 1024), 130, torch.bfloat16, seed=130)
+@pytest.mark.parametrize("shape", [(1024, 1024), (48, 4096)])
+def test_more_tensors_than_one_apply_table(shape):
+    """A bucket of 130 tensors (more than the 128 one launch's table holds): the last product
+    runs as two launches (128 tensors, then 2) on the tiled and on the short path, with
+    parameters bit for bit those of the iteration followed by the post-pass."""
+    p, g, b = _case(shape, 130, torch.bfloat16, seed=130)
     pa = [t.clone().to(DEV) for t in p]
     pb = [t.clone().to(DEV) for t in p]
     ga, gb = [t.clone().to(DEV) for t in g], [t.clone().to(DEV) for t in g]
