@@ -69,6 +69,7 @@ def _case(shape, count, dtype, seed):
     ((1100, 1536), 2),     # wide, partial last tile row (1100 of 1280 rows)
     ((1800, 1032), 2),     # tall, partial tiles both ways
     ((2, 1024, 1280), 2),  # stacked: two matrices per tensor
+    ((3, 1280, 1032), 2),  # stacked tall, partial tiles
     ((64, 8192), 3),       # iterate of at most 64 rows: the short path's last B X
     ((48, 5000), 2),       # short, padding rows 48-63 and a partial last column panel
     ((3, 32, 4096), 2),    # short, stacked
