@@ -547,6 +547,40 @@ MUON_DEVICE void mfma_substep(f32x16 (&acc)[2][4], const bf16x8_mfma (&ca)[2],
       : [ca0] "v"(ca[0]), [ca1] "v"(ca[1]), [cb0] "v"(cb[0]), [cb1] "v"(cb[1]),
         [cb2] "v"(cb[2]), [cb3] "v"(cb[3]), [aa] "v"(aa), [ba] "v"(ba));
 }
+// The right half of mfma_substep (accumulator columns fn 2-3, a diagonal tile's wave
+// block whose left half lies below the diagonal): 4 MFMAs, reading the next a fragments
+// and b fragments 2-3.
+MUON_DEVICE void mfma_substep_r(f32x16 (&acc)[2][4], const bf16x8_mfma (&ca)[2],
+                                const bf16x8_mfma (&cb)[4], bf16x8_mfma (&na)[2],
+                                bf16x8_mfma (&nb)[4], uint32_t aa, uint32_t ba) {
+  asm volatile(
+      "ds_read_b128 %[na0], %[aa]\n\t"
+      MUON_MFMA(c02, ca0, cb2)
+      "ds_read_b128 %[na1], %[aa] offset:4096\n\t"
+      MUON_MFMA(c03, ca0, cb3)
+      "ds_read_b128 %[nb2], %[ba] offset:8192\n\t"
+      MUON_MFMA(c12, ca1, cb2)
+      "ds_read_b128 %[nb3], %[ba] offset:12288\n\t"
+      MUON_MFMA(c13, ca1, cb3)
+      "s_waitcnt lgkmcnt(0)"
+      : [c02] "+v"(acc[0][2]), [c03] "+v"(acc[0][3]), [c12] "+v"(acc[1][2]),
+        [c13] "+v"(acc[1][3]), [na0] "=&v"(na[0]), [na1] "=&v"(na[1]), [nb2] "=&v"(nb[2]),
+        [nb3] "=&v"(nb[3])
+      : [ca0] "v"(ca[0]), [ca1] "v"(ca[1]), [cb2] "v"(cb[2]), [cb3] "v"(cb[3]), [aa] "v"(aa),
+        [ba] "v"(ba));
+}
+
+MUON_DEVICE void frag_load_r(bf16x8_mfma (&na)[2], bf16x8_mfma (&nb)[4], uint32_t aa, uint32_t ba) {
+  asm volatile(
+      "ds_read_b128 %[na0], %[aa]\n\t"
+      "ds_read_b128 %[na1], %[aa] offset:4096\n\t"
+      "ds_read_b128 %[nb2], %[ba] offset:8192\n\t"
+      "ds_read_b128 %[nb3], %[ba] offset:12288\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : [na0] "=&v"(na[0]), [na1] "=&v"(na[1]), [nb2] "=&v"(nb[2]), [nb3] "=&v"(nb[3])
+      : [aa] "v"(aa), [ba] "v"(ba));
+}
+
 #undef MUON_MFMA
 
 MUON_DEVICE void frag_load(bf16x8_mfma (&na)[2], bf16x8_mfma (&nb)[4], uint32_t aa, uint32_t ba) {
@@ -655,7 +689,17 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
   const int arows = pk ? 512 : 256;
   const int stageb = (pk ? 640 : 512) * V2_ROWB;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = pk ? wave : wave >> 1, wn = pk ? 0 : wave & 1;
+  // A full diagonal tile (tm == tn) stores only its upper triangle, 10 of its 16 64 x 64
+  // units. For B = b A + c A A, and for X X^T with K <= 4096, its waves take the 64 x 128
+  // blocks in another order so that each SIMD's two waves (w and w + 4) carry 3, 3, 2 and 2
+  // of those units: waves 0-3 compute blocks (0, 0), (0, 1), (1, 1), (2, 1) whole (mode 0),
+  // waves 4 and 5 blocks (1, 0) and (3, 1) only in their right half, accumulator columns
+  // fn 2-3 (mode 1), waves 6 and 7 blocks (2, 0) and (3, 0), wholly below the diagonal, not
+  // at all (mode 2). Its a and b panels are the same rows: only the a panel is loaded.
+  const bool dg = MODE == MODE_SYRK && !pk && tm == tn && (g.beta != 0.0f || g.K <= 4096);
+  const int wm = pk ? wave : (dg ? (0x32312100 >> (4 * wave)) & 15 : wave >> 1);
+  const int wn = pk ? 0 : (dg ? (0x00101110 >> (4 * wave)) & 15 : wave & 1);
+  const int wmode = dg ? (0x22110000 >> (4 * wave)) & 15 : 0;
   const bf16_t* A = (const bf16_t*)g.a + (int64_t)bidx * g.sa;
   const bf16_t* B = (const bf16_t*)g.b + (int64_t)bidx * g.sb;
   const int lda_b = (int)(g.lda * 2), ldb_b = (int)(g.ldb * 2);
@@ -694,6 +738,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
     }
   };
   auto issue_b = [&](int kt, int st) {
+    if (dg) return;
     uint8_t* sb = smem + st * stageb + arows * V2_ROWB;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -710,7 +755,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
   int foff[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) foff[ks] = fr * V2_ROWB + (((ks * 2 + fh) ^ kswz(fr)) << 4);
-  const int abase = wm * WM * V2_ROWB, bbase = arows * V2_ROWB + wn * WN * V2_ROWB;
+  const int abase = wm * WM * V2_ROWB, bbase = (dg ? 0 : arows * V2_ROWB) + wn * WN * V2_ROWB;
 
   float alpha = g.alpha, beta = g.beta;
   if (g.scale_mode != 0) {
@@ -727,6 +772,13 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
   const int64_t wrow = pk && wm >= 4 ? arow1 + (wm - 4) * WM : arow0 + wm * WM;
   const int kdiag = ratio != 0.0f ? (int)(wrow / V2_BK) : -1;
 
+  const int KT = (int)(g.K / V2_BK);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  auto aaddr = [&](int st, int ks) -> uint32_t { return lds0 + st * stageb + abase + foff[ks]; };
+  auto baddr = [&](int st, int ks) -> uint32_t { return lds0 + st * stageb + bbase + foff[ks]; };
+  // one K loop and epilogue per MFMA mode, so no path merges into another's registers
+  auto kloop = [&](auto mode_c) {
+  constexpr int MC = decltype(mode_c)::value;
   f32x16 acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -734,25 +786,30 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
     for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  const int KT = (int)(g.K / V2_BK);
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
-  auto aaddr = [&](int st, int ks) -> uint32_t { return lds0 + st * stageb + abase + foff[ks]; };
-  auto baddr = [&](int st, int ks) -> uint32_t { return lds0 + st * stageb + bbase + foff[ks]; };
+  auto substep = [&](const bf16x8_mfma (&ca)[FM], const bf16x8_mfma (&cb)[FN],
+                     bf16x8_mfma (&na)[FM], bf16x8_mfma (&nb)[FN], uint32_t aa, uint32_t ba) {
+    if constexpr (MC == 0)
+      mfma_substep(acc, ca, cb, na, nb, aa, ba);
+    else if constexpr (MC == 1)
+      mfma_substep_r(acc, ca, cb, na, nb, aa, ba);
+  };
   bf16x8_mfma a0[FM], b0[FN], a1[FM], b1[FN];
   issue_a(0, 0);
   issue_b(0, 0);
   wait_vmcnt0();
   lds_barrier();
   if (KT > 1) issue_a(1, 1);
-  frag_load(a0, b0, aaddr(0, 0), baddr(0, 0));
+  if constexpr (MC == 0)
+    frag_load(a0, b0, aaddr(0, 0), baddr(0, 0));
+  else if constexpr (MC == 1)
+    frag_load_r(a0, b0, aaddr(0, 0), baddr(0, 0));
   for (int kt = 0; kt < KT; ++kt) {
     const int cs = kt & 1;
     if (kt + 1 < KT) issue_b(kt + 1, cs ^ 1);
-    mfma_substep(acc, a0, b0, a1, b1, aaddr(cs, 1), baddr(cs, 1));
-    mfma_substep(acc, a1, b1, a0, b0, aaddr(cs, 2), baddr(cs, 2));
-    mfma_substep(acc, a0, b0, a1, b1, aaddr(cs, 3), baddr(cs, 3));
-    if (kt == kdiag) {
+    substep(a0, b0, a1, b1, aaddr(cs, 1), baddr(cs, 1));
+    substep(a1, b1, a0, b0, aaddr(cs, 2), baddr(cs, 2));
+    substep(a0, b0, a1, b1, aaddr(cs, 3), baddr(cs, 3));
+    if (MC != 2 && kt == kdiag) {
       // cin(i, j) = b(j, i): row j of the b panel, k offset i - kt*BK (4 consecutive
       // rows i of one accumulator group are 8 contiguous bytes of that row)
       mfma_to_valu_wait();
@@ -777,7 +834,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
     wait_vmcnt0();
     lds_barrier();
     if (kt + 2 < KT) issue_a(kt + 2, cs);
-    mfma_substep(acc, a1, b1, a0, b0, aaddr(cs ^ 1, 0), baddr(cs ^ 1, 0));
+    substep(a1, b1, a0, b0, aaddr(cs ^ 1, 0), baddr(cs ^ 1, 0));
   }
   mfma_to_valu_wait();
 
@@ -918,6 +975,13 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_v2_kernel(GemmArgs g) {
       *(uint4*)(out + (arow0 + il) * g.ldo + brow0 + c) = w;
     }
   }
+  };
+  if (wmode == 0)
+    kloop(std::integral_constant<int, 0>{});
+  else if (wmode == 1)
+    kloop(std::integral_constant<int, 1>{});
+  else
+    kloop(std::integral_constant<int, 2>{});
 }
 
 // ----------------------------------------------------------------------------------
@@ -1807,7 +1871,13 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g, Muon
     using no_beta = std::integral_constant<int, -1>;
     int kt = 0;
     if (kd0 >= 0) {
-      for (; kt < kd0; ++kt) kstep(kt, no_beta{});
+      // leaving this loop, the compiler may copy accumulators between registers (to the
+      // assignment the peeled K-tiles use) before any asm that follows the loop; it does not
+      // see the MFMAs in the asm, so the last K-tile of the loop ends with their latency
+      for (; kt < kd0; ++kt) {
+        kstep(kt, no_beta{});
+        if (kt + 1 == kd0) mfma_to_valu_wait();
+      }
       kstep(kt++, std::integral_constant<int, 0>{});
       kstep(kt++, std::integral_constant<int, 4>{});
     }

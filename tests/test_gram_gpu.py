@@ -27,6 +27,10 @@ SHAPES = [
     # whole 256-row tiles, K a multiple of 64: the SYRK reads the caller's tensors in place
     (3, 512, 320),
     (2, 2048, 1024),
+    # m_pad - m = 128: packed tiles for the last tile column (bf16), diagonal tiles remapped
+    # (K <= 4096) or whole (K > 4096)
+    (2, 1408, 2048),
+    (1, 1408, 4160),
 ]
 
 
