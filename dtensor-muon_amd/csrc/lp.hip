@@ -714,6 +714,218 @@ void launch_lp_tile_q(int qf, bool tall, const LpTileArgs& a, dim3 grid, hipStre
   else launch_lp_tile_t<GDT, MUON_Q_FP8, DEFER>(tall, a, grid, s);
 }
 
+// ---- row-segment blocks: 512, 1024 or 2048 values --------------------------------
+// Blocks of 512-2048 values in matrices whose width is a multiple of 2048 (the reference's
+// default block, on every Llama-sized shape). A wavefront owns 2048 consecutive values of
+// one stored row: lane l holds values 8 l .. 8 l + 7 of each 512-value quarter, so a block
+// is one, two or four quarters of one wavefront and its absmax a wave reduction. The new
+// momentum stays in registers between the absmax and the codes, as in the tile kernel, and
+// every value is read and written once (6 bytes for 8-bit and fp8 codes, against 9 for the
+// deferred-scale passes). A workgroup owns 8 rows x 2048 columns, two rows per wave with
+// every load of both issued first, and writes one norm partial. X0: the stored layout, or
+// for a tall matrix its transpose staged through LDS: 16 bytes of each of 2048 X0 rows per
+// workgroup. Workgroup w takes unit (w % 8) (units / 8) + w / 8 (when 8 divides the unit
+// count), so the eight row groups that fill one 128-byte piece of those X0 rows run on one
+// XCD (workgroups are dispatched to the XCDs round robin) in neighbouring slots, and their
+// pieces meet in that XCD's L2.
+constexpr int LPS_ROWS = 8, LPS_COLS = 2048;
+// LDS row pitch of the transpose stage: 32 mod 256 bytes, so the four rows a 16-lane
+// transposing read covers fall in distinct banks. The fp8 kernel (no code tables in LDS)
+// takes a longer pitch, 43 KB in all, so that at most three of its workgroups share a CU
+// as with the map formats: with four, the partly written X0 lines of the concurrent row
+// groups outgrow the XCD's L2 and are written back in pieces (a Llama step's fp8 pre-pass
+// took 9.3 ms at four per CU, 8.6 at three, like the 8-bit one).
+template <int QF>
+constexpr int lps_pitch() {
+  return QF == MUON_Q_FP8 ? LPS_COLS + 656 : LPS_COLS + 16;
+}
+
+template <int GDT, int QF, bool TALL>
+__global__ __launch_bounds__(256) void lp_prepass_seg_kernel(LpTileArgs a) {
+#pragma clang fp contract(off)
+  constexpr bool MAP = QF != MUON_Q_FP8;
+  __shared__ float q[256];
+  __shared__ __align__(16) uint8_t qtab[MAP ? MUON_QTAB_SIZE : 16];
+  __shared__ __align__(16) uint32_t qthr[MAP ? 256 + MUON_QTHR_PAD : 4];
+  __shared__ __align__(16) bf16_t tileT[TALL ? LPS_ROWS : 1][TALL ? lps_pitch<QF>() : 8];
+  __shared__ float wsum[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int mat = blockIdx.y;
+  float* part = a.partials + (int64_t)mat * a.parts;
+  const int units = a.tiles_used;  // row groups x column strips, = gridDim.x
+  if (tid == 0) {
+    // the partial slots past the units hold nothing
+    for (int64_t sl = units + (int64_t)blockIdx.x; sl < a.parts; sl += units) part[sl] = 0.0f;
+  }
+  const int w = blockIdx.x;
+  const int u = (units & 7) == 0 ? (w & 7) * (units >> 3) + (w >> 3) : w;
+  const int rgroups = units / a.tiles_c;
+  const int rg = u % rgroups, cs = u / rgroups;
+  const int t = (int)(mat / a.nb);
+  const int64_t mb = mat % a.nb;
+  const int64_t r0 = (int64_t)rg * LPS_ROWS, c0 = (int64_t)cs * LPS_COLS;
+  const void* gp = a.grads[t];
+  uint8_t* codes = (uint8_t*)a.codes[t];
+  float* scales = a.scales[t];
+  const float mom = a.momentum;
+
+  // table loads first, then every data load of both rows, nothing consumed in between
+  uint4 tq0 = {}, tq1 = {}, tq2 = {}, tq3 = {};
+  float tqm = 0.0f;
+  uint32_t tt0 = 0, tt1 = 0;
+  bool sparse_map = false;
+  if (MAP) {
+    const uint4* gt = (const uint4*)a.qtab + tid;
+    const uint32_t* gthr = (const uint32_t*)(a.qtab + MUON_QTAB_SIZE);
+    tqm = a.qmap[tid < (QF == MUON_Q_8BIT ? 256 : 16) ? tid : 0];
+    tq0 = gt[0];
+    tq1 = gt[256];
+    tq2 = gt[512];
+    tq3 = gt[768];
+    tt0 = gthr[tid];
+    tt1 = gthr[256 + (tid & (MUON_QTHR_PAD - 1))];
+    sparse_map = gthr[MUON_QTHR_FLAG] == 0u;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  Raw8<GDT> graw[2][4];
+  typename LpCodes<QF>::T cw[2][4];
+  float osc[2][4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t r = r0 + 2 * wave + h;
+    const int64_t rr = r < a.rows ? r : a.rows - 1;  // rows past the end: not used
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int64_t e = (mb * a.rows + rr) * a.cols + c0 + k * 512 + lane * 8;
+      graw[h][k].load(gp, e);
+      cw[h][k] = LpCodes<QF>::load(codes, e);
+      osc[h][k] = scales[e >> a.block_shift];
+    }
+  }
+  if (MAP) {
+    q[tid] = tqm;
+    ((uint4*)qtab)[tid] = tq0;
+    ((uint4*)qtab)[256 + tid] = tq1;
+    ((uint4*)qtab)[512 + tid] = tq2;
+    ((uint4*)qtab)[768 + tid] = tq3;
+    qthr[tid] = tt0;
+    if (tid < MUON_QTHR_PAD) qthr[256 + tid] = tt1;
+    lds_sync();
+  }
+
+  bf16_t* x0 = (bf16_t*)a.x0 + (int64_t)mat * a.x_mstride;
+  const float gs = a.maximize ? -1.0f : 1.0f;  // g * gs is exact: the fma rounds once
+  float ss = 0.0f;
+  // max over the wavefront: within each 32-lane half, then the two halves
+  auto wmax = [&](uint32_t v) -> uint32_t {
+    v = group_max_u32(v, 32);
+    return max((uint32_t)__builtin_amdgcn_readlane((int)v, 0),
+               (uint32_t)__builtin_amdgcn_readlane((int)v, 32));
+  };
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int rl = 2 * wave + h;
+    const int64_t r = r0 + rl;
+    uint4 xw[4] = {};
+    if (r < a.rows) {
+      float m[4][8];
+      uint32_t ab[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float g[8];
+        graw[h][k].unpack(g);
+        ab[k] = 0;
+        lp_momentum8<QF>(g, cw[h][k], osc[h][k], mom, gs, q, m[k], ab[k]);
+      }
+      // the absmax of each block: quarters k of one block share it
+      uint32_t bm[4];
+      if (a.block_shift == 11) {
+        bm[0] = bm[1] = bm[2] = bm[3] = wmax(max(max(ab[0], ab[1]), max(ab[2], ab[3])));
+      } else if (a.block_shift == 10) {
+        bm[0] = bm[1] = wmax(max(ab[0], ab[1]));
+        bm[2] = bm[3] = wmax(max(ab[2], ab[3]));
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bm[k] = wmax(ab[k]);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int64_t e = (mb * a.rows + r) * a.cols + c0 + k * 512 + lane * 8;
+        const float sc = block_scale<QF>(bm[k]);
+        int cq[8];
+        uint2 c8 = {0u, 0u};
+        lp_codes8<QF>(m[k], sc, sparse_map, qthr, qtab, cq, c8);
+        if constexpr (QF == MUON_Q_FP8)
+          *(uint2*)(codes + e) = c8;
+        else
+          LpCodes<QF>::store(codes, e, cq);
+        if (lane == 0 && ((k * 512) & ((1 << a.block_shift) - 1)) == 0) scales[e >> a.block_shift] = sc;
+        float g[8];
+        graw[h][k].unpack(g);
+        uint32_t xv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float gq0 = m[k][2 * i], gq1 = m[k][2 * i + 1];
+          if (a.nesterov) {
+            gq0 = __builtin_fmaf(g[2 * i], gs, m[k][2 * i] * mom);
+            gq1 = __builtin_fmaf(g[2 * i + 1], gs, m[k][2 * i + 1] * mom);
+          }
+          const f2x v = {gq0, gq1};
+          xv[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2x));
+          // sum of squares of the two bf16 values (products exact in fp32)
+          ss = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2v, xv[i]),
+                                               __builtin_bit_cast(bf2v, xv[i]), ss, false);
+        }
+        xw[k] = make_uint4(xv[0], xv[1], xv[2], xv[3]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if constexpr (TALL)
+        *(uint4*)&tileT[rl][k * 512 + lane * 8] = xw[k];
+      else
+        *(uint4*)(x0 + r * a.x_pitch + c0 + k * 512 + lane * 8) = xw[k];
+    }
+  }
+  if constexpr (TALL) {
+    lds_sync();
+    // X0 row c0 + j holds stored column j of rows r0 .. r0 + 7: ds_read_b64_tr_b16 over 16
+    // lanes, lane i pointing at 4 elements of row kb + i/4, columns jb + 4 (i % 4) .. +3,
+    // returns column jb + i of rows kb .. kb + 3; two reads give the 8 rows. Round it: lane
+    // group gg of wave wv takes the 16 columns from jb = 16 (16 it + 4 wv + gg).
+    const int gg = lane >> 4, ti = lane & 15;
+#pragma unroll
+    for (int it = 0; it < LPS_COLS / 256; ++it) {
+      const int jb = 16 * (16 * it + 4 * wave + gg);
+      const lp_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) lp_i16x4*)&tileT[ti >> 2][jb + 4 * (ti & 3)]);
+      const lp_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) lp_i16x4*)&tileT[4 + (ti >> 2)][jb + 4 * (ti & 3)]);
+      const uint4 wv = __builtin_bit_cast(uint4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      *(uint4*)(x0 + (c0 + jb + ti) * a.x_pitch + r0) = wv;
+    }
+  }
+  ss = warp_sum(ss);
+  if (lane == 0) wsum[wave] = ss;
+  __syncthreads();
+  if (tid == 0) part[u] = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+}
+
+template <int GDT, int QF>
+void launch_lp_seg_t(bool tall, const LpTileArgs& a, dim3 grid, hipStream_t s) {
+  if (tall)
+    hipLaunchKernelGGL((lp_prepass_seg_kernel<GDT, QF, true>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((lp_prepass_seg_kernel<GDT, QF, false>), grid, dim3(256), 0, s, a);
+}
+
+template <int GDT>
+void launch_lp_seg_q(int qf, bool tall, const LpTileArgs& a, dim3 grid, hipStream_t s) {
+  if (qf == MUON_Q_8BIT) launch_lp_seg_t<GDT, MUON_Q_8BIT>(tall, a, grid, s);
+  else if (qf == MUON_Q_4BIT) launch_lp_seg_t<GDT, MUON_Q_4BIT>(tall, a, grid, s);
+  else launch_lp_seg_t<GDT, MUON_Q_FP8>(tall, a, grid, s);
+}
+
 // ---- deferred scales: blocks of more than 256 values --------------------------------
 // The tile kernel (DEFER) has left each block's absmax (unsigned max of the |m| bit
 // patterns, so a NaN wins); this kernel keeps the old scale for the requant pass and
@@ -958,12 +1170,16 @@ int muon_launch_lp_prepass_tiled(int ntensors, void* const* grads, int gdt, void
   int shift = 0;
   while ((1LL << shift) < block) ++shift;
   // blocks of at most 256 values (a power of two) lie within one tile row: one pass;
-  // larger blocks (multiples of 256, up to the whole tensor) defer their scale to a
-  // reduction over the tiles' absmax partials and a requant pass
+  // blocks of 512, 1024 or 2048 values in rows of a multiple of 2048 lie within one
+  // wavefront's row segment: one pass (lp_prepass_seg_kernel); other multiples of 256, up
+  // to the whole tensor, defer their scale to a reduction over the tiles' absmax partials
+  // and a requant pass
   const int64_t numel = nb * rows * cols;
   const bool fused = (1LL << shift) == block && block >= 8 && block <= LPT_COLS;
-  const bool defer = !fused && block % 256 == 0 && (numel >> 8) < (1LL << 32);
-  if (cols % LPT_COLS || !(fused || defer)) return MUON_ERR_SHAPE;
+  const bool seg = !fused && (block == 512 || block == 1024 || block == 2048) &&
+                   cols % LPS_COLS == 0;
+  const bool defer = !fused && !seg && block % 256 == 0 && (numel >> 8) < (1LL << 32);
+  if (cols % LPT_COLS || !(fused || seg || defer)) return MUON_ERR_SHAPE;
   for (int i = 0; i < ntensors; ++i) {
     if (((uintptr_t)grads[i] & 15) || ((uintptr_t)codes[i] & 7) || ((uintptr_t)scales[i] & 3))
       return MUON_ERR_SHAPE;
@@ -987,8 +1203,8 @@ int muon_launch_lp_prepass_tiled(int ntensors, void* const* grads, int gdt, void
   a.parts = L.parts;
   a.qtab = (const uint8_t*)ws + L.off_qtab;
   const int64_t rows_pad = L.tall ? L.n_pad : L.m_pad;
-  a.tiles_c = (int)(cols / LPT_COLS);
-  a.tiles_used = (int)((rows_pad / LPT_ROWS) * a.tiles_c);
+  a.tiles_c = (int)(cols / (seg ? LPS_COLS : LPT_COLS));
+  a.tiles_used = (int)((rows_pad / (seg ? LPS_ROWS : LPT_ROWS)) * a.tiles_c);
   if (a.tiles_used > L.parts) return MUON_ERR_SHAPE;
   a.momentum = momentum;
   a.nesterov = nesterov;
@@ -1022,6 +1238,17 @@ int muon_launch_lp_prepass_tiled(int ntensors, void* const* grads, int gdt, void
   if (gdt != MUON_DT_F32 && gdt != MUON_DT_BF16 && gdt != MUON_DT_F16) {
     muon_set_error("lp_prepass: unsupported grad dtype %d", gdt);
     return MUON_ERR_DTYPE;
+  }
+  if (seg) {
+    // one workgroup per unit; the units' workgroups zero the partial slots past them
+    dim3 sgrid((unsigned)a.tiles_used, (unsigned)(ntensors * nb));
+    switch (gdt) {
+      case MUON_DT_F32: launch_lp_seg_q<MUON_DT_F32>(qf, L.tall, a, sgrid, s); break;
+      case MUON_DT_BF16: launch_lp_seg_q<MUON_DT_BF16>(qf, L.tall, a, sgrid, s); break;
+      default: launch_lp_seg_q<MUON_DT_F16>(qf, L.tall, a, sgrid, s); break;
+    }
+    MUON_CHECK_LAUNCH("lp_prepass_seg");
+    return MUON_OK;
   }
   dim3 grid((unsigned)L.parts, (unsigned)(ntensors * nb));
   switch (gdt) {

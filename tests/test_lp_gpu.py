@@ -206,7 +206,9 @@ def test_lp_deferred_scale_prepass_outputs_exact(fmt, cls, block, shape, gdtype)
 
 ROWSEG = [("8bit", OptimState8bit), ("4bit", OptimState4bit), ("fp8", OptimStateFp8)]
 ROWSEG_CASES = [(2048, (128, 2048)), (2048, (3000, 2048)), (2048, (192, 4096)), (512, (1024, 512)),
-                (1024, (200, 1024)), (8192, (64, 8192)), (2048, (2, 256, 2048)), (2048, (4096, 6144))]
+                (1024, (200, 1024)), (8192, (64, 8192)), (2048, (2, 256, 2048)), (2048, (4096, 6144)),
+                (512, (256, 2048)), (1024, (2560, 2048)), (512, (2100, 2048)), (2048, (64, 4096)),
+                (1024, (3, 40, 6144))]
 
 
 @pytest.mark.parametrize("fmt,cls", ROWSEG)
@@ -214,23 +216,26 @@ ROWSEG_CASES = [(2048, (128, 2048)), (2048, (3000, 2048)), (2048, (192, 4096)), 
 @pytest.mark.parametrize("gdtype", [torch.float32, torch.bfloat16])
 def test_lp_row_segment_blocks_exact(fmt, cls, block, shape, gdtype):
     """Blocks of 512 to 8192 values whose width divides the column count (the reference's
-    default 2048 on every Llama shape: each block a whole row segment) through the
-    deferred-scale path. Codes, scales, X0 and the norm partials exactly as the oracle, wide
-    and tall (3000 and 4096 rows: partial and whole 64-row tiles), stacked, a 64-row
-    iterate, two steps."""
+    default 2048 on every Llama shape: each block a whole row segment). Blocks of 512-2048
+    in rows of a multiple of 2048 take the one-pass row-segment kernel (wide, and tall
+    through its LDS transpose: 2100, 2560 and 3000 rows, partial row groups included),
+    the others the deferred-scale path. Codes, scales, X0 and the norm partials exactly as
+    the oracle, stacked, 64-row and shorter iterates, two steps."""
     _check_tiled_prepass(fmt, cls, block, shape, gdtype)
 
 
 @pytest.mark.parametrize("fmt,cls,block,shape", [
     ("8bit", OptimState8bit, 2048, (256, 768)), ("4bit", OptimState4bit, 2048, (768, 256)),
     ("fp8", OptimStateFp8, 2048, (256, 768)), ("fp8", OptimStateFp8, "numel", (768, 256)),
-    ("8bit", OptimState8bit, 256, (768, 256))])
+    ("8bit", OptimState8bit, 256, (768, 256)), ("8bit", OptimState8bit, 2048, (256, 2048)),
+    ("4bit", OptimState4bit, 1024, (128, 4096))])
 def test_lp_prepass_bucket_spanning_two_chunks(fmt, cls, block, shape):
     """A foreach bucket of 34 same-shape tensors in one muon_lp_prepass call: more than
     MUON_MAX_TENSORS (32), so the library launches two chunks (32 + 2), each with its own
     per-tensor block-max slots, old-scale slots and requant grid on the deferred-scale path
-    (blocks of 2048 and one per tensor). Every tensor's codes, scales and X0 bit-exact
-    against the oracle over two steps, wide and tall."""
+    (blocks of 2048 and one per tensor), and its own tensor table on the row-segment path
+    (rows of 2048 and 4096). Every tensor's codes, scales and X0 bit-exact against the
+    oracle over two steps, wide and tall."""
     from muonium_amd import _lib
 
     lib = _lib.load()

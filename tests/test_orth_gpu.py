@@ -34,8 +34,8 @@ SHAPES = [(8, 256, 128), (8, 128, 256), (4, 512, 512), (256, 128), (128, 256), (
 # ranges, ragged column counts, tall inputs, a single row)
 SHAPES += [(64, 4096), (3, 48, 1000), (2, 1000, 33), (1, 5000), (2, 64, 70000), (5, 17, 2560)]
 # m off the 256-row tile: A A and B X contract over round_up(m, 128) < m_pad (the MoE expert
-# shape 1408 x 2048 among them)
-SHAPES += [(2, 300, 700), (2, 700, 300), (1, 1408, 2048)]
+# shapes 1408 x 2048 and 2048 x 1408 among them)
+SHAPES += [(2, 300, 700), (2, 700, 300), (1, 1408, 2048), (1, 2048, 1408)]
 STRATS = ["polar_express", "newton_schulz"]
 
 
