@@ -727,7 +727,8 @@ void launch_lp_tile_q(int qf, bool tall, const LpTileArgs& a, dim3 grid, hipStre
 // workgroup. Workgroup w takes unit (w % 8) (units / 8) + w / 8 (when 8 divides the unit
 // count), so the eight row groups that fill one 128-byte piece of those X0 rows run on one
 // XCD (workgroups are dispatched to the XCDs round robin) in neighbouring slots, and their
-// pieces meet in that XCD's L2.
+// pieces meet in that XCD's L2. Wide matrices take this kernel for blocks of 8-256 values
+// as well (block / 8 lanes of one quarter, a shuffle reduction).
 constexpr int LPS_ROWS = 8, LPS_COLS = 2048;
 // LDS row pitch of the transpose stage: 32 mod 256 bytes, so the four rows a 16-lane
 // transposing read covers fall in distinct banks. The fp8 kernel (no code tables in LDS)
@@ -837,9 +838,13 @@ __global__ __launch_bounds__(256) void lp_prepass_seg_kernel(LpTileArgs a) {
         ab[k] = 0;
         lp_momentum8<QF>(g, cw[h][k], osc[h][k], mom, gs, q, m[k], ab[k]);
       }
-      // the absmax of each block: quarters k of one block share it
+      // the absmax of each block: quarters k of one block share it; a block of 8-256
+      // values is block / 8 consecutive lanes of one quarter
       uint32_t bm[4];
-      if (a.block_shift == 11) {
+      if (a.block_shift <= 8) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bm[k] = group_max_u32(ab[k], 1 << (a.block_shift - 3));
+      } else if (a.block_shift == 11) {
         bm[0] = bm[1] = bm[2] = bm[3] = wmax(max(max(ab[0], ab[1]), max(ab[2], ab[3])));
       } else if (a.block_shift == 10) {
         bm[0] = bm[1] = wmax(max(ab[0], ab[1]));
@@ -859,7 +864,8 @@ __global__ __launch_bounds__(256) void lp_prepass_seg_kernel(LpTileArgs a) {
           *(uint2*)(codes + e) = c8;
         else
           LpCodes<QF>::store(codes, e, cq);
-        if (lane == 0 && ((k * 512) & ((1 << a.block_shift) - 1)) == 0) scales[e >> a.block_shift] = sc;
+        // the lane holding a block's first 8 values stores its scale
+        if (((k * 512 + lane * 8) & ((1 << a.block_shift) - 1)) == 0) scales[e >> a.block_shift] = sc;
         float g[8];
         graw[h][k].unpack(g);
         uint32_t xv[4];
@@ -1176,8 +1182,11 @@ int muon_launch_lp_prepass_tiled(int ntensors, void* const* grads, int gdt, void
   // and a requant pass
   const int64_t numel = nb * rows * cols;
   const bool fused = (1LL << shift) == block && block >= 8 && block <= LPT_COLS;
-  const bool seg = !fused && (block == 512 || block == 1024 || block == 2048) &&
-                   cols % LPS_COLS == 0;
+  // wide matrices with rows of a multiple of 2048 take the row-segment kernel for the
+  // one-pass blocks too (each wave store there writes 1 KB of one X0 row: q/o 583 against
+  // 670 us per launch at block 256); tall ones keep the tile kernel's 128-byte X0 pieces
+  const bool seg = cols % LPS_COLS == 0 &&
+                   (fused ? !L.tall : (block == 512 || block == 1024 || block == 2048));
   const bool defer = !fused && !seg && block % 256 == 0 && (numel >> 8) < (1LL << 32);
   if (cols % LPT_COLS || !(fused || seg || defer)) return MUON_ERR_SHAPE;
   for (int i = 0; i < ntensors; ++i) {

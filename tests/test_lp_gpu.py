@@ -140,11 +140,16 @@ TILED = [("8bit", OptimState8bit, 256), ("4bit", OptimState4bit, 128), ("fp8", O
 TILED_SHAPES = [(512, 256), (256, 768), (300, 256), (2, 256, 512), (4, 96, 512)]
 
 
+# wide rows of a multiple of 2048 values: the row-segment kernel serves these blocks too
+TILED_SHAPES += [(128, 2048), (40, 4096), (3, 96, 2048)]
+
+
 @pytest.mark.parametrize("fmt,cls,block", TILED)
 @pytest.mark.parametrize("shape", TILED_SHAPES)
 @pytest.mark.parametrize("gdtype", [torch.float32, torch.bfloat16])
 def test_lp_tiled_prepass_outputs_exact(fmt, cls, block, shape, gdtype):
-    """Shapes whose column count is a multiple of 256 take the one-pass tiled prepass,
+    """Shapes whose column count is a multiple of 256 take the one-pass tiled prepass
+    (wide ones with rows of a multiple of 2048: the row-segment kernel),
     which writes X straight into the iteration's wide buffer X0 (transposed through LDS
     for tall matrices, zero padding included) and the norm partials. Called through
     the C ABI: codes and scales bit-exact against the quantizer oracle, X0 equal to
