@@ -160,15 +160,18 @@ def test_lp_tiled_prepass_outputs_exact(fmt, cls, block, shape, gdtype):
 @pytest.mark.parametrize("fmt,cls,block", [("8bit", OptimState8bit, 256), ("4bit", OptimState4bit, 128),
                                            ("fp8", OptimStateFp8, 256), ("8bit", OptimState8bit, 2048),
                                            ("fp8", OptimStateFp8, 2048)])
-def test_lp_extreme_values_exact(fmt, cls, block):
+@pytest.mark.parametrize("shape", [(256, 512), (64, 2048)])
+def test_lp_extreme_values_exact(fmt, cls, block, shape):
     """Blocks at the edges of fp32 through the tiled pre-pass (one-pass and deferred
     scales): a 1e38 absmax (a scale above 2^125, whose reciprocal is subnormal); values of
     1e-35 and subnormals beside an absmax of 1; a block clipped at 1e-12 holding 1e-31;
     signed zeros and all-zero blocks. Codes and scales bit-exact against the oracle's IEEE
-    quotients, X0 equal to bf16(g'). (The norm partials of values near 1e38 overflow fp32;
-    not checked.)"""
+    quotients, X0 equal to bf16(g'). 512 columns: the tile kernel (and deferred scales at
+    2048); 2048 columns: the row-segment kernel. (The norm partials of values near 1e38
+    overflow fp32; not checked.)"""
+    rows, cols = shape
     gen = torch.Generator().manual_seed(17)
-    g = torch.randn(256, 512, generator=gen)
+    g = torch.randn(rows, cols, generator=gen)
     special = [
         [1e38, -3e37, 1e30, 1.0, 1e-10, -2.5e36],
         [1.0, 1e-35, -2e-38, 3e-39, -1e-40, 1e-45, 0.0, -0.0],
@@ -178,11 +181,11 @@ def test_lp_extreme_values_exact(fmt, cls, block):
     ]
     for r, vals in enumerate(special):
         row = torch.tensor(vals, dtype=torch.float32)
-        reps = -(-512 // len(vals))
-        g[2 * r] = row.repeat(reps)[:512] * (torch.rand(512, generator=gen) < 0.97)
-        g[2 * r + 1] = row.flip(0).repeat(reps)[:512]
+        reps = -(-cols // len(vals))
+        g[2 * r] = row.repeat(reps)[:cols] * (torch.rand(cols, generator=gen) < 0.97)
+        g[2 * r + 1] = row.flip(0).repeat(reps)[:cols]
     g[10, 300:] = 0.0
-    _check_tiled_prepass(fmt, cls, block, (256, 512), torch.float32, g=g, check_partials=False)
+    _check_tiled_prepass(fmt, cls, block, shape, torch.float32, g=g, check_partials=False)
 
 
 # blocks of more than 256 values: the reference's default 2048 (optim_lp.py:49), other
@@ -406,21 +409,25 @@ def _same_scales(got, want):
 @pytest.mark.filterwarnings("ignore:invalid value encountered:RuntimeWarning")
 @pytest.mark.parametrize("fmt,cls,block", TILED[:3])
 @pytest.mark.parametrize("path", ["quantize", "general", "tiled-wide", "tiled-tall",
-                                  "deferred-wide", "deferred-tall"])
+                                  "deferred-wide", "deferred-tall", "rowseg-wide", "rowseg-tall",
+                                  "rowseg-small-blocks"])
 def test_lp_nan_and_inf_blocks_match_oracle(fmt, cls, block, path):
     """A NaN in a block makes the block's scale NaN and codes every value of it as a NaN
     quotient (0 for the maps, 0x7f for fp8), as torch's amax / clamp do in the reference;
     an infinite value makes the scale infinite (its own quotient NaN, the others 0).
     Covered for the standalone quantizer, the general pre-pass (columns not a multiple
     of 256), the tiled pre-pass in both orientations and its deferred-scale form (blocks
-    of 2048), two steps each."""
+    of 2048 across 256-column tiles), and the row-segment kernel (rows of a multiple of
+    2048: blocks of 2048 wide and tall, and the one-pass blocks on a wide matrix), two steps
+    each."""
     from muonium_amd import _lib
 
     shape = {"quantize": (64, 256), "general": (128, 96), "tiled-wide": (256, 768),
              "tiled-tall": (512, 256), "deferred-wide": (256, 768),
-             "deferred-tall": (512, 256)}[path]
-    if path.startswith("deferred"):
-        block = 2048  # a block longer than a tile row: the scale is reduced across tiles
+             "deferred-tall": (512, 256), "rowseg-wide": (64, 4096), "rowseg-tall": (2304, 2048),
+             "rowseg-small-blocks": (64, 2048)}[path]
+    if path.startswith("deferred") or path in ("rowseg-wide", "rowseg-tall"):
+        block = 2048  # a block longer than a tile row
     gen = torch.Generator().manual_seed(9)
     g = torch.randn(shape, generator=gen)
     g[0, 5] = float("nan")
