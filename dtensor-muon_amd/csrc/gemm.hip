@@ -1542,6 +1542,25 @@ MUON_DEVICE void n16_block(f32x4 (&acc)[8], const bf16x8_mfma& cb, const bf16x8_
   else
     asm volatile(N16_BLOCK(M16) : N16_OUT(acc) : N16_IN);
 }
+// The same as the first block of a tile: the MFMAs start from zero (C = 0) and define the
+// accumulators, so no instruction zeroes them between tiles.
+#define M16Z(C, X, B) "v_mfma_f32_16x16x32_bf16 %[" #C "], %[" #X "], %[" #B "], 0\n\t"
+#define M16SZ(C, X, B) "v_mfma_f32_16x16x32_bf16 %[" #C "], %[" #B "], %[" #X "], 0\n\t"
+#define N16_OUTZ(ACC)                                                                     \
+  [c0] "=a"(ACC[0]), [c1] "=a"(ACC[1]), [c2] "=a"(ACC[2]), [c3] "=a"(ACC[3]),               \
+  [c4] "=a"(ACC[4]), [c5] "=a"(ACC[5]), [c6] "=a"(ACC[6]), [c7] "=a"(ACC[7]),               \
+  [nb] "=&v"(nb), [nl] "=&v"(nl), [nh] "=&v"(nh)
+template <int FI, int XO, bool SW = false>
+MUON_DEVICE void n16_block_z(f32x4 (&acc)[8], const bf16x8_mfma& cb, const bf16x8_mfma (&cx)[8],
+                             bf16x8_mfma& nb, i16x4& nl, i16x4& nh, uint32_t ba, uint32_t xa) {
+  if constexpr (SW)
+    asm volatile(N16_BLOCK(M16SZ) : N16_OUTZ(acc) : N16_IN);
+  else
+    asm volatile(N16_BLOCK(M16Z) : N16_OUTZ(acc) : N16_IN);
+}
+#undef M16Z
+#undef M16SZ
+#undef N16_OUTZ
 // The same with two loads of the DMA of a K-tile (slabs 2 FI and 2 FI + 1 of the 16 this
 // wave issues per K-tile: B panel slabs for FI < 4, X panel slabs for FI >= 4), each after an
 // MFMA, with per-lane offsets vo0 and vo1. m0 and the scalar offsets of both loads come in
@@ -1628,11 +1647,24 @@ MUON_DEVICE void n16_join(bf16x8_mfma (&cx)[8], const i16x4 (&lo)[8], const i16x
   }
 }
 
-// One 32-k substep: 8 blocks, then the wait for its 24 reads.
-template <int XO, bool SW = false>
+// One 32-k substep: 8 blocks, then the wait for its 24 reads. The first of a tile (Z)
+// starts the accumulators from zero.
+template <int XO, bool SW = false, bool Z = false>
 MUON_DEVICE void n16_substep(f32x4 (&acc)[8][8], const bf16x8_mfma (&cb)[8], const bf16x8_mfma (&cx)[8],
                              bf16x8_mfma (&nb)[8], i16x4 (&nl)[8], i16x4 (&nh)[8], uint32_t ba,
                              const uint32_t (&xa)[8]) {
+  if constexpr (Z) {
+    n16_block_z<0, XO, SW>(acc[0], cb[0], cx, nb[0], nl[0], nh[0], ba, xa[0]);
+    n16_block_z<1, XO, SW>(acc[1], cb[1], cx, nb[1], nl[1], nh[1], ba, xa[1]);
+    n16_block_z<2, XO, SW>(acc[2], cb[2], cx, nb[2], nl[2], nh[2], ba, xa[2]);
+    n16_block_z<3, XO, SW>(acc[3], cb[3], cx, nb[3], nl[3], nh[3], ba, xa[3]);
+    n16_block_z<4, XO, SW>(acc[4], cb[4], cx, nb[4], nl[4], nh[4], ba, xa[4]);
+    n16_block_z<5, XO, SW>(acc[5], cb[5], cx, nb[5], nl[5], nh[5], ba, xa[5]);
+    n16_block_z<6, XO, SW>(acc[6], cb[6], cx, nb[6], nl[6], nh[6], ba, xa[6]);
+    n16_block_z<7, XO, SW>(acc[7], cb[7], cx, nb[7], nl[7], nh[7], ba, xa[7]);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    return;
+  }
   n16_block<0, XO, SW>(acc[0], cb[0], cx, nb[0], nl[0], nh[0], ba, xa[0]);
   n16_block<1, XO, SW>(acc[1], cb[1], cx, nb[1], nl[1], nh[1], ba, xa[1]);
   n16_block<2, XO, SW>(acc[2], cb[2], cx, nb[2], nl[2], nh[2], ba, xa[2]);
@@ -1831,11 +1863,6 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g, Muon
     const int kd = (int)((arow0 + wm * WM) / V2_BK);
     const int kd0 = ratio != 0.0f && kd < KT ? kd : -1;
 
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
     // one K-tile: substep 0 (reading substep 1's fragments), wait for K-tile kt + 1's DMA,
     // barrier, substep 1 (reading K-tile kt + 1's first fragments) with the DMA of K-tile
     // kt + 2 (this tile's or the next's) into this K-tile's stage. In the two K-tiles whose k
@@ -1845,7 +1872,10 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g, Muon
       constexpr int FB = decltype(beta_fi0)::value;
       const int cs = kt & 1;
       set_xa(cs);
-      n16_substep<16 * NN_XROWB * 2, SW>(acc, b0, x0, b1, xl, xh, baddr(cs, 1), xa);
+      if (kt == 0)
+        n16_substep<16 * NN_XROWB * 2, SW, true>(acc, b0, x0, b1, xl, xh, baddr(cs, 1), xa);
+      else
+        n16_substep<16 * NN_XROWB * 2, SW>(acc, b0, x0, b1, xl, xh, baddr(cs, 1), xa);
       if constexpr (FB >= 0) {
         bf16x8_mfma db[2][2];
         n16_beta_frags(ratio, lane, db);
