@@ -1868,14 +1868,21 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g, Muon
     // kt + 2 (this tile's or the next's) into this K-tile's stage. In the two K-tiles whose k
     // range is the wave's rows (peeled off the loops), each substep also adds ratio * X to
     // the two row blocks its 32 k rows are.
-    auto kstep = [&](int kt, auto beta_fi0) {
+    // first: the tile's K-tile 0, whose first MFMAs start from zero (a compile-time true or
+    // false, or a run-time test)
+    auto kstep = [&](int kt, auto beta_fi0, auto first) {
       constexpr int FB = decltype(beta_fi0)::value;
       const int cs = kt & 1;
       set_xa(cs);
-      if (kt == 0)
-        n16_substep<16 * NN_XROWB * 2, SW, true>(acc, b0, x0, b1, xl, xh, baddr(cs, 1), xa);
-      else
-        n16_substep<16 * NN_XROWB * 2, SW>(acc, b0, x0, b1, xl, xh, baddr(cs, 1), xa);
+      if constexpr (std::is_same_v<decltype(first), bool>) {
+        if (first)
+          n16_substep<16 * NN_XROWB * 2, SW, true>(acc, b0, x0, b1, xl, xh, baddr(cs, 1), xa);
+        else
+          n16_substep<16 * NN_XROWB * 2, SW>(acc, b0, x0, b1, xl, xh, baddr(cs, 1), xa);
+      } else {
+        n16_substep<16 * NN_XROWB * 2, SW, decltype(first)::value>(acc, b0, x0, b1, xl, xh,
+                                                                     baddr(cs, 1), xa);
+      }
       if constexpr (FB >= 0) {
         bf16x8_mfma db[2][2];
         n16_beta_frags(ratio, lane, db);
@@ -1899,19 +1906,49 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn16_kernel(GemmArgs g, Muon
       n16_join(x0, xl, xh);
     };
     using no_beta = std::integral_constant<int, -1>;
-    int kt = 0;
-    if (kd0 >= 0) {
-      // leaving this loop, the compiler may copy accumulators between registers (to the
-      // assignment the peeled K-tiles use) before any asm that follows the loop; it does not
-      // see the MFMAs in the asm, so the last K-tile of the loop ends with their latency
-      for (; kt < kd0; ++kt) {
-        kstep(kt, no_beta{});
-        if (kt + 1 == kd0) mfma_to_valu_wait();
+    using beta_lo = std::integral_constant<int, 0>;
+    using beta_hi = std::integral_constant<int, 4>;
+    const std::true_type first{};
+    const std::false_type later{};
+    // Leaving a loop that the peeled beta K-tiles follow, the compiler may copy accumulators
+    // between registers before any asm that follows the loop; it does not see the MFMAs in
+    // the asm, so the last K-tile of such a loop ends with their latency.
+    if constexpr (APPLY == 0) {
+      // K-tile 0 peeled off every loop, so the loops carry no test for it (B X 1.6% faster on
+      // the Llama set than with the test in the loops)
+      int kt;
+      if (kd0 == 0) {
+        kstep(0, beta_lo{}, first);
+        kstep(1, beta_hi{}, later);
+        kt = 2;
+      } else {
+        kstep(0, no_beta{}, first);
+        kt = 1;
+        if (kd0 > 0) {
+          for (; kt < kd0; ++kt) {
+            kstep(kt, no_beta{}, later);
+            if (kt + 1 == kd0) mfma_to_valu_wait();
+          }
+          kstep(kt++, beta_lo{}, later);
+          kstep(kt++, beta_hi{}, later);
+        }
       }
-      kstep(kt++, std::integral_constant<int, 0>{});
-      kstep(kt++, std::integral_constant<int, 4>{});
+      for (; kt < KT; ++kt) kstep(kt, no_beta{}, later);
+    } else {
+      // the apply kernels test for K-tile 0 in the loops: peeled, their larger epilogue spilled
+      // (their launches took 7% longer on the MoE experts)
+      int kt = 0;
+      if (kd0 >= 0) {
+        for (; kt < kd0; ++kt) {
+          kstep(kt, no_beta{}, kt == 0);
+          if (kt + 1 == kd0) mfma_to_valu_wait();
+        }
+        kstep(kt, beta_lo{}, kt == 0);
+        ++kt;
+        kstep(kt++, beta_hi{}, later);
+      }
+      for (; kt < KT; ++kt) kstep(kt, no_beta{}, kt == 0);
     }
-    for (; kt < KT; ++kt) kstep(kt, no_beta{});
     mfma_to_valu_wait();
 
     // epilogue: accumulator (fi, fj) element q is X'(i, j + q) with i = 128 wm + 16 fi +
