@@ -623,7 +623,7 @@ def main() -> None:
         achieved = (gwork / max(gn, 1)) / (avg_ms * 1e-3) / 1e12
         # the optimizer iterates in bf16 whatever the params' dtype (zeropower casts to
         # bf16, orthogonalize.py:101-102), so fp32 params (plumbing) run this kernel too
-        # two kernels serve this product: gemm_bf16_nn16_kernel for K >= 1024 (its plain
+        # two kernels serve this product: gemm_bf16_nn16_kernel for K >= 768 (its plain
         # instantiation <0, 0>; the <1|2, 1> ones carry the fused apply, timed apart as
         # gemm_bx_apply) and gemm_bf16_nn4_kernel below; the launch brackets time whichever ran
         knames = ["gemm_bf16_nn16_kernel<0, 0>", "gemm_bf16_nn4_kernel"]
@@ -631,7 +631,7 @@ def main() -> None:
         traffic, traffic_src = _measured_traffic(knames, args.config, args.lp)
         roofline = {
             "bound": "mfma",
-            "kernel": "gemm_bf16_nn16_kernel<0, 0> (K >= 1024) / gemm_bf16_nn4_kernel "
+            "kernel": "gemm_bf16_nn16_kernel<0, 0> (K >= 768) / gemm_bf16_nn4_kernel "
                       "(X' = a X + B X)",
             "achieved": round(achieved, 1),
             "peak": peak,

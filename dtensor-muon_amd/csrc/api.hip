@@ -519,9 +519,9 @@ int muon_orth_run_apply(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch,
   if (fuse) {
     const OrthLayout L = muon_orth_layout(ws_dtype, ws_batch, rows, cols);
     const int64_t kq = std::min(L.m_pad, round_up(L.m, 128));
-    // the tiled path from K = 1024; iterates of at most 64 rows when the parameter is wide
+    // the tiled path from K = 768; iterates of at most 64 rows when the parameter is wide
     // (its rows are the iterate's)
-    fuse = L.short_m ? !L.tall : kq >= 1024;
+    fuse = L.short_m ? !L.tall : kq >= 768;
     for (int t = 0; fuse && t < ntensors; ++t) fuse = params[t] && !((uintptr_t)params[t] & 15);
   }
   if (!fuse) {

@@ -1483,7 +1483,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn4_kernel(GemmArgs g) {
 }
 
 // ----------------------------------------------------------------------------------
-// The persistent B X kernel on 16 x 16 x 32 MFMAs, for K of at least 1024.
+// The persistent B X kernel on 16 x 16 x 32 MFMAs, for K of at least 768.
 //
 // Same tiling, waves, LDS layout, tile order and epilogue staging as gemm_bf16_nn4_kernel;
 // the wave's 128 x 128 block is 8 x 8 accumulators of 16 x 16 (AGPRs) and a K-tile is two
@@ -1508,7 +1508,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_nn4_kernel(GemmArgs g) {
 // registers hold X values through the loop, which the double-buffered fragments need), by
 // 32 more MFMAs per substep (n16_beta), so the accumulators never leave their AGPRs; those
 // two K-tiles are peeled off the loop. It takes its own K-loop structure and per-tile work,
-// so below K = 1024 (where that work weighs more) gemm_bf16_nn4_kernel is used instead.
+// so below K = 768 (where that work weighs more) gemm_bf16_nn4_kernel is used instead.
 #define M16(C, X, B) "v_mfma_f32_16x16x32_bf16 %[" #C "], %[" #X "], %[" #B "], %[" #C "]\n\t"
 #define N16_OUT(ACC)                                                                      \
   [c0] "+a"(ACC[0]), [c1] "+a"(ACC[1]), [c2] "+a"(ACC[2]), [c3] "+a"(ACC[3]),               \
@@ -2624,7 +2624,7 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
       }
       // persistent: at most one workgroup per CU walks the tile list
       const int wgs = persistent_wgs(blocks);
-      if (K >= 1024) {
+      if (K >= 768) {
         MuonApply none;
         none.nb = 1;
         hipLaunchKernelGGL(gemm_bf16_nn16_kernel<0>, dim3((unsigned)wgs), dim3(256), N4_SMEM,
@@ -2669,7 +2669,7 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
 }
 
 // The last iteration's X' = a X + B X with the post-pass applied in its epilogue (bf16
-// parameters, K >= 1024: the 16 x 16 x 32 GEMM); extents and operands as muon_launch_gemm's
+// parameters, K >= 768: the 16 x 16 x 32 GEMM); extents and operands as muon_launch_gemm's
 // GEMM mode, X' is not stored. tall: the parameter is the transpose of the iterate (its
 // rows are the columns of X'). Parameter rows of whole 8-element chunks (pcols % 8 == 0) and
 // 16-byte aligned tensors are the caller's to check.
@@ -2677,7 +2677,7 @@ int muon_launch_gemm_apply(int64_t batch, int64_t M, int64_t N, int64_t K, const
                            int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb,
                            int64_t Mv, int64_t Nv, float alpha, float beta, const float* scale,
                            int scale_mode, const MuonApply& ap, int tall, hipStream_t stream) {
-  if (K < 1024 || K % 128 || M % BF_BM || N % BF_BM || alpha == 0.0f || ap.nb <= 0 ||
+  if (K < 768 || K % 128 || M % BF_BM || N % BF_BM || alpha == 0.0f || ap.nb <= 0 ||
       (batch + ap.nb - 1) / ap.nb > MUON_APPLY_MAX || ap.pcols % 8) {
     muon_set_error("gemm_apply: unsupported launch (K %lld, batch %lld)", (long long)K,
                    (long long)batch);

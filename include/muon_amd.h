@@ -116,7 +116,7 @@ int muon_orth_run(void* ws, int ws_dtype, int64_t ws_batch, int64_t batch, int64
 
 /* muon_orth_run followed by muon_postpass of its result (u = NULL, the same arguments),
  * with the post-pass fused into the last iteration's X = a*X + B X where the shapes allow
- * (bf16 workspace and parameters; on the iterate's short side either at least 1024 valid
+ * (bf16 workspace and parameters; on the iterate's short side either at least 768 valid
  * rows after padding to 128, or at most 64 rows with the parameter stored wide;
  * ntensors * nb == batch, parameter rows a multiple of 8 elements in the stored
  * orientation, 16-byte aligned parameters; the last product launches once per 128 tensors):

@@ -8,7 +8,7 @@ the post-pass does from the stored U. Wide matrices, tall ones (whose last produ
 with swapped MFMA operands so its accumulators hold parameter rows), partial edge tiles,
 stacked 3D tensors, iterates of at most 64 rows (the short path's last product, wide
 parameters), and the shapes that fall back to the two calls (fp32 parameters, a short side
-from 65 to below 1024 after padding to 128 rows, fp16 parameters, tall short parameters).
+from 65 to below 768 after padding to 128 rows, fp16 parameters, tall short parameters).
 """
 
 import pytest
@@ -74,6 +74,8 @@ def _case(shape, count, dtype, seed):
     ((48, 5000), 2),       # short, padding rows 48-63 and a partial last column panel
     ((3, 32, 4096), 2),    # short, stacked
     ((64, 1408 * 2048), 1),  # a flattened MoE expert stack
+    ((768, 2304), 2),      # K = 768 (the GPT-2 shapes), wide
+    ((3072, 768), 2),      # K = 768, tall
 ])
 @pytest.mark.parametrize("wd,cautious", [(0.1, True), (0.1, False), (0.0, True)])
 def test_fused_apply_matches_postpass_bit_for_bit(shape, count, wd, cautious):
@@ -94,7 +96,7 @@ def test_fused_apply_matches_postpass_bit_for_bit(shape, count, wd, cautious):
 
 @pytest.mark.parametrize("shape,dtype", [
     ((1024, 2048), torch.float32),   # fp32 parameters: the separate post-pass
-    ((512, 2048), torch.bfloat16),   # short side 512 < 1024: the separate post-pass
+    ((512, 2048), torch.bfloat16),   # short side 512 < 768: the separate post-pass
     ((2048, 1024), torch.float16),
     ((4096, 64), torch.bfloat16),    # tall with at most 64 columns: the separate post-pass
     ((64, 4096), torch.float32),     # short, fp32 parameters
