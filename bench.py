@@ -583,7 +583,7 @@ def main() -> None:
             if k == "prepass" and work > 12.5 * numel * args.steps:
                 # the pre-pass also writes the Nesterov g' back into the gradients (2 B per
                 # bf16 value, the foreach driver's in-place update); without that write it
-                # moves the survey's 12 B per value (g 2 + m 4 in, m 4 + X 2 out)
+                # moves 12 B per value (g 2 + m 4 in, m 4 + X 2 out)
                 gbs12 = 12.0 * numel * args.steps / (ms * 1e-3) / 1e9
                 entry.update(gbs_12B=round(gbs12, 1), frac_12B=round(gbs12 / PEAK_HBM_GBS, 4))
         kernels[k] = entry
@@ -644,12 +644,12 @@ def main() -> None:
         }
     upd_ms = sum(kern[k][0] for k in ("prepass", "postpass", "lp_prepass")) / args.steps
     upd_bytes = sum(kern[k][2] for k in ("prepass", "postpass", "lp_prepass")) / args.steps
-    # the survey's convention for the fp32-momentum passes: 18 B per bf16 value
-    # (pre 12 + post 6), without the pre-pass's write-back of g' into the gradients
+    # the passes' bytes without the pre-pass's write-back of g' into the gradients: 18 B
+    # per bf16 value with fp32 momentum (pre 12 + post 6)
     upd_bytes18 = (18.0 * numel if (not args.lp and pdtype == torch.bfloat16 and not apply_fused)
                    else None)
-    # with the apply fused, the update kernels are the pre-pass alone: 12 B per value at the
-    # survey's convention (without the write-back of g' into the gradients)
+    # with the apply fused, the update kernels are the pre-pass alone: 12 B per value
+    # without the write-back of g' into the gradients
     upd_bytes12 = 12.0 * numel if (apply_fused and not args.lp and pdtype == torch.bfloat16) else None
 
     cpu = None

@@ -470,7 +470,7 @@ def test_offloaded_batches_pipeline_matches_device_run(algo, nesterov, maximize,
 
 
 def test_plumbing_config_is_bit_repeatable():
-    """Survey config 1: one fp32 256 x 512 parameter (p ~ N(0,1) seed 1, g ~ N(0,1) seed 0),
+    """The plumbing configuration: one fp32 256 x 512 parameter (p ~ N(0,1) seed 1, g ~ N(0,1) seed 0),
     Newton-Schulz 5, cautious wd 0.1, Nesterov 0.95, foreach=False: two runs of the step from
     the same state give bit-identical parameters and momentum."""
     p0 = torch.randn(256, 512, generator=torch.Generator().manual_seed(1))
