@@ -2220,12 +2220,13 @@ MUON_DEVICE void s16_frag_load(s16_frags& n, uint32_t aa, uint32_t ba) {
 // holds rows 16 fi + 4 g + 2 h and + 1 of the lane's column 16 fj + r. Unless `full`,
 // elements outside the valid extent are cleared to +0: rem_i counts the valid rows from the
 // lane's first row (4 g included), rem_j the valid columns from its column.
-MUON_DEVICE void s16_pack(const f32x4 (&acc)[4][8], float alpha, bool full, int rem_i, int rem_j,
-                          uint32_t (&hv)[4][8][2]) {
+template <int FJ>
+MUON_DEVICE void s16_pack(const f32x4 (&acc)[4][FJ], float alpha, bool full, int rem_i, int rem_j,
+                          uint32_t (&hv)[4][FJ][2]) {
 #pragma unroll
   for (int fi = 0; fi < 4; ++fi)
 #pragma unroll
-    for (int fj = 0; fj < 8; ++fj)
+    for (int fj = 0; fj < FJ; ++fj)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const f2x v = {alpha * acc[fi][fj][2 * h], alpha * acc[fi][fj][2 * h + 1]};
@@ -2235,7 +2236,7 @@ MUON_DEVICE void s16_pack(const f32x4 (&acc)[4][8], float alpha, bool full, int 
 #pragma unroll
   for (int fi = 0; fi < 4; ++fi)
 #pragma unroll
-    for (int fj = 0; fj < 8; ++fj)
+    for (int fj = 0; fj < FJ; ++fj)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int il0 = fi * 16 + 2 * h;
@@ -2454,6 +2455,308 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_s16_kernel(GemmArgs g) {
     kloop(I2{}, std::true_type{});
 }
 
+// ----------------------------------------------------------------------------------
+// The SYRK on 128 x 128 tiles, for launches whose 256-row tiles would leave most CUs idle
+// (12 matrices of 768 rows: 72 workgroups of 256-row tiles, 252 of 128-row ones). Four
+// waves (2 x 2, 64 x 64 each: 4 x 4 accumulators of 16 x 16) and 64 KB of LDS per
+// workgroup, so that two workgroups share a CU (two waves per SIMD, as in
+// gemm_bf16_s16_kernel). The same K-tile pipeline: two 32-k substeps of 16 MFMAs, each
+// reading the next substep's 8 fragments (4 a, 4 b) between its MFMAs, and the DMA of
+// K-tile k + 2 spread over the second substep of K-tile k (two loads per block). Fragments
+// and accumulator layout as gemm_bf16_s16_kernel's.
+constexpr int H_TILEB = 128 * V2_ROWB;  // one 128-row K-panel
+constexpr int H_STAGEB = 2 * H_TILEB;   // a and b panels
+constexpr int H_EP_PITCH = 128 + 8;     // staging row pitch (elements)
+constexpr int H_SMEM = 2 * H_STAGEB;
+static_assert(128 * H_EP_PITCH * 2 <= H_SMEM, "the 128-row staging fits the stages");
+
+#define H16(C, B) "v_mfma_f32_16x16x32_bf16 %[" #C "], %[a], %[" #B "], %[" #C "]\n\t"
+#define H16_OUT                                                                              \
+  [c0] "+v"(acc[0]), [c1] "+v"(acc[1]), [c2] "+v"(acc[2]), [c3] "+v"(acc[3]), [na] "=&v"(na), \
+  [nb] "=&v"(nb)
+#define H16_IN                                                                               \
+  [a] "v"(ca), [b0] "v"(cb[0]), [b1] "v"(cb[1]), [b2] "v"(cb[2]), [b3] "v"(cb[3]), [aa] "v"(aa), \
+  [ba] "v"(ba), [oa] "i"(FI * 16 * V2_ROWB)
+#define H16_RA "ds_read_b128 %[na], %[aa] offset:%[oa]\n\t"
+#define H16_RB "ds_read_b128 %[nb], %[ba] offset:%[oa]\n\t"
+#define H16_M0(N) "s_mov_b32 m0, %[mz" #N "]\n\t"
+#define H16_DL(N) "buffer_load_dwordx4 %[vo" #N "], %[rs" #N "], %[so" #N "] offen lds\n\t"
+#define H16_LD(N) [vo##N] "v"(vo##N), [rs##N] "s"(rs##N), [so##N] "s"(so##N), [mz##N] "s"(mz##N)
+// One block of a 32-k substep: the 4 MFMAs of row block FI with the reads of the next
+// substep's a fragment FI (aa + 2 KB FI) and b fragment FI (ba + 2 KB FI). MODE 0: all of
+// it; 2 (a wave wholly below a diagonal tile's diagonal): nothing.
+template <int FI, int MODE = 0>
+MUON_DEVICE void h16_block(f32x4 (&acc)[4], const bf16x8_mfma& ca, const bf16x8_mfma (&cb)[4],
+                           bf16x8_mfma& na, bf16x8_mfma& nb, uint32_t aa, uint32_t ba) {
+  if constexpr (MODE == 0)
+    asm volatile(H16_RA H16(c0, b0) H16(c1, b1) H16_RB H16(c2, b2) H16(c3, b3)
+                 : H16_OUT
+                 : H16_IN);
+}
+// The same with two loads of a K-tile's DMA, each after an MFMA that follows its M0 write
+// (MODE 2: the loads alone, each one wait state after its M0 write).
+template <int FI, int MODE = 0>
+MUON_DEVICE void h16_block_dma(f32x4 (&acc)[4], const bf16x8_mfma& ca, const bf16x8_mfma (&cb)[4],
+                               bf16x8_mfma& na, bf16x8_mfma& nb, uint32_t aa, uint32_t ba,
+                               int vo0, u32x4 rs0, int so0, uint32_t mz0, int vo1, u32x4 rs1,
+                               int so1, uint32_t mz1) {
+  if constexpr (MODE == 0)
+    asm volatile(H16_M0(0) H16_RA H16(c0, b0) H16_DL(0) H16(c1, b1) H16_M0(1) H16_RB
+                 H16(c2, b2) H16_DL(1) H16(c3, b3)
+                 : H16_OUT
+                 : H16_IN, H16_LD(0), H16_LD(1)
+                 : "m0", "memory");
+  else
+    asm volatile(H16_M0(0) "s_nop 0\n\t" H16_DL(0) H16_M0(1) "s_nop 0\n\t" H16_DL(1)
+                 :
+                 : H16_LD(0), H16_LD(1)
+                 : "m0", "memory");
+}
+#undef H16
+#undef H16_OUT
+#undef H16_IN
+#undef H16_RA
+#undef H16_RB
+#undef H16_M0
+#undef H16_DL
+#undef H16_LD
+
+typedef bf16x8_mfma h16_frags[8];  // a fragments 0-3, b fragments 0-3
+
+template <int MODE = 0>
+MUON_DEVICE void h16_substep(f32x4 (&acc)[4][4], const h16_frags& c, h16_frags& n, uint32_t aa,
+                             uint32_t ba) {
+  const bf16x8_mfma(&cb)[4] = *(const bf16x8_mfma(*)[4]) & c[4];
+  h16_block<0, MODE>(acc[0], c[0], cb, n[0], n[4], aa, ba);
+  h16_block<1, MODE>(acc[1], c[1], cb, n[1], n[5], aa, ba);
+  h16_block<2, MODE>(acc[2], c[2], cb, n[2], n[6], aa, ba);
+  h16_block<3, MODE>(acc[3], c[3], cb, n[3], n[7], aa, ba);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// One substep with the DMA of one K-tile into one stage: this wave's slabs q = 0..3 of the
+// a panel (scalar offsets soa + q sta, M0 ma + 4 KB q) and of the b panel (sob + q stb,
+// mb + 4 KB q), two after each block. DIAG (a diagonal tile): the a panel only.
+template <int MODE = 0, bool DIAG = false>
+MUON_DEVICE void h16_substep_dma(f32x4 (&acc)[4][4], const h16_frags& c, h16_frags& n, uint32_t aa,
+                                 uint32_t ba, int voa, int vob, u32x4 rsa, u32x4 rsb, int soa,
+                                 int sta, int sob, int stb, uint32_t ma, uint32_t mb) {
+  const bf16x8_mfma(&cb)[4] = *(const bf16x8_mfma(*)[4]) & c[4];
+  h16_block_dma<0, MODE>(acc[0], c[0], cb, n[0], n[4], aa, ba, voa, rsa, soa, ma, voa, rsa,
+                         soa + sta, ma + 0x1000);
+  h16_block_dma<1, MODE>(acc[1], c[1], cb, n[1], n[5], aa, ba, voa, rsa, soa + 2 * sta,
+                         ma + 0x2000, voa, rsa, soa + 3 * sta, ma + 0x3000);
+  if constexpr (DIAG) {
+    h16_block<2, MODE>(acc[2], c[2], cb, n[2], n[6], aa, ba);
+    h16_block<3, MODE>(acc[3], c[3], cb, n[3], n[7], aa, ba);
+  } else {
+    h16_block_dma<2, MODE>(acc[2], c[2], cb, n[2], n[6], aa, ba, vob, rsb, sob, mb, vob, rsb,
+                           sob + stb, mb + 0x1000);
+    h16_block_dma<3, MODE>(acc[3], c[3], cb, n[3], n[7], aa, ba, vob, rsb, sob + 2 * stb,
+                           mb + 0x2000, vob, rsb, sob + 3 * stb, mb + 0x3000);
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+MUON_DEVICE void h16_frag_load(h16_frags& n, uint32_t aa, uint32_t ba) {
+#pragma unroll
+  for (int f = 0; f < 4; ++f)
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(n[f]) : "v"(aa), "i"(f * 16 * V2_ROWB));
+#pragma unroll
+  for (int f = 0; f < 4; ++f)
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(n[4 + f]) : "v"(ba), "i"(f * 16 * V2_ROWB));
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+__global__ __launch_bounds__(256, 2) void gemm_bf16_s16h_kernel(GemmArgs g) {
+  constexpr int NW = 4, WM = 64, WN = 64;
+  extern __shared__ __align__(16) uint8_t smem[];
+
+  int bidx, tm, tn;
+  map_tile(g, MODE_SYRK, bidx, tm, tn);
+  const int64_t arow0 = (int64_t)tm * 128, brow0 = (int64_t)tn * 128;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  // A diagonal tile (tm == tn) stores its upper triangle: wave (1, 0) lies wholly below the
+  // diagonal and runs no MFMAs, and since the a and b panels are the same rows only the a
+  // panel is loaded, the b fragments read from it.
+  const bool diag = tm == tn;
+  const bool idle = diag && wm == 1 && wn == 0;
+  const bf16_t* A = (const bf16_t*)g.a + (int64_t)bidx * g.sa;
+  const bf16_t* B = (const bf16_t*)g.b + (int64_t)bidx * g.sb;
+  const int lda_b = (int)(g.lda * 2), ldb_b = (int)(g.ldb * 2);
+  const u32x4 rsa = n4_rsrc(A + arow0 * g.lda, false);
+  const u32x4 rsb = n4_rsrc(B + brow0 * g.ldb, false);
+  const u32x4 rs_none = n4_rsrc(A, true);
+  const __amdgpu_buffer_rsrc_t rsa_p =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(A + arow0 * g.lda), 0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb_p =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(B + brow0 * g.ldb), 0, 0x7fffffff, 0x00020000);
+  // load slab q*NW + wave = panel rows (q*NW + wave)*8 .. +7; lane -> row lane/8, chunk
+  // position lane%8, which holds logical chunk (lane%8) ^ kswz(row)
+  const int r_in = wave * 8 + (lane >> 3);
+  const int lch = (lane & 7) ^ kswz(r_in);
+  const int voa = r_in * lda_b + lch * 16;
+  const int vob = r_in * ldb_b + lch * 16;
+  const int sta = NW * 8 * lda_b, stb = NW * 8 * ldb_b;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  const uint32_t m0w = lds0 + wave * 1024;
+
+  const int fr = lane & 15, fg = lane >> 4;
+  int foff[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) foff[ks] = fr * V2_ROWB + (((ks * 4 + fg) ^ kswz(fr)) << 4);
+  const int abase = wm * WM * V2_ROWB, bbase = (diag ? 0 : H_TILEB) + wn * WN * V2_ROWB;
+
+  float alpha = g.alpha, beta = g.beta;
+  if (g.scale_mode != 0) {
+    const float s = g.scale[bidx];
+    if (g.scale_mode == 1) {
+      alpha *= s;
+      beta *= s;
+    } else {
+      alpha *= s * s;
+    }
+  }
+  const float ratio = beta != 0.0f ? beta / alpha : 0.0f;
+  // K-tile whose k range equals this wave's output rows (WM == BK)
+  const int kdiag = ratio != 0.0f ? (int)((arow0 + wm * WM) / V2_BK) : -1;
+
+  const int KT = (int)(g.K / V2_BK);
+  auto aaddr = [&](int st, int ks) -> uint32_t { return lds0 + st * H_STAGEB + abase + foff[ks]; };
+  auto baddr = [&](int st, int ks) -> uint32_t { return lds0 + st * H_STAGEB + bbase + foff[ks]; };
+  auto issue = [&](int kt, int st) {
+    uint8_t* sa = smem + st * H_STAGEB;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa_p, (lds_ptr_t)(sa + (q * NW + wave) * 1024), 16,
+                                               voa, q * sta + kt * V2_ROWB, 0, 0);
+      if (!diag)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rsb_p, (lds_ptr_t)(sa + H_TILEB + (q * NW + wave) * 1024), 16, vob,
+            q * stb + kt * V2_ROWB, 0, 0);
+    }
+  };
+  issue(0, 0);
+  wait_vmcnt0();
+  lds_barrier();
+  if (KT > 1) issue(1, 1);
+  auto kloop = [&](auto mode_c, auto diag_c) {
+    constexpr int MODE = decltype(mode_c)::value;
+    constexpr bool DIAG = decltype(diag_c)::value;
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    h16_frags f0, f1;
+    if (MODE != 2) h16_frag_load(f0, aaddr(0, 0), baddr(0, 0));
+    for (int kt = 0; kt < KT; ++kt) {
+      const int cs = kt & 1;
+      h16_substep<MODE>(acc, f0, f1, aaddr(cs, 1), baddr(cs, 1));
+      if (MODE != 2 && kt == kdiag) {
+        // cin(i, j) = b(j, i): row j of the b panel, k offset i - kt*BK
+        mfma_to_valu_wait();
+        const uint32_t sb = lds0 + cs * H_STAGEB + bbase + fr * V2_ROWB + (fg & 1) * 8;
+#pragma unroll
+        for (int fi = 0; fi < 4; ++fi)
+#pragma unroll
+          for (int fj = 0; fj < 4; ++fj) {
+            const u32x2 w = *(const u32x2 __attribute__((address_space(3)))*)(
+                sb + fj * 16 * V2_ROWB + (((2 * fi + (fg >> 1)) ^ kswz(fr)) << 4));
+            acc[fi][fj][0] += ratio * __uint_as_float(w.x << 16);
+            acc[fi][fj][1] += ratio * __uint_as_float(w.x & 0xffff0000u);
+            acc[fi][fj][2] += ratio * __uint_as_float(w.y << 16);
+            acc[fi][fj][3] += ratio * __uint_as_float(w.y & 0xffff0000u);
+          }
+        valu_to_mfma_wait();
+      }
+      wait_vmcnt0();
+      lds_barrier();
+      // K-tile kt + 2 into this K-tile's stage; past the last K-tile the null descriptor
+      // reads no memory
+      const bool more = kt + 2 < KT;
+      const int kb = (kt + 2) * V2_ROWB;
+      const uint32_t ma = m0w + cs * H_STAGEB;
+      h16_substep_dma<MODE, DIAG>(acc, f1, f0, aaddr(cs ^ 1, 0), baddr(cs ^ 1, 0), voa, vob,
+                                  more ? rsa : rs_none, more ? rsb : rs_none, kb, sta, kb, stb,
+                                  ma, ma + H_TILEB);
+    }
+    mfma_to_valu_wait();
+    wait_vmcnt0();
+
+    // ---- epilogue: stage through LDS, store 16-byte row chunks ----
+    if (g.out == nullptr) return;
+    bf16_t* T = (bf16_t*)smem;
+    const int row0w = wm * WM, col0w = wn * WN;  // wave origin within the tile
+    uint32_t hv[4][4][2];
+    s16_pack<4>(acc, alpha, arow0 + 128 <= g.Mv && brow0 + 128 <= g.Nv,
+                clamp_rem(g.Mv - (arow0 + row0w + fg * 4)),
+                clamp_rem(g.Nv - (brow0 + col0w + fr)), hv);
+    bf16_t* out = (bf16_t*)g.out + (int64_t)bidx * g.so;
+    if (!diag) {
+      // mirror half of the symmetric output: T[j][i], 4 consecutive i per lane
+      lds_barrier();
+#pragma unroll
+      for (int fi = 0; fi < 4; ++fi)
+#pragma unroll
+        for (int fj = 0; fj < 4; ++fj) {
+          const int jl = col0w + fj * 16 + fr;
+          const int il = row0w + fi * 16 + fg * 4;
+          *(uint2*)(T + jl * H_EP_PITCH + il) = make_uint2(hv[fi][fj][0], hv[fi][fj][1]);
+        }
+      lds_barrier();
+#pragma unroll 4
+      for (int it = 0; it < 8; ++it) {
+        const int id = it * 256 + tid;
+        const int jl = id >> 4, c = (id & 15) * 8;
+        const uint4 w = *(const uint4*)(T + jl * H_EP_PITCH + c);
+        *(uint4*)(out + (brow0 + jl) * g.ldo + arow0 + c) = w;
+      }
+    }
+    // row-major stage: T[i][j]
+    lds_barrier();
+#pragma unroll
+    for (int fi = 0; fi < 4; ++fi)
+#pragma unroll
+      for (int fj = 0; fj < 4; ++fj)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int il = row0w + fi * 16 + fg * 4 + q;
+          const int jl = col0w + fj * 16 + fr;
+          T[il * H_EP_PITCH + jl] = (bf16_t)(hv[fi][fj][q >> 1] >> (16 * (q & 1)));
+        }
+    lds_barrier();
+#pragma unroll 4
+    for (int it = 0; it < 8; ++it) {
+      const int id = it * 256 + tid;
+      const int il = id >> 4, c = (id & 15) * 8;
+      uint4 w;
+      if (!diag || c >= il) {
+        w = *(const uint4*)(T + il * H_EP_PITCH + c);
+      } else {
+        // diagonal tile, chunk reaching below the diagonal: those columns come from the
+        // computed (upper) element of the mirror position
+        uint16_t e[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          e[q] = (c + q < il) ? T[(c + q) * H_EP_PITCH + il] : T[il * H_EP_PITCH + c + q];
+        __builtin_memcpy(&w, e, 16);
+      }
+      *(uint4*)(out + (arow0 + il) * g.ldo + brow0 + c) = w;
+    }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I2 = std::integral_constant<int, 2>;
+  if (!diag)
+    kloop(I0{}, std::false_type{});
+  else if (!idle)
+    kloop(I0{}, std::true_type{});
+  else
+    kloop(I2{}, std::true_type{});
+}
+
 // Wave grid of the register-staged bf16 kernel (gemm_bf16_kernel), which serves the
 // masked gram_ path and SYRKs whose beta term has no alpha to fold into: 4 x 2
 // wavefronts, each 64 x 128, two waves per SIMD.
@@ -2485,6 +2788,9 @@ int reserve_bf16_lds() {
       status = -1;
     if (hipFuncSetAttribute((const void*)gemm_bf16_s16_kernel,
                             hipFuncAttributeMaxDynamicSharedMemorySize, V2_SMEM) != hipSuccess)
+      status = -1;
+    if (hipFuncSetAttribute((const void*)gemm_bf16_s16h_kernel,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, H_SMEM) != hipSuccess)
       status = -1;
     if (hipFuncSetAttribute((const void*)gemm_bf16_nn4_kernel,
                             hipFuncAttributeMaxDynamicSharedMemorySize, N4_SMEM) != hipSuccess)
@@ -2643,6 +2949,14 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
         hipLaunchKernelGGL((gemm_bf16_v2_kernel<MODE_SYRK, true>),
                            dim3((unsigned)(gp.tiles_per_batch * batch)), dim3(512),
                            v2_smem(true), stream, gp);
+      } else if (2 * blocks <= device_cus()) {
+        // 256-row tiles would leave most CUs idle: 128-row tiles, two workgroups per CU
+        GemmArgs gh = g;
+        gh.tiles_m = (int)(M / 128);
+        gh.tiles_per_batch = gh.tiles_m * (gh.tiles_m + 1) / 2;
+        gh.tiles_total = gh.tiles_per_batch * (int)batch;
+        hipLaunchKernelGGL(gemm_bf16_s16h_kernel, dim3((unsigned)gh.tiles_total), dim3(256),
+                           H_SMEM, stream, gh);
       } else {
         // full tiles only: the 16 x 16 x 32 MFMA kernel
         hipLaunchKernelGGL(gemm_bf16_s16_kernel, grid, dim3(512), V2_SMEM, stream, g);
