@@ -175,7 +175,11 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 
 def stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The current stream of ``device`` as the raw handle the C ABI takes (the same value as
+    ``torch.cuda.current_stream(device).cuda_stream``, without building a Stream object:
+    a step makes a few calls per bucket and the host time adds up for small buckets)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
 
 
 def ptr_array(tensors: Sequence[torch.Tensor | None]):

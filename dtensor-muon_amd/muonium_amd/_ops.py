@@ -51,7 +51,7 @@ def workspace(device: torch.device, dtype: torch.dtype, batch: int, rows: int, c
     of ``device`` only. Contents need no initialization (every launch rewrites what
     it reads later)."""
     m, n = _padded_extents(dtype, rows, cols)
-    key = (device, torch.cuda.current_stream(device).cuda_stream, dtype, m, n)
+    key = (device, _lib.stream(device), dtype, m, n)
     with _ws_lock:
         hit = _ws_cache.get(key)
         if hit is not None and hit[0] >= batch:
