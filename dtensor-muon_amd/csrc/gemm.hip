@@ -2456,8 +2456,9 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_s16_kernel(GemmArgs g) {
 }
 
 // ----------------------------------------------------------------------------------
-// The SYRK on 128 x 128 tiles, for launches whose 256-row tiles would leave most CUs idle
-// (12 matrices of 768 rows: 72 workgroups of 256-row tiles, 252 of 128-row ones). Four
+// The SYRK on 128 x 128 tiles, for launches of at most two rounds of 256-row tiles, which
+// leave CUs idle (12 matrices of 768 rows: 72 workgroups of 256-row tiles, 252 of 128-row
+// ones; 32 of 1024 rows: 320 = 256 + 64, against 1152 in two workgroups per CU). Four
 // waves (2 x 2, 64 x 64 each: 4 x 4 accumulators of 16 x 16) and 64 KB of LDS per
 // workgroup, so that two workgroups share a CU (two waves per SIMD, as in
 // gemm_bf16_s16_kernel). The same K-tile pipeline: two 32-k substeps of 16 MFMAs, each
@@ -2949,8 +2950,9 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
         hipLaunchKernelGGL((gemm_bf16_v2_kernel<MODE_SYRK, true>),
                            dim3((unsigned)(gp.tiles_per_batch * batch)), dim3(512),
                            v2_smem(true), stream, gp);
-      } else if (2 * blocks <= device_cus()) {
-        // 256-row tiles would leave most CUs idle: 128-row tiles, two workgroups per CU
+      } else if (blocks <= 2 * device_cus()) {
+        // at most two rounds of 256-row tiles, the CUs idle for much of them (72 workgroups,
+        // or 320 in two rounds of 256 and 64): 128-row tiles, two workgroups per CU
         GemmArgs gh = g;
         gh.tiles_m = (int)(M / 128);
         gh.tiles_per_batch = gh.tiles_m * (gh.tiles_m + 1) / 2;
