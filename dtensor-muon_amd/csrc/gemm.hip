@@ -2829,6 +2829,21 @@ int device_cus() {
 // CU needs, with the tiles spread evenly over them (a launch of a few hundred tiles leaves
 // the CUs it does not need to kernels on other streams instead of idling them in its last
 // round). Unchanged when the tile count is a multiple of the CU count.
+// Whether a full-tile SYRK launch of `blocks` 256-row tiles (tiles_m per side, `batch`
+// matrices) takes gemm_bf16_s16h_kernel's 128-row tiles instead: when it has at most two
+// rounds of 256-row tiles (one workgroup per CU) and the 128-row tiles, two workgroups per
+// CU with a quarter of the work each, need fewer rounds, counting a 128-row round as half
+// a 256-row one at 85% of its efficiency (72 workgroups of 12 matrices of 768 rows: one
+// round against one half-round; 320 of 32 matrices of 1024 rows: two rounds against three
+// half-rounds; 200 would be one round against two half-rounds, and stays).
+static bool use_h128(int tiles_m, int64_t batch, int64_t blocks) {
+  const int64_t cus = device_cus();
+  const int64_t th = 2 * (int64_t)tiles_m;
+  const int64_t bh = th * (th + 1) / 2 * batch;
+  const int64_t rounds = (blocks + cus - 1) / cus, rounds_h = (bh + 2 * cus - 1) / (2 * cus);
+  return blocks <= 2 * cus && 20 * rounds_h <= 34 * rounds;
+}
+
 static int persistent_wgs(int64_t blocks) {
   const int64_t cus = device_cus();
   if (blocks <= cus) return (int)blocks;
@@ -2950,11 +2965,11 @@ int muon_launch_gemm(int dtype, int mode, bool masked, int64_t batch, int64_t M,
         hipLaunchKernelGGL((gemm_bf16_v2_kernel<MODE_SYRK, true>),
                            dim3((unsigned)(gp.tiles_per_batch * batch)), dim3(512),
                            v2_smem(true), stream, gp);
-      } else if (blocks <= 2 * device_cus()) {
+      } else if (use_h128(g.tiles_m, batch, blocks)) {
         // at most two rounds of 256-row tiles, the CUs idle for much of them (72 workgroups,
         // or 320 in two rounds of 256 and 64): 128-row tiles, two workgroups per CU
         GemmArgs gh = g;
-        gh.tiles_m = (int)(M / 128);
+        gh.tiles_m = 2 * g.tiles_m;
         gh.tiles_per_batch = gh.tiles_m * (gh.tiles_m + 1) / 2;
         gh.tiles_total = gh.tiles_per_batch * (int)batch;
         hipLaunchKernelGGL(gemm_bf16_s16h_kernel, dim3((unsigned)gh.tiles_total), dim3(256),
